@@ -1,0 +1,163 @@
+/*
+ * sdq — MI355X (gfx950) int8 qGEMM, C ABI.
+ *
+ * Drop-in device implementation of the reference's int8 Linear path
+ * (JasonHonKL/Self-evolve-diffusion-cpp):
+ *
+ *   sd::qgemm(const Tensor& A, const Tensor& Bq, const Tensor& bs, Tensor& out)
+ *       src/core/tensor.h:48-52, src/core/qgemm.cpp:73-142
+ *   mlin(x, Linear, y)  — qgemm + bias pass, src/model/ovi_dit.cpp:66-84
+ *   and the consumers that follow mlin in the DiT blocks:
+ *       gelu_tanh_inplace  src/model/ovi_dit.cpp:132-142 (after ffn fc1, 217-218)
+ *       gated_add_inplace  src/model/ovi_dit.cpp:152-159 (after ffn fc2 / self o, 187, 221)
+ *       add_inplace        src/model/ovi_dit.cpp:144-149 (after cross o, 251)
+ *   .sdcpp v1 packed weights: src/serde/sdcpp.cpp:1-133 (int8 [N,K] row-major,
+ *       then N f32 scales, no alignment padding).
+ *
+ * Semantics (bit-exact with the reference CPU path):
+ *   per row i of A:   mx = max_k |A[i,k]|, sc = mx/127 (1 if 0), inv = 1/sc,
+ *                     aq[i,k] = clamp(cvt_rne(A[i,k]*inv), -127, 127)
+ *                     (NaN / out-of-int32 products give -127, as x86 cvtss2si)
+ *   acc[i,j] = sum_k aq[i,k] * Bq[j,k]             (exact int32)
+ *   y[i,j]   = fl( fl((float)acc) * fl(sc_i * bs[j]) )
+ *   bias:      y = fl(y + bias[j])
+ *   epilogue:  GELU  y = gelu_tanh(y)               (tolerance, libm tanh)
+ *              GATED x[i,j] = fma(y, gate[j], x[i,j]) (or x + fl(y*gate))
+ *              RESID x[i,j] = fl(x[i,j] + y)
+ *
+ * Conventions: every function returns SDQ_OK (0) or a positive SDQ_ERR_*
+ * code and never throws; sdq_last_error() gives the calling thread's last
+ * message. Device pointers are plain HIP device addresses; `stream` is a
+ * hipStream_t passed as void* (NULL = the null stream). Functions named
+ * *_host take host pointers and are synchronous.
+ */
+#ifndef SDQ_H_
+#define SDQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SDQ_OK 0
+#define SDQ_ERR_INVALID 1 /* bad argument or shape */
+#define SDQ_ERR_HIP 2     /* HIP runtime error */
+#define SDQ_ERR_NOMEM 3   /* device allocation failed */
+#define SDQ_ERR_FORMAT 4  /* malformed .sdcpp file */
+#define SDQ_ERR_NODEV 5   /* no usable gfx950 device */
+#define SDQ_ERR_NOTFOUND 6
+
+/* Epilogue kinds (see semantics above). */
+#define SDQ_EPI_NONE 0  /* Y = y (+bias)                                  */
+#define SDQ_EPI_GELU 1  /* Y = gelu_tanh(y (+bias))                       */
+#define SDQ_EPI_GATED 2 /* Y = fma(y (+bias), gate, resid)                */
+#define SDQ_EPI_RESID 3 /* Y = resid + (y (+bias))                        */
+#define SDQ_EPI_ACC 4   /* Y (int32*) = raw accumulators, no rescale      */
+
+typedef struct sdq_weight sdq_weight;
+
+typedef struct sdq_epilogue {
+  int kind;            /* SDQ_EPI_*                                             */
+  int gate_fma;        /* GATED: 1 = fma(y,g,x) (reference -march=native build), */
+                       /*        0 = x + fl(y*g)                                 */
+  const float* bias;   /* [N] or NULL                                           */
+  const float* gate;   /* [N] (GATED)                                           */
+  const float* resid;  /* [M,N] residual input (GATED/RESID); may equal Y       */
+} sdq_epilogue;
+
+typedef struct sdq_device_info {
+  int device;
+  int cu_count;
+  int max_clock_khz;     /* shader clock as reported by the runtime */
+  int mem_clock_khz;
+  int64_t total_mem;
+  char arch[64];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} sdq_device_info;
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* sdq_last_error(void);
+
+/* Library version string. */
+const char* sdq_version(void);
+
+/* Select `device` for this thread and check it is gfx950. Idempotent.
+ * Replaces: nothing (the reference is CPU-only; tensor.cpp:81-83 sizes its
+ * thread pool instead). */
+int sdq_init(int device);
+int sdq_device_info_get(sdq_device_info* out);
+
+/* ---- weights (one-time upload + repack) --------------------------------
+ * Upload an int8 [N,K] row-major weight and its N f32 per-row scales from
+ * HOST memory (e.g. views into an mmapped .sdcpp file; `scale` may be
+ * unaligned, as .sdcpp v1 has no padding) and repack it on the GPU into the
+ * MFMA fragment layout. The handle owns the device copy.
+ * Replaces: the I8 + ".scale" views of load_sdcpp (src/serde/sdcpp.cpp:107-131)
+ * consumed by OviDit::load_impl's lin() (src/model/ovi_dit.cpp:397-415). */
+int sdq_weight_upload(const int8_t* q, const float* scale, int64_t N, int64_t K, void* stream,
+                      sdq_weight** out);
+/* Same from DEVICE memory (q and scale already resident in HBM). */
+int sdq_weight_upload_device(const int8_t* q_dev, const float* scale_dev, int64_t N, int64_t K,
+                             void* stream, sdq_weight** out);
+int sdq_weight_free(sdq_weight* w);
+int sdq_weight_dims(const sdq_weight* w, int64_t* N, int64_t* K);
+/* Unpack the device copy back to row-major int8 [N,K] + f32 [N] in host
+ * memory (repack round-trip check). */
+int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale);
+
+/* ---- the qGEMM ---------------------------------------------------------
+ * Y[M,N] = epilogue(qgemm(A[M,K], W)), A and Y device pointers (row-major,
+ * contiguous). K must equal the weight's K. M == 0 is a no-op; K == 0 gives
+ * y = 0 (then bias/epilogue), matching the zero-filled Tensor the reference
+ * returns (src/core/qgemm.cpp:74-76). Stream-ordered; no host sync.
+ * Replaces: sd::qgemm (src/core/tensor.h:52) + mlin's bias pass
+ * (src/model/ovi_dit.cpp:66-84) + the consumer named by epi->kind. */
+int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
+                void* Y, void* stream);
+
+/* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
+int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
+
+/* Host-pointer synchronous variant of sdq_qlinear: copies A (and bias /
+ * gate / resid) in, runs, copies Y out. Replaces sd::qgemm's host-tensor
+ * contract (tensor.h:52) for callers that hold CPU tensors. */
+int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
+                     const sdq_epilogue* epi, void* Y);
+
+/* ---- activation quantizer (exposed for parity checks and for callers
+ * that quantize once and reuse) ------------------------------------------
+ * Row-major output: aq [M,K] int8, as [M] f32 (src/core/qgemm.cpp:82-96). */
+int sdq_act_quant(const float* A, int64_t M, int64_t K, int8_t* aq, float* as, void* stream);
+
+/* ---- device memory, for host code that reaches HIP only through this ABI */
+#define SDQ_H2D 0
+#define SDQ_D2H 1
+#define SDQ_D2D 2
+int sdq_device_alloc(size_t bytes, void** out);
+int sdq_device_free(void* p);
+/* Stream-ordered copy; `kind` is SDQ_H2D / SDQ_D2H / SDQ_D2D. */
+int sdq_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int sdq_stream_sync(void* stream);
+
+/* ---- per-kernel timing -------------------------------------------------
+ * Between sdq_profile_begin() and sdq_profile_end(), every kernel this
+ * thread launches through sdq is bracketed by HIP events recorded on its
+ * launch stream. sdq_profile_end() waits for them and returns one record per
+ * kernel name (launch count, summed device milliseconds). */
+typedef struct sdq_kernel_time {
+  char name[48];
+  int launches;
+  double total_ms;
+} sdq_kernel_time;
+int sdq_profile_begin(void);
+int sdq_profile_end(sdq_kernel_time* out, int max_records, int* n_records);
+
+/* Synchronize the current device (convenience for ctypes callers). */
+int sdq_sync(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDQ_H_ */

@@ -1,0 +1,260 @@
+/*
+ * CPU ORACLE — test infrastructure only.
+ *
+ * A plain-C restatement of the reference's int8 qGEMM path, used by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the CHECKER.
+ * Nothing in the shipped library links, loads or calls this file: the GPU
+ * product path fails loudly when its HIP library is missing instead of
+ * falling back here.
+ *
+ * Every function cites the reference file:line it follows
+ * (reference = JasonHonKL/Self-evolve-diffusion-cpp).
+ *
+ * Parity pins (what checks each function, see tests/test_oracle.py):
+ *   orc_act_quant        - compiled reference sd::qgemm (oracle/_ref) bit-exact,
+ *                          closed-form special cases (zero row, +-amax -> +-127,
+ *                          NaN/Inf/denormal rows), brute-force numpy restatement.
+ *   orc_qgemm_acc        - brute-force int64 numpy matmul (exact integer sum).
+ *   orc_qgemm            - compiled reference sd::qgemm (oracle/_ref) bit-exact on
+ *                          many shapes incl. M>=2048 (widen path) and M<2048;
+ *                          reference golden vectors (cosine > 0.999 vs fp32).
+ *   orc_bias_add         - closed form fl(y+b) vs numpy float32 add.
+ *   orc_gated_add        - closed form fma(y,g,x): checked against float64
+ *                          y*g+x rounded once (exact for fp32 inputs).
+ *   orc_add              - numpy float32 add.
+ *   orc_gelu_tanh        - float64 closed form within tolerance only.
+ *   orc_quantize_rowwise - compiled reference sd::quantize_rowwise bit-exact,
+ *                          reference golden replica (lround) bit-exact.
+ *   orc_quant_rows       - closed form of the packer's numpy expression
+ *                          (float32 semantics) evaluated by numpy itself.
+ *   orc_randu            - compiled reference sd::randu bit-exact.
+ *   orc_randn            - closed-form splitmix64 + Box-Muller in numpy float64.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; no -ffast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <pthread.h>
+
+/* x86 cvtss2si under the default MXCSR (round-to-nearest-even): NaN and any
+ * value whose rounded result does not fit int32 give INT32_MIN (the "integer
+ * indefinite" value). The reference's round_to_i8 (src/core/qgemm.cpp:62-69)
+ * uses _mm_cvtss_si32 on AVX2 builds (Makefile:4 builds with -march=native). */
+static int32_t cvt_rne_i32(float y) {
+  if (isnan(y)) return INT32_MIN;
+  float r = rintf(y); /* FE_TONEAREST: ties to even */
+  if (!(r >= -2147483648.0f && r < 2147483648.0f)) return INT32_MIN;
+  return (int32_t)r;
+}
+
+/* src/core/qgemm.cpp:62-69 round_to_i8: clamp(cvtss2si(x), -127, 127). */
+int orc_round_to_i8(float x) {
+  int32_t v = cvt_rne_i32(x);
+  if (v < -127) v = -127;
+  if (v > 127) v = 127;
+  return (int)v;
+}
+
+/* src/core/qgemm.cpp:84-96: per-row dynamic activation quantization.
+ *   mx  = max_k |r_k|        (std::max(mx, fabs(r)) keeps mx when r is NaN)
+ *   sc  = mx / 127.f ; sc == 0 -> 1
+ *   inv = 1.f / sc
+ *   q_k = round_to_i8(r_k * inv)
+ * aq is row-major [M,K], as is [M]. */
+void orc_act_quant(const float* A, int64_t M, int64_t K, int8_t* aq, float* as) {
+  for (int64_t i = 0; i < M; i++) {
+    const float* r = A + i * K;
+    float mx = 0.f;
+    for (int64_t k = 0; k < K; k++) {
+      float a = fabsf(r[k]);
+      mx = (mx < a) ? a : mx; /* std::max(mx, a) */
+    }
+    float sc = mx / 127.f;
+    if (sc == 0.f) sc = 1.f;
+    as[i] = sc;
+    const float inv = 1.f / sc;
+    for (int64_t k = 0; k < K; k++) aq[i * K + k] = (int8_t)orc_round_to_i8(r[k] * inv);
+  }
+}
+
+/* src/core/qgemm.cpp:22-59, 107-138: acc[i,j] = sum_k aq[i,k]*bq[j,k] in
+ * int32 (exact for K <= 133k; the widened s16 and the narrow s8 paths give the
+ * same integer). */
+typedef struct {
+  const int8_t* aq; const int8_t* bq; int32_t* acc;
+  int64_t M, N, K, j0, j1;
+} acc_job;
+
+static void* acc_worker(void* p) {
+  acc_job* jb = (acc_job*)p;
+  const int64_t K = jb->K, N = jb->N;
+  for (int64_t i = 0; i < jb->M; i++) {
+    const int8_t* a = jb->aq + i * K;
+    for (int64_t j = jb->j0; j < jb->j1; j++) {
+      const int8_t* b = jb->bq + j * K;
+      int32_t s = 0;
+      for (int64_t k = 0; k < K; k++) s += (int32_t)a[k] * (int32_t)b[k];
+      jb->acc[i * N + j] = s;
+    }
+  }
+  return NULL;
+}
+
+void orc_qgemm_acc(const int8_t* aq, const int8_t* bq, int64_t M, int64_t N, int64_t K,
+                   int32_t* acc, int nthreads) {
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > 64) nthreads = 64;
+  pthread_t th[64];
+  acc_job jobs[64];
+  int64_t per = (N + nthreads - 1) / nthreads;
+  int n = 0;
+  for (int t = 0; t < nthreads; t++) {
+    int64_t j0 = t * per, j1 = j0 + per;
+    if (j1 > N) j1 = N;
+    if (j0 >= j1) break;
+    jobs[n] = (acc_job){aq, bq, acc, M, N, K, j0, j1};
+    n++;
+  }
+  for (int t = 1; t < n; t++) pthread_create(&th[t], NULL, acc_worker, &jobs[t]);
+  if (n > 0) acc_worker(&jobs[0]);
+  for (int t = 1; t < n; t++) pthread_join(th[t], NULL);
+}
+
+/* src/core/qgemm.cpp:123-124, 135: out = (float)acc * (as[i] * bs[j]).
+ * Two roundings in this order, no fused multiply-add. */
+void orc_rescale(const int32_t* acc, const float* as, const float* bs, int64_t M, int64_t N,
+                 float* out) {
+  for (int64_t i = 0; i < M; i++)
+    for (int64_t j = 0; j < N; j++) {
+      float s = as[i] * bs[j];
+      float a = (float)acc[i * N + j];
+      out[i * N + j] = a * s;
+    }
+}
+
+/* src/core/qgemm.cpp:73-142 sd::qgemm: out [M,N] (zero-filled first by the
+ * Tensor constructor, src/core/tensor.cpp:19-24; M,N or K == 0 returns the
+ * zeros, qgemm.cpp:75-76). */
+int orc_qgemm(const float* A, const int8_t* Bq, const float* bs, int64_t M, int64_t K, int64_t N,
+              float* out, int nthreads) {
+  memset(out, 0, (size_t)(M * N) * sizeof(float));
+  if (M == 0 || N == 0 || K == 0) return 0;
+  int8_t* aq = (int8_t*)malloc((size_t)(M * K) + 1);
+  float* as = (float*)malloc((size_t)M * sizeof(float) + 4);
+  int32_t* acc = (int32_t*)malloc((size_t)(M * N) * sizeof(int32_t) + 4);
+  if (!aq || !as || !acc) { free(aq); free(as); free(acc); return -1; }
+  orc_act_quant(A, M, K, aq, as);
+  orc_qgemm_acc(aq, Bq, M, N, K, acc, nthreads);
+  orc_rescale(acc, as, bs, M, N, out);
+  free(aq); free(as); free(acc);
+  return 0;
+}
+
+/* src/model/ovi_dit.cpp:71-79 (mlin bias pass): y[i,j] += b[j]. */
+void orc_bias_add(float* y, const float* b, int64_t M, int64_t N) {
+  for (int64_t i = 0; i < M; i++)
+    for (int64_t j = 0; j < N; j++) y[i * N + j] = y[i * N + j] + b[j];
+}
+
+/* src/model/ovi_dit.cpp:152-159 gated_add_inplace: x += y * gate[c].
+ * The reference Makefile builds with -O3 -march=native and GCC's C++ default
+ * -ffp-contract=fast, which contracts this to one fused multiply-add
+ * (use_fma=1). use_fma=0 restates a build without FMA: x + fl(y*g). */
+void orc_gated_add(float* x, const float* y, const float* g, int64_t M, int64_t N, int use_fma) {
+  for (int64_t i = 0; i < M; i++)
+    for (int64_t j = 0; j < N; j++) {
+      int64_t o = i * N + j;
+      if (use_fma) x[o] = fmaf(y[o], g[j], x[o]);
+      else { float p = y[o] * g[j]; x[o] = x[o] + p; }
+    }
+}
+
+/* src/model/ovi_dit.cpp:144-149 add_inplace: x += y. */
+void orc_add(float* x, const float* y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) x[i] = x[i] + y[i];
+}
+
+/* src/model/ovi_dit.cpp:132-142 gelu_tanh_inplace (nn.GELU(approximate='tanh')).
+ * Uses libm tanhf; not bit-reproducible across libms, so only tolerance
+ * checks use it. */
+void orc_gelu_tanh(float* x, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    float v = x[i];
+    float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    x[i] = 0.5f * v * (1.f + tanhf(u));
+  }
+}
+
+/* src/core/tensor.cpp:63-78 quantize_rowwise: sc = fl(mx/127), sc==0 -> 1,
+ * q = (int8) lround(w / sc)  (half away from zero, no clamp). */
+void orc_quantize_rowwise(const float* W, int64_t N, int64_t K, int8_t* q, float* s) {
+  for (int64_t i = 0; i < N; i++) {
+    float mx = 0.f;
+    for (int64_t k = 0; k < K; k++) {
+      float a = fabsf(W[i * K + k]);
+      mx = (mx < a) ? a : mx;
+    }
+    float sc = mx / 127.f;
+    if (sc == 0.f) sc = 1.f;
+    s[i] = sc;
+    for (int64_t k = 0; k < K; k++) {
+      float v = W[i * K + k] / sc;
+      q[i * K + k] = (int8_t)lroundf(v);
+    }
+  }
+}
+
+/* tools/quantize/pack_sdcpp.py:45-51 quant_rows (numpy float32 semantics):
+ *   amax = max|x| per row; safe = amax>0 ? amax : 1
+ *   q = clip(rint(x * fl32(127/safe)), -127, 127)   (rint: ties to even)
+ *   scale = fl32(amax / 127)                        (0 for an all-zero row) */
+void orc_quant_rows(const float* W, int64_t N, int64_t K, int8_t* q, float* s) {
+  for (int64_t i = 0; i < N; i++) {
+    float amax = 0.f;
+    for (int64_t k = 0; k < K; k++) {
+      float a = fabsf(W[i * K + k]);
+      amax = (amax < a) ? a : amax;
+    }
+    float safe = amax > 0.f ? amax : 1.f;
+    float mul = 127.f / safe;
+    for (int64_t k = 0; k < K; k++) {
+      float v = rintf(W[i * K + k] * mul);
+      if (v < -127.f) v = -127.f;
+      if (v > 127.f) v = 127.f;
+      q[i * K + k] = (int8_t)v;
+    }
+    s[i] = amax / 127.f;
+  }
+}
+
+/* src/core/tensor.cpp:125-132 randu: xorshift64, values in [-1, 1]. */
+void orc_randu(float* x, int64_t n, uint64_t seed) {
+  uint64_t s = seed ? seed : 0x9e3779b97f4a7c15ull;
+  for (int64_t i = 0; i < n; i++) {
+    s ^= s << 13; s ^= s >> 7; s ^= s << 17;
+    x[i] = (float)((int32_t)(s >> 40) % 20001 - 10000) / 10000.f;
+  }
+}
+
+/* src/pipeline/gen.cpp:88-105 randn: splitmix64 + Box-Muller in double. */
+void orc_randn(float* x, int64_t n, uint64_t seed) {
+  uint64_t s = seed + 0x9E3779B97F4A7C15ull;
+  for (int64_t i = 0; i < n; i += 2) {
+    uint64_t z;
+    z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    uint64_t n1 = z ^ (z >> 31);
+    z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    uint64_t n2 = z ^ (z >> 31);
+    const double u1 = ((double)(n1 >> 11) + 1.0) / 9007199254740993.0;
+    const double u2 = (double)(n2 >> 11) / 9007199254740992.0;
+    const double r = sqrt(-2.0 * log(u1));
+    x[i] = (float)(r * cos(6.283185307179586 * u2));
+    if (i + 1 < n) x[i + 1] = (float)(r * sin(6.283185307179586 * u2));
+  }
+}

@@ -1,0 +1,551 @@
+// C ABI of the sdq library (declared in include/sdq.h).
+//
+// Owns: per-device state, weight handles (fragment-layout copies of .sdcpp
+// int8 weights in HBM), and a per-(device, stream) workspace holding the
+// quantized activations of the call in flight. Every entry point reports
+// failures as a status code plus a thread-local message and never throws
+// (the reference's loader throws std::runtime_error, src/serde/sdcpp.cpp:27;
+// its qgemm has no error path at all, src/core/qgemm.cpp:73-142).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <set>
+#include <vector>
+#include <string>
+#include <utility>
+
+#include "sdq_internal.h"
+
+struct sdq_weight {
+  int device;
+  int64_t N, K, Np, KFp;
+  int8_t* frags;  // (Np/16) * KFp * 1024 bytes
+  float* scale;   // Np floats, zero padded
+};
+
+namespace sdq {
+
+namespace {
+
+thread_local std::string t_err;
+
+struct DevState {
+  bool ready = false;
+  int cu_count = 0;
+  hipDeviceProp_t prop{};
+};
+
+constexpr int kMaxDev = 64;
+std::mutex g_mu;
+DevState g_dev[kMaxDev];
+
+struct Workspace {
+  int8_t* at = nullptr;
+  size_t at_bytes = 0;
+  float* as = nullptr;
+  size_t as_bytes = 0;
+};
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---- optional per-kernel event timing (sdq_profile_begin/end) ----
+struct ProfRec {
+  std::string name;
+  hipEvent_t a, b;
+};
+thread_local bool t_prof = false;
+thread_local std::vector<ProfRec> t_recs;
+
+hipEvent_t prof_mark(hipStream_t s) {
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventRecord(e, s) != hipSuccess) {
+    (void)hipEventDestroy(e);
+    return nullptr;
+  }
+  return e;
+}
+
+int current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+  if (*dev < 0 || *dev >= kMaxDev) return set_error(SDQ_ERR_NODEV, "device index out of range");
+  return SDQ_OK;
+}
+
+int ensure_device(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevState& d = g_dev[dev];
+  if (d.ready) return SDQ_OK;
+  hipError_t e = hipGetDeviceProperties(&d.prop, dev);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceProperties");
+  if (std::strncmp(d.prop.gcnArchName, "gfx950", 6) != 0)
+    return set_error(SDQ_ERR_NODEV, std::string("sdq kernels are built for gfx950, device is ") +
+                                        d.prop.gcnArchName);
+  d.cu_count = d.prop.multiProcessorCount;
+  d.ready = true;
+  return SDQ_OK;
+}
+
+// Grows (never shrinks) the workspace of (dev, stream). A buffer that is
+// replaced may still be read by work queued on `stream`, so the stream is
+// drained before the old buffer is freed.
+int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, Workspace** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, s}];
+  if (w.at_bytes < at_bytes || w.as_bytes < as_bytes) {
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+    if (w.at_bytes < at_bytes) {
+      if (w.at) (void)hipFree(w.at);
+      w.at = nullptr;
+      w.at_bytes = 0;
+      e = hipMalloc(&w.at, at_bytes);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(SDQ_ERR_NOMEM, "workspace allocation of " + std::to_string(at_bytes) +
+                                            " bytes failed");
+      }
+      w.at_bytes = at_bytes;
+    }
+    if (w.as_bytes < as_bytes) {
+      if (w.as) (void)hipFree(w.as);
+      w.as = nullptr;
+      w.as_bytes = 0;
+      e = hipMalloc(&w.as, as_bytes);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(SDQ_ERR_NOMEM, "workspace allocation failed");
+      }
+      w.as_bytes = as_bytes;
+    }
+  }
+  *out = &w;
+  return SDQ_OK;
+}
+
+int check_weight(const sdq_weight* w, int64_t K) {
+  if (!w) return set_error(SDQ_ERR_INVALID, "null weight handle");
+  if (K != w->K)
+    return set_error(SDQ_ERR_INVALID, "K mismatch: activations have K=" + std::to_string(K) +
+                                          ", weight has K=" + std::to_string(w->K));
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if (dev != w->device)
+    return set_error(SDQ_ERR_INVALID, "weight lives on device " + std::to_string(w->device) +
+                                          ", current device is " + std::to_string(dev));
+  return SDQ_OK;
+}
+
+int alloc_weight(int dev, int64_t N, int64_t K, sdq_weight** out) {
+  if (N < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative weight dims");
+  const int64_t Np = round_up(N < 1 ? 1 : N, kRowAlign);
+  const int64_t KFp = kfrags_padded(K);
+  const int64_t bytes = (Np / 16) * KFp * kFragBytes;
+  if (bytes >= (int64_t(1) << 40)) return set_error(SDQ_ERR_INVALID, "weight too large");
+  sdq_weight* w = new (std::nothrow) sdq_weight{dev, N, K, Np, KFp, nullptr, nullptr};
+  if (!w) return set_error(SDQ_ERR_NOMEM, "host allocation failed");
+  hipError_t e = hipMalloc(&w->frags, (size_t)bytes);
+  if (e == hipSuccess) e = hipMalloc(&w->scale, (size_t)Np * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (w->frags) (void)hipFree(w->frags);
+    delete w;
+    return set_error(SDQ_ERR_NOMEM, "weight allocation of " + std::to_string(bytes) +
+                                        " bytes failed");
+  }
+  *out = w;
+  return SDQ_OK;
+}
+
+EpiArgs make_epi(const sdq_epilogue* epi, int64_t K) {
+  EpiArgs e{};
+  e.kind = epi ? epi->kind : SDQ_EPI_NONE;
+  e.gate_fma = epi ? epi->gate_fma : 1;
+  e.kzero = K == 0 ? 1 : 0;
+  e.bias = epi ? epi->bias : nullptr;
+  e.gate = epi ? epi->gate : nullptr;
+  e.resid = epi ? epi->resid : nullptr;
+  return e;
+}
+
+int validate_epi(const sdq_epilogue* epi) {
+  if (!epi) return SDQ_OK;
+  switch (epi->kind) {
+    case SDQ_EPI_NONE:
+    case SDQ_EPI_GELU:
+    case SDQ_EPI_ACC:
+      return SDQ_OK;
+    case SDQ_EPI_GATED:
+      if (!epi->gate || !epi->resid)
+        return set_error(SDQ_ERR_INVALID, "GATED epilogue needs gate and resid");
+      return SDQ_OK;
+    case SDQ_EPI_RESID:
+      if (!epi->resid) return set_error(SDQ_ERR_INVALID, "RESID epilogue needs resid");
+      return SDQ_OK;
+    default:
+      return set_error(SDQ_ERR_INVALID, "unknown epilogue kind " + std::to_string(epi->kind));
+  }
+}
+
+}  // namespace
+
+int set_error(int code, const std::string& msg) {
+  t_err = msg;
+  return code;
+}
+
+int hip_error(hipError_t e, const char* what) {
+  t_err = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorOutOfMemory ? SDQ_ERR_NOMEM : SDQ_ERR_HIP;
+}
+
+// Core device-pointer path shared by the entry points.
+int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
+                   const sdq_epilogue* epi, void* Y, hipStream_t s) {
+  int rc = check_weight(w, K);
+  if (rc) return rc;
+  if ((rc = validate_epi(epi))) return rc;
+  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
+  if (M == 0 || w->N == 0) return SDQ_OK;
+  if (!A && K > 0) return set_error(SDQ_ERR_INVALID, "null A");
+  if (!Y) return set_error(SDQ_ERR_INVALID, "null Y");
+  if ((rc = ensure_device(w->device))) return rc;
+  const int64_t N = w->N;
+  if (M > (int64_t(1) << 30)) return set_error(SDQ_ERR_INVALID, "M too large");
+
+  const int cfg = choose_gemm_cfg(M, N, g_dev[w->device].cu_count);
+  const int64_t Mp = round_up(M, gemm_cfg_bm(cfg));
+  const size_t at_bytes = (size_t)(Mp / 16) * (size_t)w->KFp * kFragBytes;
+  Workspace* ws = nullptr;
+  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), &ws))) return rc;
+
+  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, s);
+  if (e != hipSuccess) return hip_error(e, "act_quant launch");
+  hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
+  const EpiArgs ea = make_epi(epi, K);
+  int vec = (N % 4 == 0) && aligned16(Y);
+  if (ea.bias) vec = vec && aligned16(ea.bias);
+  if (ea.gate) vec = vec && aligned16(ea.gate);
+  if (ea.resid) vec = vec && aligned16(ea.resid);
+  e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, s);
+  if (e != hipSuccess) return hip_error(e, "qgemm launch");
+  if (t_prof) {
+    hipEvent_t p2 = prof_mark(s);
+    if (p0 && p1 && p2) {
+      t_recs.push_back({"act_quant", p0, p1});
+      t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg), p1, p2});
+    } else {
+      for (hipEvent_t ev : {p0, p1, p2})
+        if (ev) (void)hipEventDestroy(ev);
+    }
+  }
+  return SDQ_OK;
+}
+
+}  // namespace sdq
+
+using namespace sdq;
+
+extern "C" {
+
+const char* sdq_last_error(void) { return t_err.c_str(); }
+
+const char* sdq_version(void) { return "sdq 0.1 gfx950"; }
+
+int sdq_init(int device) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n || device >= kMaxDev)
+    return set_error(SDQ_ERR_NODEV, "no device " + std::to_string(device) + " (" +
+                                        std::to_string(n) + " visible)");
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_error(e, "hipSetDevice");
+  return ensure_device(device);
+}
+
+int sdq_device_info_get(sdq_device_info* out) {
+  if (!out) return set_error(SDQ_ERR_INVALID, "null out");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const hipDeviceProp_t& p = g_dev[dev].prop;
+  out->device = dev;
+  out->cu_count = p.multiProcessorCount;
+  out->max_clock_khz = p.clockRate;
+  out->mem_clock_khz = p.memoryClockRate;
+  out->total_mem = (int64_t)p.totalGlobalMem;
+  std::snprintf(out->arch, sizeof(out->arch), "%s", p.gcnArchName);
+  return SDQ_OK;
+}
+
+int sdq_weight_upload(const int8_t* q, const float* scale, int64_t N, int64_t K, void* stream,
+                      sdq_weight** out) {
+  if (!out) return set_error(SDQ_ERR_INVALID, "null out");
+  *out = nullptr;
+  if (N < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative weight dims");
+  if ((N * K > 0 && !q) || (N > 0 && !scale)) return set_error(SDQ_ERR_INVALID, "null weight data");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  sdq_weight* w = nullptr;
+  if ((rc = alloc_weight(dev, N, K, &w))) return rc;
+  // Stage the .sdcpp blob as it is on disk (int8 rows, then the scales,
+  // which may be unaligned in the source) into one device buffer.
+  const size_t qbytes = (size_t)(N * K);
+  const size_t soff = (size_t)round_up((int64_t)qbytes, 256);
+  const size_t sbytes = (size_t)N * 4;
+  void* stage = nullptr;
+  hipError_t e = hipMalloc(&stage, soff + sbytes + 16);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    sdq_weight_free(w);
+    return set_error(SDQ_ERR_NOMEM, "staging allocation failed");
+  }
+  char* st = static_cast<char*>(stage);
+  if (qbytes) e = hipMemcpyAsync(st, q, qbytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && sbytes) e = hipMemcpyAsync(st + soff, scale, sbytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = launch_repack_weight(reinterpret_cast<int8_t*>(st), reinterpret_cast<float*>(st + soff), N,
+                             K, w->Np, w->KFp, w->frags, w->scale, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  (void)hipFree(stage);
+  if (e != hipSuccess) {
+    sdq_weight_free(w);
+    return hip_error(e, "weight upload");
+  }
+  *out = w;
+  return SDQ_OK;
+}
+
+int sdq_weight_upload_device(const int8_t* q_dev, const float* scale_dev, int64_t N, int64_t K,
+                             void* stream, sdq_weight** out) {
+  if (!out) return set_error(SDQ_ERR_INVALID, "null out");
+  *out = nullptr;
+  if (N < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative weight dims");
+  if ((N * K > 0 && !q_dev) || (N > 0 && !scale_dev))
+    return set_error(SDQ_ERR_INVALID, "null weight data");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  sdq_weight* w = nullptr;
+  if ((rc = alloc_weight(dev, N, K, &w))) return rc;
+  hipError_t e = launch_repack_weight(q_dev, scale_dev, N, K, w->Np, w->KFp, w->frags, w->scale, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    sdq_weight_free(w);
+    return hip_error(e, "weight repack");
+  }
+  *out = w;
+  return SDQ_OK;
+}
+
+int sdq_weight_free(sdq_weight* w) {
+  if (!w) return SDQ_OK;
+  if (w->frags) (void)hipFree(w->frags);
+  if (w->scale) (void)hipFree(w->scale);
+  delete w;
+  return SDQ_OK;
+}
+
+int sdq_weight_dims(const sdq_weight* w, int64_t* N, int64_t* K) {
+  if (!w) return set_error(SDQ_ERR_INVALID, "null weight handle");
+  if (N) *N = w->N;
+  if (K) *K = w->K;
+  return SDQ_OK;
+}
+
+int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale) {
+  if (!w) return set_error(SDQ_ERR_INVALID, "null weight handle");
+  const size_t qbytes = (size_t)(w->N * w->K);
+  int8_t* tmp = nullptr;
+  hipError_t e = hipSuccess;
+  if (qbytes) {
+    e = hipMalloc(&tmp, qbytes);
+    if (e != hipSuccess) return hip_error(e, "hipMalloc");
+    e = launch_unpack_weight(w->frags, w->N, w->K, w->KFp, tmp, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(q, tmp, qbytes, hipMemcpyDeviceToHost);
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return hip_error(e, "weight export");
+  }
+  if (scale && w->N) {
+    e = hipMemcpy(scale, w->scale, (size_t)w->N * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_error(e, "scale export");
+  }
+  return SDQ_OK;
+}
+
+int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
+                void* Y, void* stream) {
+  return qlinear_device(w, A, M, K, epi, Y, static_cast<hipStream_t>(stream));
+}
+
+int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream) {
+  return qlinear_device(w, A, M, K, nullptr, Y, static_cast<hipStream_t>(stream));
+}
+
+int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
+                     const sdq_epilogue* epi, void* Y) {
+  int rc = check_weight(w, K);
+  if (rc) return rc;
+  if ((rc = validate_epi(epi))) return rc;
+  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
+  const int64_t N = w->N;
+  if (M == 0 || N == 0) return SDQ_OK;
+  const size_t abytes = (size_t)(M * K) * 4, ybytes = (size_t)(M * N) * 4;
+  char* buf = nullptr;
+  // one block: A | Y | resid | bias | gate, each 256-byte aligned
+  auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const bool has_resid = epi && epi->resid;
+  const size_t o_y = al(abytes), o_r = o_y + al(ybytes), o_b = o_r + (has_resid ? al(ybytes) : 0);
+  const size_t o_g = o_b + al((size_t)N * 4), total = o_g + al((size_t)N * 4);
+  hipError_t e = hipMalloc(&buf, total);
+  if (e != hipSuccess) return hip_error(e, "hipMalloc (host-call buffers)");
+  sdq_epilogue de{};
+  if (epi) de = *epi;
+  if (abytes) e = hipMemcpy(buf, A, abytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess && has_resid) {
+    e = hipMemcpy(buf + o_r, epi->resid, ybytes, hipMemcpyHostToDevice);
+    de.resid = reinterpret_cast<float*>(buf + o_r);
+  }
+  if (e == hipSuccess && epi && epi->bias) {
+    e = hipMemcpy(buf + o_b, epi->bias, (size_t)N * 4, hipMemcpyHostToDevice);
+    de.bias = reinterpret_cast<float*>(buf + o_b);
+  }
+  if (e == hipSuccess && epi && epi->gate) {
+    e = hipMemcpy(buf + o_g, epi->gate, (size_t)N * 4, hipMemcpyHostToDevice);
+    de.gate = reinterpret_cast<float*>(buf + o_g);
+  }
+  if (e != hipSuccess) {
+    (void)hipFree(buf);
+    return hip_error(e, "hipMemcpy H2D");
+  }
+  rc = qlinear_device(w, reinterpret_cast<float*>(buf), M, K, epi ? &de : nullptr, buf + o_y,
+                      nullptr);
+  if (rc == SDQ_OK) {
+    e = hipMemcpy(Y, buf + o_y, ybytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) rc = hip_error(e, "hipMemcpy D2H");
+  }
+  (void)hipFree(buf);
+  return rc;
+}
+
+int sdq_act_quant(const float* A, int64_t M, int64_t K, int8_t* aq, float* as, void* stream) {
+  if (M < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative dims");
+  if (M == 0) return SDQ_OK;
+  if (!as || (K > 0 && (!A || !aq))) return set_error(SDQ_ERR_INVALID, "null pointer");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  hipError_t e = launch_act_quant_rowmajor(A, M, K, aq, as, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_error(e, "act_quant launch");
+  return SDQ_OK;
+}
+
+int sdq_device_alloc(size_t bytes, void** out) {
+  if (!out) return set_error(SDQ_ERR_INVALID, "null out");
+  *out = nullptr;
+  hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(SDQ_ERR_NOMEM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  }
+  return SDQ_OK;
+}
+
+int sdq_device_free(void* p) {
+  if (!p) return SDQ_OK;
+  hipError_t e = hipFree(p);
+  if (e != hipSuccess) return hip_error(e, "hipFree");
+  return SDQ_OK;
+}
+
+int sdq_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+  if (bytes == 0) return SDQ_OK;
+  if (!dst || !src) return set_error(SDQ_ERR_INVALID, "null pointer");
+  hipMemcpyKind k;
+  switch (kind) {
+    case SDQ_H2D: k = hipMemcpyHostToDevice; break;
+    case SDQ_D2H: k = hipMemcpyDeviceToHost; break;
+    case SDQ_D2D: k = hipMemcpyDeviceToDevice; break;
+    default: return set_error(SDQ_ERR_INVALID, "bad copy kind");
+  }
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, k, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync");
+  return SDQ_OK;
+}
+
+int sdq_stream_sync(void* stream) {
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  return SDQ_OK;
+}
+
+int sdq_profile_begin(void) {
+  t_prof = true;
+  return SDQ_OK;
+}
+
+int sdq_profile_end(sdq_kernel_time* out, int max_records, int* n_records) {
+  t_prof = false;
+  std::vector<std::pair<std::string, std::pair<int, double>>> agg;
+  std::set<hipEvent_t> owned;
+  int rc = SDQ_OK;
+  for (const ProfRec& r : t_recs) {
+    owned.insert(r.a);
+    owned.insert(r.b);
+    if (rc != SDQ_OK) continue;
+    hipError_t e = hipEventSynchronize(r.b);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) {
+      rc = hip_error(e, "profile events");
+      continue;
+    }
+    auto it = agg.begin();
+    for (; it != agg.end(); ++it)
+      if (it->first == r.name) break;
+    if (it == agg.end()) {
+      agg.push_back({r.name, {0, 0.0}});
+      it = agg.end() - 1;
+    }
+    it->second.first += 1;
+    it->second.second += ms;
+  }
+  for (hipEvent_t ev : owned) (void)hipEventDestroy(ev);
+  t_recs.clear();
+  if (rc != SDQ_OK) return rc;
+  int n = 0;
+  for (const auto& a : agg) {
+    if (out && n < max_records) {
+      std::snprintf(out[n].name, sizeof(out[n].name), "%s", a.first.c_str());
+      out[n].launches = a.second.first;
+      out[n].total_ms = a.second.second;
+    }
+    n++;
+  }
+  if (n_records) *n_records = n;
+  return SDQ_OK;
+}
+
+int sdq_sync(void) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_error(e, "hipDeviceSynchronize");
+  return SDQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+// Internal declarations shared by the sdq HIP translation units.
+//
+// Fragment layout ("frag layout") used for both operands in HBM:
+//   an operand with R rows and K int8 columns is cut into 16-row x 64-byte
+//   fragments; fragment (rb, kb) covers rows [16rb, 16rb+16) and columns
+//   [64kb, 64kb+64). It occupies 1024 contiguous bytes at
+//   ((rb * KFp) + kb) * 1024, and inside it lane l (0..63) owns the 16 bytes
+//   at l*16, holding row 16rb + (l & 15), columns 64kb + 16(l >> 4) .. +15.
+//   This is exactly the per-lane operand of v_mfma_i32_16x16x64_i8, so a
+//   1 KB fragment moves global -> LDS -> VGPRs as one linear, conflict-free
+//   wave-wide 16-byte-per-lane copy. Rows are padded to a multiple of the
+//   largest GEMM tile and KFp to a multiple of 4 fragments with zeros.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "sdq.h"
+
+namespace sdq {
+
+constexpr int kFragRows = 16;
+constexpr int kFragK = 64;
+constexpr int kFragBytes = 1024;
+constexpr int kKFragAlign = 4;   // KFp is a multiple of this many fragments
+constexpr int kRowAlign = 256;   // weight rows padded to this (largest BN)
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+inline int64_t kfrags_padded(int64_t K) {
+  return round_up(ceil_div(K < 1 ? 1 : K, kFragK), kKFragAlign);
+}
+
+// Sets the thread-local error text and returns `code`.
+int set_error(int code, const std::string& msg);
+int hip_error(hipError_t e, const char* what);
+
+#define SDQ_HIP(call)                                     \
+  do {                                                    \
+    hipError_t e_ = (call);                               \
+    if (e_ != hipSuccess) return ::sdq::hip_error(e_, #call); \
+  } while (0)
+
+struct EpiArgs {
+  int kind;
+  int gate_fma;
+  int kzero;  // K == 0: the product is +0 (the reference returns its zero-filled out)
+  const float* bias;
+  const float* gate;
+  const float* resid;
+};
+
+// ---- launchers (return hipError_t of the launch) -------------------------
+// Activation quantizer: A [M,K] f32 row-major -> frag layout (rows padded to
+// Mp, zero rows beyond M) + as[M].
+hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
+                                  int8_t* at, float* as, hipStream_t s);
+// Same quantizer, row-major int8 output [M,K] (parity API).
+hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
+                                     hipStream_t s);
+// Weight repack: q [N,K] row-major (device) + scale (device, aligned) ->
+// frag layout with Np rows + scale padded with zeros to Np.
+hipError_t launch_repack_weight(const int8_t* q, const float* scale, int64_t N, int64_t K,
+                                int64_t Np, int64_t KFp, int8_t* frags, float* scale_out,
+                                hipStream_t s);
+// Inverse of the repack (export / round-trip check).
+hipError_t launch_unpack_weight(const int8_t* frags, int64_t N, int64_t K, int64_t KFp,
+                                int8_t* q, hipStream_t s);
+
+// GEMM tile configurations.
+enum GemmCfg : int {
+  kCfgSkinny1 = 0,  // M <= 16: one 16-row activation block, split-K waves
+  kCfgSkinny2,      // M <= 32
+  kCfgSkinny4,      // M <= 64
+  kCfg128x128,      // BN=128, BM=128
+  kCfg256x256,      // BN=256, BM=256
+  kCfgCount
+};
+int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
+const char* gemm_cfg_name(int cfg);
+int choose_gemm_cfg(int64_t M, int64_t N, int cu_count);
+
+hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,
+                        const float* as, int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi,
+                        void* Y, int vec_ok, hipStream_t s);
+
+}  // namespace sdq

@@ -1,0 +1,171 @@
+// Per-row dynamic activation quantizer (gfx950).
+//
+// Restates src/core/qgemm.cpp:82-96 of the reference bit-exactly:
+//   mx  = max_k |A[i,k]|  (NaN inputs never win the max, as std::max(mx,|r|))
+//   sc  = mx / 127.f (IEEE, correctly rounded); sc == 0 -> 1
+//   inv = 1.f / sc (correctly rounded)
+//   q   = clamp(cvt_rne(A[i,k] * inv), -127, 127), where NaN and values whose
+//         rounded result leaves int32 give -127 (x86 cvtss2si "indefinite"
+//         INT_MIN, then clamped), src/core/qgemm.cpp:62-69.
+//
+// One workgroup owns one 16-row block (one fragment row) so it can emit
+// whole 1 KB fragments: every lane loads the 16 floats it will own in the
+// fragment, keeps up to CACHE fragments in registers across the amax
+// reduction (single HBM read when K <= NW*CACHE*64), and re-reads only the
+// tail beyond that.
+#include "sdq_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace sdq {
+namespace {
+
+constexpr int kQuantWaves = 8;
+constexpr int kQuantCache = 6;  // 8 waves x 6 frags x 64 = K <= 3072 in one pass
+
+__device__ __forceinline__ int quant_one(float v, float inv) {
+  const float y = v * inv;
+  const float t = __builtin_rintf(y);  // v_rndne_f32: ties to even
+  // NaN and |t| >= 2^31 fail this test, like cvtss2si returning INT_MIN.
+  if (!(t >= -2147483648.0f && t < 2147483648.0f)) return -127;
+  const float c = t < -127.f ? -127.f : (t > 127.f ? 127.f : t);
+  return (int)c;
+}
+
+__device__ __forceinline__ void load16(const float* __restrict__ rowp, int64_t k0, int64_t K,
+                                       bool row_ok, bool vec, float v[16]) {
+  if (row_ok && vec && k0 + 16 <= K) {
+    const float4* p = reinterpret_cast<const float4*>(rowp + k0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float4 x = p[i];
+      v[4 * i + 0] = x.x;
+      v[4 * i + 1] = x.y;
+      v[4 * i + 2] = x.z;
+      v[4 * i + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int64_t k = k0 + e;
+      v[e] = (row_ok && k < K) ? rowp[k] : 0.f;
+    }
+  }
+}
+
+__device__ __forceinline__ float amax16(const float v[16], float mx) {
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const float a = fabsf(v[e]);
+    mx = (mx < a) ? a : mx;  // std::max(mx, a): keeps mx when a is NaN
+  }
+  return mx;
+}
+
+__device__ __forceinline__ uint4 pack16(const float v[16], float inv) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) x |= (uint32_t)(uint8_t)(int8_t)quant_one(v[4 * i + b], inv) << (8 * b);
+    w[i] = x;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <int NW, int CACHE, bool FRAG_OUT>
+__global__ void __launch_bounds__(NW * 64)
+act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, int64_t KFp,
+                 int vec, int8_t* __restrict__ out, float* __restrict__ as) {
+  const int w = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
+  const int64_t rb = blockIdx.x;
+  const int64_t row = rb * 16 + (l & 15);
+  const bool row_ok = row < M;
+  const float* rowp = A + (row_ok ? row : 0) * K;
+  const int kg = (l >> 4) * 16;
+
+  float cache[CACHE][16];
+  float mx = 0.f;
+#pragma unroll
+  for (int c = 0; c < CACHE; c++) {
+    const int64_t kb = w + (int64_t)c * NW;
+    if (kb < KL) {
+      load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, cache[c]);
+      mx = amax16(cache[c], mx);
+    }
+  }
+  for (int64_t kb = w + (int64_t)CACHE * NW; kb < KL; kb += NW) {
+    float t[16];
+    load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, t);
+    mx = amax16(t, mx);
+  }
+  // Lanes l, l^16, l^32, l^48 hold the same row.
+  float o = __shfl_xor(mx, 16);
+  mx = (mx < o) ? o : mx;
+  o = __shfl_xor(mx, 32);
+  mx = (mx < o) ? o : mx;
+  __shared__ float red[NW][16];
+  if (l < 16) red[w][l] = mx;
+  __syncthreads();
+  mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; i++) {
+    const float r = red[i][l & 15];
+    mx = (mx < r) ? r : mx;
+  }
+  float sc = mx / 127.f;
+  if (sc == 0.f) sc = 1.f;
+  const float inv = 1.f / sc;
+  if (w == 0 && l < 16 && row_ok) as[row] = sc;
+
+  auto emit = [&](int64_t kb, const float v[16]) {
+    const uint4 q = pack16(v, inv);
+    if (FRAG_OUT) {
+      *reinterpret_cast<uint4*>(out + (rb * KFp + kb) * 1024 + l * 16) = q;
+    } else if (row_ok) {
+      const int64_t k0 = kb * 64 + kg;
+      int8_t* dst = out + row * K;
+      const uint32_t wds[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int e = 0; e < 16; e++)
+        if (k0 + e < K) dst[k0 + e] = (int8_t)(wds[e >> 2] >> (8 * (e & 3)));
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < CACHE; c++) {
+    const int64_t kb = w + (int64_t)c * NW;
+    if (kb < KL) emit(kb, cache[c]);
+  }
+  for (int64_t kb = w + (int64_t)CACHE * NW; kb < KL; kb += NW) {
+    float t[16];
+    load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, t);
+    emit(kb, t);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
+                                  int8_t* at, float* as, hipStream_t s) {
+  const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
+  const int64_t blocks = Mp / 16;
+  hipLaunchKernelGGL((act_quant_kernel<kQuantWaves, kQuantCache, true>), dim3((unsigned)blocks),
+                     dim3(kQuantWaves * 64), 0, s, A, M, K, KFp, KFp, vec, at, as);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
+                                     hipStream_t s) {
+  const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
+  const int64_t blocks = ceil_div(M, 16);
+  const int64_t KL = ceil_div(K, 64);
+  hipLaunchKernelGGL((act_quant_kernel<kQuantWaves, kQuantCache, false>), dim3((unsigned)blocks),
+                     dim3(kQuantWaves * 64), 0, s, A, M, K, KL, KL, vec, aq, as);
+  return hipGetLastError();
+}
+
+}  // namespace sdq

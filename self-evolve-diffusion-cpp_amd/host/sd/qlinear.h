@@ -1,0 +1,70 @@
+// GPU int8 Linear for the DiT blocks: the device side of the reference's
+// `mlin` (src/model/ovi_dit.cpp:66-84) and of the consumers that follow it.
+//
+// A QLinear is built once from the I8 [out,in] view + ".scale" view that
+// load_sdcpp returns (checked to sit right after the int8 blob, as
+// OviDit::load_impl's lin() requires, ovi_dit.cpp:397-415) and an F32 bias.
+// Host-tensor calls (mlin*) are synchronous and bit-identical to the
+// reference's qgemm + bias pass (+ gated_add_inplace / add_inplace);
+// device-pointer calls (forward_device) are stream-ordered.
+#pragma once
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "sd/tensor.h"
+#include "sdq.h"
+
+namespace sd {
+namespace gpu {
+
+class QLinear {
+ public:
+  QLinear() = default;
+  // w: I8 [out,in] view; scale: F32 [out] view; bias: F32 [out] or empty.
+  QLinear(const Tensor& w, const Tensor& scale, const Tensor& bias);
+  QLinear(const QLinear&) = delete;
+  QLinear& operator=(const QLinear&) = delete;
+  QLinear(QLinear&& o) noexcept;
+  QLinear& operator=(QLinear&& o) noexcept;
+  ~QLinear();
+
+  int64_t in_features() const { return K_; }
+  int64_t out_features() const { return N_; }
+  const sdq_weight* handle() const { return w_; }
+  const float* bias_device() const { return bias_dev_; }
+
+  // y = x W^T + b    (mlin, ovi_dit.cpp:66-84)
+  void mlin(const Tensor& x, Tensor& y) const;
+  // y = gelu_tanh(x W^T + b)   (ffn fc1 + gelu_tanh_inplace, ovi_dit.cpp:217-218)
+  void mlin_gelu(const Tensor& x, Tensor& y) const;
+  // res += (x W^T + b) * gate   (gated_add_inplace, ovi_dit.cpp:152-159, fma form)
+  void mlin_gated_add(const Tensor& x, const Tensor& gate, Tensor& res) const;
+  // res += x W^T + b   (add_inplace, ovi_dit.cpp:144-149)
+  void mlin_add(const Tensor& x, Tensor& res) const;
+
+  // Device pointers, stream-ordered: Y = epilogue(x W^T + b).
+  void forward_device(const float* x, int64_t M, int kind, const float* gate, const float* resid,
+                      float* Y, void* stream) const;
+
+ private:
+  void run_host(const Tensor& x, int kind, const Tensor* gate, Tensor* res, Tensor* y) const;
+  sdq_weight* w_ = nullptr;
+  float* bias_dev_ = nullptr;
+  std::vector<float> bias_host_;
+  int64_t N_ = 0, K_ = 0;
+};
+
+// OviDit::load_impl's lin() (src/model/ovi_dit.cpp:397-415) on a load_sdcpp
+// map: "<base>.weight" must be I8 [out,in] with "<base>.weight.scale" stored
+// right after the int8 blob, and "<base>.bias" F32 [out]. Throws
+// std::runtime_error("ovi_dit: …") like the reference otherwise.
+QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                          const std::string& base, int64_t in, int64_t out);
+
+// Throws std::runtime_error with sdq_last_error() when rc != SDQ_OK.
+void check(int rc, const char* what);
+
+}  // namespace gpu
+}  // namespace sd

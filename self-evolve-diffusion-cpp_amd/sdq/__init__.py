@@ -1,0 +1,244 @@
+"""Python binding of the sdq C ABI (include/sdq.h) via ctypes.
+
+The library does the work; this module only marshals pointers. Device
+buffers come from torch (ROCm) tensors and the stream from
+torch.cuda.current_stream(); nothing here computes results itself, and a
+missing libsdq.so raises instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libsdq.so")
+HOST_TEST_BIN = os.path.join(LIB_DIR, "test_host")
+
+OK = 0
+ERR_INVALID, ERR_HIP, ERR_NOMEM, ERR_FORMAT, ERR_NODEV, ERR_NOTFOUND = 1, 2, 3, 4, 5, 6
+EPI_NONE, EPI_GELU, EPI_GATED, EPI_RESID, EPI_ACC = 0, 1, 2, 3, 4
+EPI_NAMES = {"none": EPI_NONE, "gelu": EPI_GELU, "gated": EPI_GATED, "resid": EPI_RESID,
+             "acc": EPI_ACC}
+
+
+class SdqError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"sdq error {code}: {msg}")
+        self.code = code
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("gate_fma", ctypes.c_int),
+                ("bias", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("resid", ctypes.c_void_p)]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("device", ctypes.c_int), ("cu_count", ctypes.c_int),
+                ("max_clock_khz", ctypes.c_int), ("mem_clock_khz", ctypes.c_int),
+                ("total_mem", ctypes.c_int64), ("arch", ctypes.c_char * 64)]
+
+
+class KernelTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int),
+                ("total_ms", ctypes.c_double)]
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes); mirrors include/sdq.h
+SIGNATURES = {
+    "sdq_last_error": (ctypes.c_char_p, []),
+    "sdq_version": (ctypes.c_char_p, []),
+    "sdq_init": (ctypes.c_int, [ctypes.c_int]),
+    "sdq_device_info_get": (ctypes.c_int, [ctypes.POINTER(DeviceInfo)]),
+    "sdq_weight_upload": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
+    "sdq_weight_upload_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
+    "sdq_weight_free": (ctypes.c_int, [_vp]),
+    "sdq_weight_dims": (ctypes.c_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
+    "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
+    "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_qlinear_host": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp]),
+    "sdq_act_quant": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "sdq_device_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "sdq_device_free": (ctypes.c_int, [_vp]),
+    "sdq_memcpy": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
+    "sdq_stream_sync": (ctypes.c_int, [_vp]),
+    "sdq_profile_begin": (ctypes.c_int, []),
+    "sdq_profile_end": (ctypes.c_int, [ctypes.POINTER(KernelTime), ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_int)]),
+    "sdq_sync": (ctypes.c_int, []),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libsdq.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"libsdq.so not built: {path} (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc):
+    if rc != OK:
+        msg = _lib.sdq_last_error().decode(errors="replace")
+        raise SdqError(rc, msg)
+
+
+def init(device: int = 0):
+    _check(load_library().sdq_init(device))
+
+
+def device_info() -> dict:
+    info = DeviceInfo()
+    _check(load_library().sdq_device_info_get(ctypes.byref(info)))
+    return dict(device=info.device, cu_count=info.cu_count, max_clock_khz=info.max_clock_khz,
+                mem_clock_khz=info.mem_clock_khz, total_mem=info.total_mem,
+                arch=info.arch.decode())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return ctypes.c_void_p(stream)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, np.ndarray):
+        return t.ctypes.data_as(ctypes.c_void_p)
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Weight:
+    """Device copy of an int8 [N,K] weight + f32 [N] scales (one-time upload
+    and repack into the MFMA fragment layout)."""
+
+    def __init__(self, handle, N, K):
+        self.h = handle
+        self.N, self.K = int(N), int(K)
+
+    @classmethod
+    def from_host(cls, q: np.ndarray, scale, stream=None):
+        """q: int8 [N,K]; scale: float32 [N], or raw bytes / uint8 array of
+        4N bytes (e.g. an unaligned slice of a .sdcpp blob)."""
+        lib = load_library()
+        q = np.ascontiguousarray(q, np.int8)
+        N, K = q.shape
+        if isinstance(scale, (bytes, bytearray, memoryview)):
+            sbuf = np.frombuffer(scale, np.uint8)
+        else:
+            sbuf = np.ascontiguousarray(scale)
+        if sbuf.nbytes != 4 * N:
+            raise ValueError("scale must hold N float32 values")
+        h = ctypes.c_void_p()
+        _check(lib.sdq_weight_upload(_ptr(q), _ptr(sbuf), N, K,
+                                     _stream(stream) if stream is not None else None,
+                                     ctypes.byref(h)))
+        return cls(h, N, K)
+
+    @classmethod
+    def from_device(cls, q_dev, scale_dev, stream=None):
+        lib = load_library()
+        N, K = q_dev.shape
+        h = ctypes.c_void_p()
+        _check(lib.sdq_weight_upload_device(_ptr(q_dev), _ptr(scale_dev), N, K, _stream(stream),
+                                            ctypes.byref(h)))
+        return cls(h, N, K)
+
+    def export(self):
+        q = np.empty((self.N, self.K), np.int8)
+        s = np.empty((self.N,), np.float32)
+        _check(_lib.sdq_weight_export_host(self.h, _ptr(q), _ptr(s)))
+        return q, s
+
+    def free(self):
+        if self.h is not None and self.h.value:
+            _lib.sdq_weight_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:  # pragma: no cover - interpreter shutdown
+            pass
+
+
+def make_epilogue(kind="none", bias=None, gate=None, resid=None, gate_fma=True):
+    e = Epilogue()
+    e.kind = EPI_NAMES[kind] if isinstance(kind, str) else int(kind)
+    e.gate_fma = 1 if gate_fma else 0
+    e.bias = _ptr(bias)
+    e.gate = _ptr(gate)
+    e.resid = _ptr(resid)
+    return e
+
+
+def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, gate_fma=True,
+            stream=None):
+    """out = epilogue(qgemm(A, W) + bias) on device tensors (stream-ordered)."""
+    M, K = A.shape
+    e = make_epilogue(kind, bias, gate, resid, gate_fma)
+    _check(_lib.sdq_qlinear(w.h, _ptr(A), M, K, ctypes.byref(e), _ptr(out), _stream(stream)))
+    return out
+
+
+def qgemm(w: Weight, A, out, stream=None):
+    M, K = A.shape
+    _check(_lib.sdq_qgemm(w.h, _ptr(A), M, K, _ptr(out), _stream(stream)))
+    return out
+
+
+def qlinear_host(w: Weight, A: np.ndarray, kind="none", bias=None, gate=None, resid=None,
+                 gate_fma=True):
+    """Synchronous host-array variant (copies in and out)."""
+    A = np.ascontiguousarray(A, np.float32)
+    M, K = A.shape
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    gate = None if gate is None else np.ascontiguousarray(gate, np.float32)
+    resid = None if resid is None else np.ascontiguousarray(resid, np.float32)
+    out = np.empty((M, w.N), np.int32 if kind == "acc" else np.float32)
+    e = make_epilogue(kind, bias, gate, resid, gate_fma)
+    _check(_lib.sdq_qlinear_host(w.h, _ptr(A), M, K, ctypes.byref(e), _ptr(out)))
+    return out
+
+
+def act_quant(A, aq, asc, stream=None):
+    M, K = A.shape
+    _check(_lib.sdq_act_quant(_ptr(A), M, K, _ptr(aq), _ptr(asc), _stream(stream)))
+
+
+def profile_begin():
+    _check(load_library().sdq_profile_begin())
+
+
+def profile_end() -> dict:
+    """{kernel name: (launches, total device ms)} since profile_begin()."""
+    recs = (KernelTime * 32)()
+    n = ctypes.c_int()
+    _check(_lib.sdq_profile_end(recs, 32, ctypes.byref(n)))
+    return {recs[i].name.decode(): (recs[i].launches, recs[i].total_ms)
+            for i in range(min(n.value, 32))}
+
+
+def sync():
+    _check(_lib.sdq_sync())

@@ -1,0 +1,83 @@
+"""C ABI surface (no GPU needed): the library loads, exports exactly what
+include/sdq.h declares, links nothing from oracle/, and errors cleanly."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import PKG, ROOT
+
+HEADER = os.path.join(ROOT, "include", "sdq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sdq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("sdq_init", "sdq_weight_upload", "sdq_qlinear", "sdq_qgemm",
+                 "sdq_qlinear_host", "sdq_act_quant", "sdq_weight_free", "sdq_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    import sdq
+
+    lib = sdq.load_library()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared_functions()) == set(sdq.SIGNATURES), "binding out of sync with header"
+
+
+def test_library_does_not_link_the_oracle():
+    out = subprocess.run(["ldd", os.path.join(PKG, "lib", "libsdq.so")], capture_output=True,
+                         text=True).stdout
+    assert "oracle" not in out and "sdref" not in out
+    nm = subprocess.run(["nm", "-D", "--defined-only", os.path.join(PKG, "lib", "libsdq.so")],
+                        capture_output=True, text=True).stdout
+    assert "orc_" not in nm and "sdref_" not in nm
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    import sdq
+
+    monkeypatch.setattr(sdq, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        sdq.load_library(str(tmp_path / "nope.so"))
+
+
+def test_errors_without_device_are_codes_not_crashes():
+    """Argument validation runs before any device work."""
+    import sdq
+
+    lib = sdq.load_library()
+    out = ctypes.c_void_p()
+    rc = lib.sdq_weight_upload(None, None, -1, 4, None, ctypes.byref(out))
+    assert rc == sdq.ERR_INVALID
+    assert b"negative" in lib.sdq_last_error()
+    rc = lib.sdq_qgemm(None, None, 4, 4, None, None)
+    assert rc == sdq.ERR_INVALID
+    assert b"null weight" in lib.sdq_last_error()
+    assert lib.sdq_weight_free(None) == 0
+    assert lib.sdq_version().startswith(b"sdq")
+
+
+def test_host_mirror_headers_compile_standalone(tmp_path):
+    """The C++17 mirror of the reference interface builds with plain g++."""
+    src = tmp_path / "use.cpp"
+    src.write_text(
+        '#include "sd/tensor.h"\n#include "sd/sdcpp.h"\n#include "sd/qlinear.h"\n'
+        "int main(){ sd::Tensor t({2,3}, sd::DType::F32); return (int)t.numel() - 6; }\n")
+    exe = tmp_path / "use"
+    r = subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), "-I",
+                        os.path.join(PKG, "host"), str(src), "-o", str(exe), "-L",
+                        os.path.join(PKG, "lib"), "-lsd_host", "-lsdq",
+                        "-Wl,-rpath," + os.path.join(PKG, "lib")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    assert subprocess.run([str(exe)]).returncode == 0

@@ -1,0 +1,343 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle:
+bit-exact quantized activations, int32 accumulators and fp32 outputs."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(M, K, N, seed):
+    import pyoracle
+
+    A = pyoracle.randn(M * K, seed).reshape(M, K)
+    W = pyoracle.randn(N * K, seed + 1).reshape(N, K) * np.float32(0.02)
+    q, s = pyoracle.quant_rows(W)
+    bias = pyoracle.randn(N, seed + 2) * np.float32(0.01)
+    return A, q, s, bias
+
+
+def _run(sdq_dev, w, A, kind="none", bias=None, gate=None, resid=None, gate_fma=True):
+    import torch
+
+    import sdq
+
+    M = A.shape[0]
+    dt = torch.int32 if kind == "acc" else torch.float32
+    A_d = torch.from_numpy(np.ascontiguousarray(A)).to(sdq_dev)
+    Y = torch.full((M, w.N), -7, dtype=dt, device=sdq_dev)
+    b_d = None if bias is None else torch.from_numpy(bias).to(sdq_dev)
+    g_d = None if gate is None else torch.from_numpy(gate).to(sdq_dev)
+    r_d = None if resid is None else torch.from_numpy(np.ascontiguousarray(resid)).to(sdq_dev)
+    sdq.qlinear(w, A_d, Y, kind=kind, bias=b_d, gate=g_d, resid=r_d, gate_fma=gate_fma)
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+# --------------------------------------------------------------- quantizer
+@pytest.mark.parametrize("M,K", [(1, 31), (17, 64), (37, 320), (256, 3072), (5, 14336),
+                                 (33, 4160), (3, 1), (20, 100)])
+def test_act_quant_bitexact(sdq_dev, oracle, M, K):
+    import torch
+
+    import sdq
+
+    rng = np.random.default_rng(M * 1000 + K)
+    A = (rng.standard_normal((M, K)) * rng.uniform(1e-3, 1e3, (M, 1))).astype(np.float32)
+    A_d = torch.from_numpy(A).to(sdq_dev)
+    aq = torch.zeros((M, K), dtype=torch.int8, device=sdq_dev)
+    asc = torch.zeros((M,), dtype=torch.float32, device=sdq_dev)
+    sdq.act_quant(A_d, aq, asc)
+    torch.cuda.synchronize()
+    want_q, want_s = oracle.act_quant(A)
+    assert_bitexact(asc.cpu().numpy(), want_s, "as")
+    assert_bitexact(aq.cpu().numpy(), want_q, "aq")
+
+
+def test_act_quant_special_rows(sdq_dev, oracle):
+    import torch
+
+    import sdq
+
+    g = np.load(os.path.join(GOLDEN, "ref_qgemm.npz"))
+    A = g["special_a"]
+    M, K = A.shape
+    A_d = torch.from_numpy(A).to(sdq_dev)
+    aq = torch.zeros((M, K), dtype=torch.int8, device=sdq_dev)
+    asc = torch.zeros((M,), dtype=torch.float32, device=sdq_dev)
+    sdq.act_quant(A_d, aq, asc)
+    torch.cuda.synchronize()
+    want_q, want_s = oracle.act_quant(A)
+    assert_bitexact(asc.cpu().numpy(), want_s, "as")
+    assert_bitexact(aq.cpu().numpy(), want_q, "aq")
+
+
+# ------------------------------------------------------------ weight repack
+@pytest.mark.parametrize("N,K", [(13, 31), (256, 3072), (300, 257), (18432, 64)])
+def test_weight_repack_roundtrip(sdq_dev, N, K):
+    import sdq
+
+    rng = np.random.default_rng(N + K)
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    # scales at an odd byte offset, as in a .sdcpp blob with no padding
+    raw = bytearray(b"\x00" + s.tobytes())
+    w = sdq.Weight.from_host(q, memoryview(raw)[1:])
+    q2, s2 = w.export()
+    assert_bitexact(q2, q, "q")
+    assert_bitexact(s2, s, "scale")
+
+
+# ------------------------------------------------------------------- qgemm
+SHAPES = [
+    (1, 3072, 18432),    # AdaLN time_projection (skinny, M=1)
+    (1, 256, 3072),      # time_embedding.0
+    (3, 31, 13),         # tiny, K and N not multiples of anything
+    (17, 31, 13),        # tests/test_core.cpp shape
+    (20, 3072, 3072),    # skinny16..32
+    (64, 1024, 512),     # tests/test_core.cpp shape, skinny64
+    (65, 4096, 3072),    # text_embedding.0 K, first tiled size
+    (157, 3072, 3072),   # audio branch tokens
+    (192, 3072, 14336),  # video tokens at 256x256/9 frames, FFN up
+    (256, 3072, 3072),   # BASELINE cfg1
+    (300, 257, 129),     # ragged everything
+    (512, 3072, 3072),   # cross-attn K/V on ctx[512]
+    (768, 14336, 3072),  # cfg2 FFN down
+]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+def test_qgemm_bitexact(sdq_dev, oracle, M, K, N):
+    import sdq
+
+    A, q, s, bias = _inputs(M, K, N, seed=M + 3 * K + 7 * N)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A)
+    assert_bitexact(got, oracle.qgemm(A, q, s), f"qgemm {M}x{K}x{N}")
+    got_b = _run(sdq_dev, w, A, bias=bias)
+    assert_bitexact(got_b, oracle.linear(A, q, s, bias=bias), f"mlin {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(9, 200, 77), (130, 3072, 1000), (700, 512, 4096)])
+def test_accumulators_bitexact(sdq_dev, oracle, M, K, N):
+    import sdq
+
+    A, q, s, _ = _inputs(M, K, N, seed=5 * M + K)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A, kind="acc")
+    aq, _ = oracle.act_quant(A)
+    assert_bitexact(got, oracle.qgemm_acc(aq, q), "int32 acc")
+
+
+def test_golden_vectors_on_gpu(sdq_dev, oracle):
+    """The reference's golden qgemm inputs (gen_basic.py) and its compiled
+    outputs on the test_core shapes and special rows."""
+    import sdq
+
+    g = np.load(os.path.join(GOLDEN, "basic_golden.npz"))
+    w = sdq.Weight.from_host(g["qg_bq"], g["qg_bs"])
+    got = _run(sdq_dev, w, g["qg_a"])
+    assert_bitexact(got, oracle.qgemm(g["qg_a"], g["qg_bq"], g["qg_bs"]), "golden qg")
+    a = got.astype(np.float64).ravel()
+    b = g["qg_out"].astype(np.float64).ravel()
+    assert a @ b / np.sqrt((a @ a) * (b @ b)) > 0.999
+    r = np.load(os.path.join(GOLDEN, "ref_qgemm.npz"))
+    for (M, K, N) in [(17, 31, 13), (64, 1024, 512)]:
+        A = oracle.randu(M * K, 7 + M).reshape(M, K)
+        W = oracle.randu(N * K, 13 + N).reshape(N, K)
+        q, s = oracle.quantize_rowwise(W)
+        w = sdq.Weight.from_host(q, s)
+        assert_bitexact(_run(sdq_dev, w, A), r[f"core_{M}x{K}x{N}_out"], f"ref core {M}x{K}x{N}")
+    w = sdq.Weight.from_host(r["special_bq"], r["special_bs"])
+    assert_bitexact(_run(sdq_dev, w, r["special_a"]), r["special_out"], "ref special rows")
+
+
+def test_cfg1_matches_reference_hash(sdq_dev, oracle):
+    import hashlib
+
+    import sdq
+
+    r = np.load(os.path.join(GOLDEN, "ref_qgemm.npz"))
+    M, K, N = 256, 3072, 3072
+    A = oracle.randn(M * K, 1001).reshape(M, K)
+    W = oracle.randn(N * K, 1002).reshape(N, K) * np.float32(0.02)
+    q, s = oracle.quant_rows(W)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A)
+    assert hashlib.sha256(got.tobytes()).digest() == r["cfg1_sha256"].tobytes()
+
+
+def test_core_3072x5120x5120_matches_reference_hash(sdq_dev, oracle):
+    """The reference's --bench shape (tests/test_core.cpp:165-174)."""
+    import hashlib
+
+    import sdq
+
+    r = np.load(os.path.join(GOLDEN, "ref_qgemm.npz"))
+    M, K, N = 3072, 5120, 5120
+    A = oracle.randu(M * K, 7 + M).reshape(M, K)
+    W = oracle.randu(N * K, 13 + N).reshape(N, K)
+    q, s = oracle.quantize_rowwise(W)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A)
+    assert hashlib.sha256(got.tobytes()).digest() == r["core_3072x5120x5120_sha256"].tobytes()
+
+
+# ---------------------------------------------------------------- epilogues
+@pytest.mark.parametrize("M,K,N", [(40, 3072, 3072), (300, 1024, 3072), (5, 14336, 3072)])
+@pytest.mark.parametrize("fma", [True, False])
+def test_gated_residual_bitexact(sdq_dev, oracle, M, K, N, fma):
+    import sdq
+
+    A, q, s, bias = _inputs(M, K, N, seed=M + K + N)
+    gate = oracle.randn(N, 99)
+    x = oracle.randn(M * N, 98).reshape(M, N)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A, kind="gated", bias=bias, gate=gate, resid=x, gate_fma=fma)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x, use_fma=fma)
+    assert_bitexact(got, want, "gated")
+
+
+@pytest.mark.parametrize("M,K,N", [(40, 3072, 3072), (300, 1024, 3072)])
+def test_plain_residual_bitexact(sdq_dev, oracle, M, K, N):
+    import sdq
+
+    A, q, s, bias = _inputs(M, K, N, seed=2 * M + K)
+    x = oracle.randn(M * N, 97).reshape(M, N)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A, kind="resid", bias=bias, resid=x)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="resid", resid=x)
+    assert_bitexact(got, want, "resid")
+
+
+def test_gated_residual_in_place(sdq_dev, oracle):
+    """Y aliases resid: x <- fma(y, g, x) in place, as gated_add_inplace."""
+    import torch
+
+    import sdq
+
+    M, K, N = 300, 3072, 3072
+    A, q, s, bias = _inputs(M, K, N, seed=4242)
+    gate = oracle.randn(N, 1)
+    x = oracle.randn(M * N, 2).reshape(M, N)
+    w = sdq.Weight.from_host(q, s)
+    X = torch.from_numpy(x.copy()).to(sdq_dev)
+    sdq.qlinear(w, torch.from_numpy(A).to(sdq_dev), X, kind="gated",
+                bias=torch.from_numpy(bias).to(sdq_dev), gate=torch.from_numpy(gate).to(sdq_dev),
+                resid=X)
+    torch.cuda.synchronize()
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x)
+    assert_bitexact(X.cpu().numpy(), want, "in-place gated")
+
+
+@pytest.mark.parametrize("M,K,N", [(30, 3072, 14336), (200, 3072, 1000)])
+def test_gelu_epilogue_tolerance(sdq_dev, oracle, M, K, N):
+    """GELU uses the device tanhf; the reference uses libm tanh, so this one
+    is a tolerance check: max abs err <= 1e-6 * (1 + |y|)."""
+    import sdq
+
+    A, q, s, bias = _inputs(M, K, N, seed=M * 3 + N)
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A, kind="gelu", bias=bias)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gelu")
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-6 * (1.0 + np.abs(want))), float(err.max())
+    # the pre-activation is bit-exact, so the GELU input matches the oracle's
+    pre = _run(sdq_dev, w, A, kind="none", bias=bias)
+    assert_bitexact(pre, oracle.linear(A, q, s, bias=bias), "pre-gelu")
+
+
+def test_k_zero_and_m_zero(sdq_dev, oracle):
+    """K == 0 gives the reference's zero-filled out (+bias); M == 0 is a no-op."""
+    import torch
+
+    import sdq
+
+    N = 40
+    q = np.zeros((N, 0), np.int8)
+    s = np.ones(N, np.float32)
+    w = sdq.Weight.from_host(q, s)
+    A = np.zeros((5, 0), np.float32)
+    got = _run(sdq_dev, w, A)
+    assert_bitexact(got, np.zeros((5, N), np.float32), "K=0")
+    bias = oracle.randn(N, 3)
+    got = _run(sdq_dev, w, A, bias=bias)
+    assert_bitexact(got, np.broadcast_to(bias, (5, N)).astype(np.float32), "K=0 + bias")
+    w2 = sdq.Weight.from_host(np.ones((8, 16), np.int8), np.ones(8, np.float32))
+    Y = torch.full((0, 8), 1.0, device=sdq_dev)
+    sdq.qlinear(w2, torch.zeros((0, 16), device=sdq_dev), Y)
+
+
+def test_errors_are_reported(sdq_dev):
+    import torch
+
+    import sdq
+
+    w = sdq.Weight.from_host(np.ones((8, 16), np.int8), np.ones(8, np.float32))
+    A = torch.zeros((4, 15), device=sdq_dev)
+    Y = torch.zeros((4, 8), device=sdq_dev)
+    with pytest.raises(sdq.SdqError, match="K mismatch"):
+        sdq.qlinear(w, A, Y)
+    with pytest.raises(sdq.SdqError, match="GATED"):
+        sdq.qlinear(w, torch.zeros((4, 16), device=sdq_dev), Y, kind="gated")
+
+
+def test_host_pointer_entry_point(sdq_dev, oracle):
+    import sdq
+
+    M, K, N = 123, 3072, 640
+    A, q, s, bias = _inputs(M, K, N, seed=77)
+    w = sdq.Weight.from_host(q, s)
+    got = sdq.qlinear_host(w, A, bias=bias)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias), "host entry")
+    gate = oracle.randn(N, 5)
+    x = oracle.randn(M * N, 6).reshape(M, N)
+    got = sdq.qlinear_host(w, A, kind="gated", bias=bias, gate=gate, resid=x)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x),
+                    "host gated")
+
+
+def test_unaligned_and_strided_buffers(sdq_dev, oracle):
+    """A and Y at 4-byte (not 16-byte) aligned device addresses take the
+    scalar load/store paths and still match bit for bit."""
+    import torch
+
+    import sdq
+
+    M, K, N = 50, 1028, 516
+    A, q, s, bias = _inputs(M, K, N, seed=31)
+    w = sdq.Weight.from_host(q, s)
+    Abuf = torch.zeros(M * K + 1, device=sdq_dev)
+    Abuf[1:] = torch.from_numpy(A.ravel()).to(sdq_dev)
+    Ybuf = torch.zeros(M * N + 1, device=sdq_dev)
+    A_v = Abuf[1:].view(M, K)
+    Y_v = Ybuf[1:].view(M, N)
+    sdq.qlinear(w, A_v, Y_v, bias=torch.from_numpy(bias).to(sdq_dev))
+    torch.cuda.synchronize()
+    assert_bitexact(Y_v.cpu().numpy(), oracle.linear(A, q, s, bias=bias), "unaligned")
+
+
+def test_repeated_calls_and_streams(sdq_dev, oracle):
+    """Same result on a second stream and on repeated calls (workspace reuse)."""
+    import torch
+
+    import sdq
+
+    M, K, N = 400, 3072, 2048
+    A, q, s, _ = _inputs(M, K, N, seed=555)
+    w = sdq.Weight.from_host(q, s)
+    A_d = torch.from_numpy(A).to(sdq_dev)
+    want = oracle.qgemm(A, q, s)
+    st = torch.cuda.Stream()
+    outs = []
+    for i in range(3):
+        Y = torch.empty((M, N), device=sdq_dev)
+        with torch.cuda.stream(st if i == 1 else torch.cuda.current_stream()):
+            sdq.qgemm(w, A_d, Y)
+        torch.cuda.synchronize()
+        outs.append(Y.cpu().numpy())
+    for o in outs:
+        assert_bitexact(o, want, "repeat")

@@ -1,0 +1,185 @@
+"""The C++17 host mirror of the reference interface (sd::load_sdcpp,
+sd::qgemm, sd::gpu::QLinear), driven through lib/test_host.
+
+CPU tests: the .sdcpp v1 reader against our numpy writer (a restatement of
+tools/quantize/pack_sdcpp.py) and against the reference's own compiled
+loader, plus the error cases of tests/test_sdcpp.cpp:130-143.
+GPU tests: sd::qgemm and QLinear (built from a .sdcpp pack, as
+OviDit::load_impl does) bit-exact against the oracle."""
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import PKG, assert_bitexact
+
+BIN = os.path.join(PKG, "lib", "test_host")
+
+
+def run(*args, check=True):
+    r = subprocess.run([BIN, *map(str, args)], capture_output=True, text=True, timeout=300)
+    if check and r.returncode != 0:
+        raise AssertionError(f"test_host {args[0]} rc={r.returncode}\n{r.stdout}\n{r.stderr}")
+    return r
+
+
+def listing(path):
+    out = {}
+    for line in run("sdcpp", path).stdout.splitlines():
+        f = line.split()
+        name, code, nd = f[0], int(f[1]), int(f[2])
+        out[name] = dict(code=code, dims=[int(x) for x in f[3:3 + nd]], off=int(f[3 + nd]))
+    return out
+
+
+def make_pack(path, oracle):
+    rng = np.random.default_rng(0)
+    tensors = {
+        "blocks.0.ffn.0.weight": (rng.standard_normal((96, 700)) * 0.02).astype(np.float32),
+        "blocks.0.ffn.0.bias": (rng.standard_normal(96) * 0.01).astype(np.float32),
+        "tiny": rng.standard_normal(17).astype(np.float32),
+        "f32t": rng.standard_normal((5, 7)).astype(np.float32),
+        "blocks.0.self_attn.o.weight": (rng.standard_normal((200, 331)) * 0.02).astype(np.float32),
+        "blocks.0.self_attn.o.bias": (rng.standard_normal(200) * 0.01).astype(np.float32),
+    }
+    written = oracle.write_sdcpp(path, tensors)
+    return tensors, written
+
+
+def test_sdcpp_listing_matches_format(tmp_path, oracle):
+    p = str(tmp_path / "a.sdcpp")
+    tensors, written = make_pack(p, oracle)
+    got = listing(p)
+    # 2 quantized (+2 scale views) and 4 raw
+    assert set(got) == set(tensors) | {"blocks.0.ffn.0.weight.scale",
+                                       "blocks.0.self_attn.o.weight.scale"}
+    raw = open(p, "rb").read()
+    for name, (code, a, s) in written.items():
+        e = got[name]
+        assert e["dims"] == list(tensors[name].shape)
+        if code == 0:
+            assert e["code"] == 2  # DType::I8
+            n = a.size
+            assert raw[e["off"]:e["off"] + n] == a.tobytes()
+            sc = got[name + ".scale"]
+            assert sc["off"] == e["off"] + n          # scales right after the int8 blob
+            assert raw[sc["off"]:sc["off"] + 4 * s.size] == s.tobytes()
+        else:
+            assert e["code"] == 0  # DType::F32
+            assert raw[e["off"]:e["off"] + a.nbytes] == a.tobytes()
+
+
+def test_sdcpp_reader_agrees_with_reference_loader(tmp_path, oracle, ref):
+    p = str(tmp_path / "b.sdcpp")
+    tensors, _ = make_pack(p, oracle)
+    got = listing(p)
+    for name in tensors:
+        r = ref.sdcpp_lookup(p, name)
+        assert r["dims"] == got[name]["dims"]
+        assert r["data_off"] == got[name]["off"]
+        assert r["dtype"] == got[name]["code"]
+        if r["scale_off"] >= 0:
+            assert r["scale_off"] == got[name + ".scale"]["off"]
+        assert r["count"] == len(got)
+
+
+def _corrupt(tmp_path, oracle, fn, tag):
+    p = str(tmp_path / "c.sdcpp")
+    make_pack(p, oracle)
+    data = bytearray(open(p, "rb").read())
+    data = fn(data)
+    q = str(tmp_path / f"{tag}.sdcpp")
+    open(q, "wb").write(bytes(data))
+    return q
+
+
+@pytest.mark.parametrize("tag,fn,msg", [
+    ("trunc", lambda d: d[:-64], "data out of bounds"),
+    ("magic", lambda d: bytearray(b"X") + d[1:], "bad magic"),
+    ("version", lambda d: d[:4] + struct.pack("<I", 2) + d[8:], "unsupported version"),
+    ("short", lambda d: d[:15], "truncated"),
+    ("hdr", lambda d: d[:40], "truncated"),
+])
+def test_sdcpp_errors(tmp_path, oracle, tag, fn, msg):
+    q = _corrupt(tmp_path, oracle, fn, tag)
+    r = run("sdcpp_err", q, check=False)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.startswith("sdcpp: ") and msg in r.stdout
+
+
+def test_sdcpp_missing_file(tmp_path):
+    r = run("sdcpp_err", tmp_path / "nope.sdcpp", check=False)
+    assert r.returncode == 0 and "cannot open" in r.stdout
+
+
+def test_sdcpp_bad_dtype_code(tmp_path, oracle):
+    p = str(tmp_path / "d.sdcpp")
+    oracle.write_sdcpp(p, {"x": np.zeros(4, np.float32)})
+    data = bytearray(open(p, "rb").read())
+    # header: magic(4) ver(4) count(4) name_len(4) name(1) code(1)
+    data[17] = 7
+    open(p, "wb").write(bytes(data))
+    r = run("sdcpp_err", p, check=False)
+    assert r.returncode == 0 and "bad dtype code" in r.stdout
+
+
+def test_linear_from_pack_checks(tmp_path, oracle):
+    p = str(tmp_path / "e.sdcpp")
+    make_pack(p, oracle)
+    r = run("linear_err", p, "blocks.0.ffn.0", 700, 95, check=False)
+    assert r.returncode == 0 and "bad shape" in r.stdout
+    r = run("linear_err", p, "blocks.9.ffn.0", 700, 96, check=False)
+    assert r.returncode == 0 and "missing tensor" in r.stdout
+    # a raw f32 weight (small tensor) is not an int8 pack entry
+    oracle.write_sdcpp(p, {"l.weight": np.zeros((4, 8), np.float32),
+                           "l.bias": np.zeros(4, np.float32)})
+    r = run("linear_err", p, "l", 8, 4, check=False)
+    assert r.returncode == 0 and "not an int8" in r.stdout
+
+
+# ------------------------------------------------------------------ GPU
+@pytest.mark.gpu
+def test_sd_qgemm_host_tensor_api(tmp_path, sdq_dev, oracle):
+    M, K, N = 77, 1000, 300
+    A = oracle.randn(M * K, 1).reshape(M, K)
+    W = oracle.randn(N * K, 2).reshape(N, K) * np.float32(0.02)
+    q, s = oracle.quant_rows(W)
+    for nm, arr in (("A", A), ("q", q), ("s", s)):
+        arr.tofile(tmp_path / f"{nm}.bin")
+    r = run("qgemm", M, K, N, tmp_path / "A.bin", tmp_path / "q.bin", tmp_path / "s.bin",
+            tmp_path / "o.bin")
+    assert "cache entries 1" in r.stdout
+    got = np.fromfile(tmp_path / "o.bin", np.float32).reshape(M, N)
+    assert_bitexact(got, oracle.qgemm(A, q, s), "sd::qgemm")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["mlin", "gelu", "gated", "add"])
+def test_qlinear_from_pack(tmp_path, sdq_dev, oracle, mode):
+    p = str(tmp_path / "f.sdcpp")
+    tensors, written = make_pack(p, oracle)
+    base, K, N = "blocks.0.self_attn.o", 331, 200
+    _, q, s = written[base + ".weight"]
+    bias = tensors[base + ".bias"]
+    M = 45
+    x = oracle.randn(M * K, 3).reshape(M, K)
+    g = oracle.randn(N, 4)
+    res = oracle.randn(M * N, 5).reshape(M, N)
+    x.tofile(tmp_path / "x.bin")
+    g.tofile(tmp_path / "g.bin")
+    res.tofile(tmp_path / "r.bin")
+    run("linear", p, base, K, N, M, mode, tmp_path / "x.bin", tmp_path / "g.bin",
+        tmp_path / "r.bin", tmp_path / "o.bin")
+    got = np.fromfile(tmp_path / "o.bin", np.float32).reshape(M, N)
+    if mode == "mlin":
+        assert_bitexact(got, oracle.linear(x, q, s, bias=bias), mode)
+    elif mode == "gated":
+        assert_bitexact(got, oracle.linear(x, q, s, bias=bias, epilogue="gated", gate=g,
+                                           resid=res), mode)
+    elif mode == "add":
+        assert_bitexact(got, oracle.linear(x, q, s, bias=bias, epilogue="resid", resid=res), mode)
+    else:
+        want = oracle.linear(x, q, s, bias=bias, epilogue="gelu")
+        assert np.all(np.abs(got - want) <= 1e-6 * (1 + np.abs(want)))
