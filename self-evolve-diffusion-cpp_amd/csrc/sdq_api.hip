@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -23,7 +24,7 @@
 struct sdq_weight {
   int device;
   int64_t N, K, Np, KFp;
-  int8_t* frags;  // (Np/16) * KFp * 1024 bytes
+  int8_t* frags;  // (Np/32) * KFp * 1024 bytes
   float* scale;   // Np floats, zero padded
 };
 
@@ -36,6 +37,7 @@ thread_local std::string t_err;
 struct DevState {
   bool ready = false;
   int cu_count = 0;
+  int stagger = 4;  // tile phases per XCD in the persistent GEMM (SDQ_STAGGER)
   hipDeviceProp_t prop{};
 };
 
@@ -44,10 +46,15 @@ std::mutex g_mu;
 DevState g_dev[kMaxDev];
 
 struct Workspace {
-  int8_t* at = nullptr;
+  int8_t* at = nullptr;  // quantized activations, fragment layout
   size_t at_bytes = 0;
-  float* as = nullptr;
+  float* as = nullptr;   // per-row activation scales
   size_t as_bytes = 0;
+  float* cols = nullptr;  // [2][col_cap]: zero-padded bias, gate copies
+  size_t col_cap = 0;
+  float* sink = nullptr;  // 1 KB target of masked epilogue stores
+  void* partials = nullptr;  // staggered-tile partial sums, one slot per workgroup
+  size_t partials_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -88,6 +95,10 @@ int ensure_device(int dev) {
     return set_error(SDQ_ERR_NODEV, std::string("sdq kernels are built for gfx950, device is ") +
                                         d.prop.gcnArchName);
   d.cu_count = d.prop.multiProcessorCount;
+  if (const char* st = std::getenv("SDQ_STAGGER")) {
+    const int v = std::atoi(st);
+    if (v >= 1 && v <= 64) d.stagger = v;
+  }
   d.ready = true;
   return SDQ_OK;
 }
@@ -95,36 +106,41 @@ int ensure_device(int dev) {
 // Grows (never shrinks) the workspace of (dev, stream). A buffer that is
 // replaced may still be read by work queued on `stream`, so the stream is
 // drained before the old buffer is freed.
-int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, Workspace** out) {
+int grow(hipStream_t s, void** p, size_t* have, size_t need) {
+  if (*have >= need) return SDQ_OK;
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  if (*p) (void)hipFree(*p);
+  *p = nullptr;
+  *have = 0;
+  e = hipMalloc(p, need);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(SDQ_ERR_NOMEM, "workspace allocation of " + std::to_string(need) +
+                                        " bytes failed");
+  }
+  *have = need;
+  return SDQ_OK;
+}
+
+int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t col_cap,
+              Workspace** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace& w = g_ws[{dev, s}];
-  if (w.at_bytes < at_bytes || w.as_bytes < as_bytes) {
-    hipError_t e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
-    if (w.at_bytes < at_bytes) {
-      if (w.at) (void)hipFree(w.at);
-      w.at = nullptr;
-      w.at_bytes = 0;
-      e = hipMalloc(&w.at, at_bytes);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return set_error(SDQ_ERR_NOMEM, "workspace allocation of " + std::to_string(at_bytes) +
-                                            " bytes failed");
-      }
-      w.at_bytes = at_bytes;
-    }
-    if (w.as_bytes < as_bytes) {
-      if (w.as) (void)hipFree(w.as);
-      w.as = nullptr;
-      w.as_bytes = 0;
-      e = hipMalloc(&w.as, as_bytes);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return set_error(SDQ_ERR_NOMEM, "workspace allocation failed");
-      }
-      w.as_bytes = as_bytes;
-    }
+  int rc = grow(s, reinterpret_cast<void**>(&w.at), &w.at_bytes, at_bytes);
+  if (!rc) rc = grow(s, reinterpret_cast<void**>(&w.as), &w.as_bytes, as_bytes);
+  size_t cb = w.col_cap * 2 * sizeof(float);
+  if (!rc && cb < col_cap * 2 * sizeof(float)) {
+    rc = grow(s, reinterpret_cast<void**>(&w.cols), &cb, col_cap * 2 * sizeof(float));
+    if (!rc) w.col_cap = col_cap;
   }
+  if (!rc && !w.sink) {
+    size_t have = 0;
+    rc = grow(s, reinterpret_cast<void**>(&w.sink), &have, 4096);
+  }
+  // one 256x256 int32 tile per resident workgroup of the persistent GEMM
+  if (!rc) rc = grow(s, &w.partials, &w.partials_bytes, (size_t)g_dev[dev].cu_count * 256 * 256 * 4);
+  if (rc) return rc;
   *out = &w;
   return SDQ_OK;
 }
@@ -147,7 +163,7 @@ int alloc_weight(int dev, int64_t N, int64_t K, sdq_weight** out) {
   if (N < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative weight dims");
   const int64_t Np = round_up(N < 1 ? 1 : N, kRowAlign);
   const int64_t KFp = kfrags_padded(K);
-  const int64_t bytes = (Np / 16) * KFp * kFragBytes;
+  const int64_t bytes = (Np / kFragRows) * KFp * kFragBytes;
   if (bytes >= (int64_t(1) << 40)) return set_error(SDQ_ERR_INVALID, "weight too large");
   sdq_weight* w = new (std::nothrow) sdq_weight{dev, N, K, Np, KFp, nullptr, nullptr};
   if (!w) return set_error(SDQ_ERR_NOMEM, "host allocation failed");
@@ -222,20 +238,31 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
 
   const int cfg = choose_gemm_cfg(M, N, g_dev[w->device].cu_count);
   const int64_t Mp = round_up(M, gemm_cfg_bm(cfg));
-  const size_t at_bytes = (size_t)(Mp / 16) * (size_t)w->KFp * kFragBytes;
+  const size_t at_bytes = (size_t)(Mp / kFragRows) * (size_t)w->KFp * kFragBytes;
+  const size_t col_cap = (size_t)(w->Np + kColPad);
   Workspace* ws = nullptr;
-  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), &ws))) return rc;
+  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap, &ws))) return rc;
+  const EpiArgs ea = make_epi(epi, K);
+  ColCopy cc{};
+  cc.bias = ea.bias;
+  cc.gate = ea.gate;
+  cc.bias_pad = ea.bias ? ws->cols : nullptr;
+  cc.gate_pad = ea.gate ? ws->cols + ws->col_cap : nullptr;
+  cc.N = N;
+  cc.CP = (int64_t)col_cap;
 
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, s);
+  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, s);
   if (e != hipSuccess) return hip_error(e, "act_quant launch");
   hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
-  const EpiArgs ea = make_epi(epi, K);
   int vec = (N % 4 == 0) && aligned16(Y);
   if (ea.bias) vec = vec && aligned16(ea.bias);
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
-  e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, s);
+  GemmAux aux{cc.bias_pad,    cc.gate_pad,          ws->sink,
+              ws->partials,   ws->partials_bytes,   g_dev[w->device].stagger,
+              g_dev[w->device].cu_count};
+  e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) return hip_error(e, "qgemm launch");
   if (t_prof) {
     hipEvent_t p2 = prof_mark(s);

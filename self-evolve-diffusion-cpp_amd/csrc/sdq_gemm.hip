@@ -10,18 +10,34 @@
 // result is bit-identical to the reference CPU path.
 //
 // MFMA roles: the WEIGHT fragment is the instruction's A operand (rows = n)
-// and the ACTIVATION fragment its B operand (columns = m), so the 16x16 i32
-// result C^T[n][m] lands as 4 consecutive n of one m per lane: lane l holds
-// n = 4(l>>4) + r (r = 0..3), m = l & 15, i.e. a 16-byte row-contiguous
-// store of Y[m, n..n+3].
+// and the ACTIVATION fragment its B operand (columns = m), so the 32x32 i32
+// result C^T[n][m] of v_mfma_i32_32x32x32_i8 lands as groups of 4
+// consecutive n of one m per lane: lane l, accumulator register r holds
+// m = l & 31, n = 8(r >> 2) + 4(l >> 5) + (r & 3), i.e. four 16-byte
+// row-contiguous stores of Y[m, n..n+3] per 32x32 block.
 #include "sdq_internal.h"
 
 #pragma clang fp contract(off)
 
 namespace sdq {
+
+// Per-column operands of the persistent kernel, read by LDS-DMA.
+struct ColOps {
+  const float* scale;  // [>= tiles_n*BN + 256] zero padded
+  const float* bias;   // same size, or nullptr
+  const float* gate;   // same size, or nullptr
+};
+
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] at [15:14]; the other counters are left at their maximum).
+constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
 
 __device__ __forceinline__ float gelu_tanh(float v) {
   // nn.GELU(approximate='tanh'), src/model/ovi_dit.cpp:132-142.
@@ -40,8 +56,8 @@ __device__ __forceinline__ void load4(const float* __restrict__ p, int64_t n0, i
   }
 }
 
-// Epilogue for acc = C^T[n0..n0+3][m] of one lane.
-__device__ __forceinline__ void store_out(const v4i acc, int64_t m, int64_t n0, int64_t M,
+// Epilogue for the accumulators of Y[m, n0..n0+3] held by one lane.
+__device__ __forceinline__ void store_out(const int acc[4], int64_t m, int64_t n0, int64_t M,
                                           int64_t N, float as_m, const float* __restrict__ bs,
                                           const EpiArgs& e, void* Y, bool vec) {
   if (m >= M || n0 >= N) return;
@@ -106,25 +122,103 @@ __device__ __forceinline__ void store_out(const v4i acc, int64_t m, int64_t n0, 
   }
 }
 
+// Stores one 32x32 accumulator block: n_lane = n of this lane's group 0.
+__device__ __forceinline__ void store_block(const v16i& acc, int64_t m, int64_t n_lane, int64_t M,
+                                            int64_t N, float as_m, const float* __restrict__ bs,
+                                            const EpiArgs& e, void* Y, bool vec) {
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int a4[4] = {acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+    store_out(a4, m, n_lane + 8 * g, M, N, as_m, bs, e, Y, vec);
+  }
+}
+
+// Epilogue of Y[m, n0..n0+3] with the per-column operands already in
+// registers (weight scale s4, bias b4, gate g4); only the residual, when the
+// epilogue has one, is read from global memory here.
+__device__ __forceinline__ void finish4(const int* acc, int64_t m, int64_t n0, int64_t M, int64_t N,
+                                        float as_m, const float4 s4, const float4 b4,
+                                        const float4 g4, const EpiArgs& e, void* Y, bool vec) {
+  if (m >= M || n0 >= N) return;
+  const int64_t o = m * N + n0;
+  if (e.kind == SDQ_EPI_ACC) {
+    int* y = static_cast<int*>(Y) + o;
+    if (vec) {
+      *reinterpret_cast<int4*>(y) = make_int4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (n0 + r < N) y[r] = acc[r];
+    }
+    return;
+  }
+  const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+  const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+  const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float s = as_m * sv[r];
+    const float a = (float)acc[r];
+    v[r] = e.kzero ? 0.f : a * s;
+  }
+  if (e.bias) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
+  }
+  if (e.kind == SDQ_EPI_GELU) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
+  } else if (e.kind == SDQ_EPI_GATED || e.kind == SDQ_EPI_RESID) {
+    float x[4];
+    load4(e.resid + m * N, n0, N, vec, x);
+    if (e.kind == SDQ_EPI_RESID) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
+    } else if (e.gate_fma) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = __builtin_fmaf(v[r], gv[r], x[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float p = v[r] * gv[r];
+        v[r] = x[r] + p;
+      }
+    }
+  }
+  float* y = static_cast<float*>(Y) + o;
+  if (vec) {
+    *reinterpret_cast<float4*>(y) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if (n0 + r < N) y[r] = v[r];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Tiled kernel: one workgroup computes a BN (weight rows) x BM (activation
-// rows) output tile. Each stage moves KS k-fragments of both panels
-// global -> LDS with direct-to-LDS 16-byte loads (no VGPR staging), double
-// buffered; WN x WM waves each own FN x FM 16x16 accumulator fragments.
-template <int BN, int BM, int WN, int WM, int KS>
+// rows) output tile. Each pipeline stage moves KS k-fragments (32 bytes of K
+// each) of both panels global -> LDS with direct-to-LDS 16-byte loads (no
+// VGPR staging) into a ring of STAGES buffers; STAGES-1 stages are in
+// flight while one is consumed, and each wave waits only for its own oldest
+// stage (vmcnt) before the workgroup barrier. WN x WM waves each own
+// FN x FM 32x32 accumulator blocks.
+template <int BN, int BM, int WN, int WM, int KS, int STAGES>
 __global__ void __launch_bounds__(WN* WM * 64, 1)
 qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
             const int8_t* __restrict__ at, const float* __restrict__ as, int64_t M, int64_t N,
             int64_t KFp, int tiles_n, int tiles_m, EpiArgs epi, void* Y, int vec) {
   constexpr int NW = WN * WM;
-  constexpr int RBN = BN / 16, RBM = BM / 16;
+  constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
   constexpr int WFR = RBN * KS, AFR = RBM * KS, SFR = WFR + AFR;
-  constexpr int WLD = WFR / NW, ALD = AFR / NW;  // load instructions per wave per stage
+  constexpr int WLD = WFR / NW, ALD = AFR / NW, LPW = WLD + ALD;
   constexpr int STAGE = SFR * 1024;
   static_assert(WFR % NW == 0 && AFR % NW == 0, "stage fragments must split evenly over waves");
   static_assert(NW % KS == 0, "waves must be a multiple of k-fragments per stage");
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
 
   const int lane = threadIdx.x & 63;
   // Wave index as a scalar: keeps every per-wave offset in SGPRs.
@@ -147,24 +241,42 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
   const int tm = first_m + rem % gsz;
   const int tn = rem / gsz;
 
-  // ---- per-lane global offsets of this wave's loads (stage 0).
-  // Stage fragment f = t*NW + w; W fragments first, then activation ones.
-  // With NW % KS == 0 the k index of all of a wave's fragments is w % KS and
-  // the row block advances by NW/KS per t.
+  // ---- per-column epilogue operands of this tile (weight scale, bias,
+  // gate) staged in LDS and per-row activation scales in registers, so the
+  // epilogue does not wait on global loads. Visible to all waves after the
+  // first pipeline barrier.
+  __shared__ __attribute__((aligned(16))) float col_ops[3][BN];
+  for (int t = threadIdx.x; t < BN; t += NW * 64) {
+    const int64_t n = (int64_t)tn * BN + t;  // < Np: bs is zero padded
+    col_ops[0][t] = bs[n];
+    col_ops[1][t] = (epi.bias && n < N) ? epi.bias[n] : 0.f;
+    col_ops[2][t] = (epi.gate && n < N) ? epi.gate[n] : 0.f;
+  }
+  float as_reg[FM];
+#pragma unroll
+  for (int j = 0; j < FM; j++) {
+    const int64_t m = (int64_t)tm * BM + (wm * FM + j) * 32 + (lane & 31);
+    as_reg[j] = (m < M) ? as[m] : 0.f;
+  }
+
+  // ---- per-wave global offsets (stage 0). Stage fragment f = t*NW + w,
+  // weight fragments first; with NW % KS == 0 all of a wave's fragments sit
+  // at k index w % KS and the row block advances by NW/KS per t.
   const uint32_t lane_off = (uint32_t)lane * 16u;
   const int64_t wbase = ((int64_t)(tn * RBN + w / KS) * KFp + (w % KS)) * 1024;
   const int64_t abase = ((int64_t)(tm * RBM + w / KS) * KFp + (w % KS)) * 1024;
   const int64_t tstride = (int64_t)(NW / KS) * KFp * 1024;
 
-  v4i acc[FN][FM];
+  v16i acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; i++)
 #pragma unroll
-    for (int j = 0; j < FM; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < FM; j++) acc[i][j] = v16i{};
 
   const int nks = (int)(KFp / KS);
 
-  auto issue = [&](int ks, char* buf) {
+  auto issue = [&](int ks) {
+    char* buf = lds + (ks % STAGES) * STAGE;
     const int64_t koff = (int64_t)ks * KS * 1024;
 #pragma unroll
     for (int t = 0; t < WLD; t++) {
@@ -178,48 +290,408 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
                                        0, 0);
     }
   };
-
-  issue(0, lds);
-  for (int ks = 0; ks < nks; ks++) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (ks + 1 < nks) issue(ks + 1, lds + ((ks + 1) & 1) * STAGE);
-    const char* cb = lds + (ks & 1) * STAGE;
+  // Operand fragments of one stage, double buffered in registers.
+  struct Frags {
+    v4i a[KS][FN], b[KS][FM];
+  };
+  auto lds_read = [&](int ks, Frags& f) {
+    const char* cb = lds + (ks % STAGES) * STAGE;
 #pragma unroll
     for (int kk = 0; kk < KS; kk++) {
-      v4i a[FN], b[FM];
 #pragma unroll
       for (int i = 0; i < FN; i++)
-        a[i] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + i) * KS + kk) * 1024 + lane_off);
+        f.a[kk][i] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + i) * KS + kk) * 1024 + lane_off);
 #pragma unroll
       for (int j = 0; j < FM; j++)
-        b[j] = *reinterpret_cast<const v4i*>(cb + WFR * 1024 + ((wm * FM + j) * KS + kk) * 1024 +
-                                             lane_off);
-#pragma unroll
-      for (int i = 0; i < FN; i++)
-#pragma unroll
-        for (int j = 0; j < FM; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        f.b[kk][j] = *reinterpret_cast<const v4i*>(cb + WFR * 1024 +
+                                                   ((wm * FM + j) * KS + kk) * 1024 + lane_off);
     }
+  };
+  auto mma = [&](const Frags& f, int kk) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[kk][i], f.b[kk][j], acc[i][j], 0, 0, 0);
+  };
+  // Waits until this wave's loads of stage `next` have landed (later stages
+  // may stay in flight), then syncs the workgroup.
+  auto wait_and_sync = [&](int next) {
+    if (next + STAGES - 2 < nks)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("s_barrier" ::: "memory");
+  };
+  // One pipeline step: MFMAs of stage ks from `cur` (first k-fragment, then
+  // the rest), with the barrier for stage ks+1, the refill of the buffer
+  // that stage ks occupied, and the LDS reads of stage ks+1 into `nxt`
+  // placed between them so the MFMA pipe stays busy across the barrier and
+  // the LDS latency.
+  auto step = [&](int ks, const Frags& cur, Frags& nxt) {
+    mma(cur, 0);
+    if (ks + 1 < nks) {
+      wait_and_sync(ks + 1);
+      if (ks + STAGES < nks) issue(ks + STAGES);
+      lds_read(ks + 1, nxt);
+    }
+#pragma unroll
+    for (int kk = 1; kk < KS; kk++) mma(cur, kk);
+  };
+
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES; s0++)
+    if (s0 < nks) issue(s0);
+  if (STAGES - 1 < nks)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
+  else
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  asm volatile("s_barrier" ::: "memory");
+  Frags f0, f1;
+  lds_read(0, f0);
+  int ks = 0;
+  for (; ks + 1 < nks; ks += 2) {
+    step(ks, f0, f1);
+    step(ks + 1, f1, f0);
   }
+  if (ks < nks) step(ks, f0, f1);
 
   // ---- epilogue
-  const int64_t mb = (int64_t)tm * BM + wm * FM * 16 + (lane & 15);
-  const int64_t nb = (int64_t)tn * BN + wn * FN * 16 + (lane >> 4) * 4;
+  const int64_t mb = (int64_t)tm * BM + wm * FM * 32 + (lane & 31);
+  const int nl0 = wn * FN * 32 + (lane >> 5) * 4;
 #pragma unroll
-  for (int j = 0; j < FM; j++) {
-    const int64_t m = mb + j * 16;
-    const float as_m = (m < M) ? as[m] : 0.f;
+  for (int i = 0; i < FN; i++) {
 #pragma unroll
-    for (int i = 0; i < FN; i++) store_out(acc[i][j], m, nb + i * 16, M, N, as_m, bs, epi, Y, vec);
+    for (int g = 0; g < 4; g++) {
+      const int nl = nl0 + i * 32 + 8 * g;
+      const float4 s4 = *reinterpret_cast<const float4*>(&col_ops[0][nl]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&col_ops[1][nl]);
+      const float4 g4 = *reinterpret_cast<const float4*>(&col_ops[2][nl]);
+      const int64_t n0 = (int64_t)tn * BN + nl;
+#pragma unroll
+      for (int j = 0; j < FM; j++) {
+        const int a4[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                           acc[i][j][4 * g + 3]};
+        finish4(a4, mb + j * 32, n0, M, N, as_reg[j], s4, b4, g4, epi, Y, vec);
+      }
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (M <= 16*FMS): one workgroup per 16 weight rows; its SPLIT
+// Persistent tiled kernel (the main path; needs 16-byte vector epilogue
+// access). gridDim.x workgroups walk the tile list with stride gridDim.x,
+// and the LDS pipeline runs straight across tile boundaries: the next
+// tile's first STAGES stages are prefetched while the current tile's last
+// stages compute, so the epilogue of one tile overlaps the loads of the
+// next. On this GPU family one counter (vmcnt) tracks loads and stores and
+// a store may complete before an older load, so after an epilogue the
+// first wait drains everything (vmcnt(0)); later waits count loads only.
+// Per-tile weight scales, bias, gate and activation scales arrive by
+// LDS-DMA into a double buffer alongside stage 0.
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int EPI>
+__global__ void __launch_bounds__(WN* WM * 64, 1)
+qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
+              const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
+              int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger) {
+  constexpr int NW = WN * WM;
+  constexpr int RBN = BN / 32, RBM = BM / 32;
+  constexpr int FN = RBN / WN, FM = RBM / WM;
+  constexpr int WFR = RBN * KS, AFR = RBM * KS, SFR = WFR + AFR;
+  constexpr int WLD = WFR / NW, ALD = AFR / NW, LPW = WLD + ALD;
+  constexpr int STAGE = SFR * 1024;
+  static_assert(WFR % NW == 0 && AFR % NW == 0, "stage fragments must split evenly over waves");
+  static_assert(NW % KS == 0, "waves must be a multiple of k-fragments per stage");
+  static_assert(NW >= 4, "four waves load the per-tile operands");
+  static_assert((STAGES - 1) * LPW < 64, "vmcnt range");
+  static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
+  __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
+  __shared__ __attribute__((aligned(16))) float rowb[2][BM];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = w % WN, wm = w / WN;
+  const uint32_t lane_off = (uint32_t)lane * 16u;
+
+  const int T = tiles_n * tiles_m;
+  const int G = gridDim.x;
+  const int ntile = (T - (int)blockIdx.x + G - 1) / G;
+  const int nks = (int)(KFp / KS);
+  const int total = ntile * nks;
+
+  // Tile i of this workgroup -> (tm, tn): the XCD-aware grouped order used
+  // by the non-persistent kernel, applied to the virtual block id
+  // blockIdx.x + i*G (G is a multiple of 8, so it stays on this XCD).
+  auto coords = [&](int i, int& tm, int& tn) {
+    const int bid = (int)blockIdx.x + i * G;
+    const int xcd = bid & 7, jx = bid >> 3, q8 = T >> 3, r8 = T & 7;
+    const int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + jx;
+    constexpr int GROUP_M = 8;
+    const int per_group = GROUP_M * tiles_n;
+    const int g = lin / per_group;
+    const int first_m = g * GROUP_M;
+    const int gsz = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+    const int rem = lin - g * per_group;
+    tm = first_m + rem % gsz;
+    tn = rem / gsz;
+  };
+
+  // ---- work segments. Tiles finishing in lockstep on all CUs of an XCD
+  // would push their stores through the XCD's memory path in one burst, so
+  // workgroups are staggered: workgroup b starts its first tile at stage s0
+  // (a per-CU phase within the XCD), saves that tile's partial int32
+  // accumulators to its own scratch slot, runs its other tiles whole, and
+  // finishes the first tile's stages [0, s0) last, adding the saved
+  // partial back (integer addition: exact). Segment j covers tile tseg(j),
+  // stages [kbeg(j), kend(j)).
+  int s0 = 0;
+  if (ntile > 1 && stagger > 1) {
+    const int phase = ((int)blockIdx.x >> 3) % stagger;
+    s0 = ((phase * nks / stagger) / 2) * 2;  // even: stages run in pairs
+  }
+  const int nseg = s0 > 0 ? ntile + 1 : ntile;
+  auto tseg = [&](int j) { return (s0 > 0 && j == ntile) ? 0 : j; };
+  auto kbeg = [&](int j) { return j == 0 ? s0 : 0; };
+  auto kend = [&](int j) { return (s0 > 0 && j == ntile) ? s0 : nks; };
+
+  // ---- issue cursor: the next stage to load (segment cj, stage cks), with
+  // buffer descriptors over that tile's weight / activation panels (raw
+  // buffers: out-of-range reads return 0) so every load is one SGPR
+  // descriptor + SGPR offset + the lane's 16-byte VGPR offset.
+  constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, valid
+  const int64_t wpanel = (int64_t)RBN * KFp * 1024, apanel = (int64_t)RBM * KFp * 1024;
+  int cj = 0, cks = s0, cend = kend(0), ctm = 0, ctn = 0, cgs = 0;
+  __amdgpu_buffer_rsrc_t wr, ar;
+  auto set_tile = [&](int i) {
+    coords(i, ctm, ctn);
+    wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(wt) + (int64_t)ctn * wpanel, (short)0, (int)wpanel, kRsrcWord3);
+    ar = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(at) + (int64_t)ctm * apanel, (short)0, (int)apanel, kRsrcWord3);
+  };
+  set_tile(tseg(0));
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  auto dma_row = [&](const float* src, int64_t off, int count, float* dst) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(src) + off, (short)0, count * 4, kRsrcWord3);
+    if (lane * 4 < count)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, lane_off, 0, 0, 0);
+  };
+  // Loads the next stage in issue order (global stage cgs).
+  auto issue = [&]() {
+    const int par = cj & 1;
+    if (cks == kbeg(cj)) {
+      if (w < 3) {
+        const float* src = w == 0 ? cols.scale : (w == 1 ? cols.bias : cols.gate);
+        if (src) dma_row(src, (int64_t)ctn * BN, BN, &colb[par][w][0]);
+      } else if (w == 3) {
+        dma_row(as, (int64_t)ctm * BM, BM, &rowb[par][0]);
+      }
+    }
+    char* buf = lds + (cgs % STAGES) * STAGE;
+    const int kb = cks * KS + (w % KS);
+    const int wso = ((w / KS) * (int)KFp + kb) * 1024;
+    const int tso = (NW / KS) * (int)KFp * 1024;
+#pragma unroll
+    for (int t = 0; t < WLD; t++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(buf + (t * NW + w) * 1024), 16,
+                                               lane_off, wso + t * tso, 0, 0);
+#pragma unroll
+    for (int t = 0; t < ALD; t++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ar, (lds_ptr_t)(buf + WFR * 1024 + (t * NW + w) * 1024), 16, lane_off, wso + t * tso, 0,
+          0);
+    cgs++;
+    if (++cks == cend) {
+      if (++cj < nseg) {
+        cks = kbeg(cj);
+        cend = kend(cj);
+        set_tile(tseg(cj));
+      }
+    }
+  };
+
+  struct Frags {
+    v4i a[KS][FN], b[KS][FM];
+  };
+  auto lds_read = [&](int gs, Frags& f) {
+    const char* cb = lds + (gs % STAGES) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < KS; kk++) {
+#pragma unroll
+      for (int i = 0; i < FN; i++)
+        f.a[kk][i] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + i) * KS + kk) * 1024 + lane_off);
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+        f.b[kk][j] = *reinterpret_cast<const v4i*>(cb + WFR * 1024 +
+                                                   ((wm * FM + j) * KS + kk) * 1024 + lane_off);
+    }
+  };
+  v16i acc[FN][FM];
+  auto mma = [&](const Frags& f, int kk) {
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+      for (int j = 0; j < FM; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[kk][i], f.b[kk][j], acc[i][j], 0, 0, 0);
+  };
+  // Waits until this wave's loads of stage `next` have landed: at most the
+  // loads of the STAGES-2 later stages may be outstanding. Stores do not
+  // enter the count; a pending store only makes the wait longer.
+  auto wait_and_sync = [&](int next) {
+    if (next + STAGES - 2 < total)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("s_barrier" ::: "memory");
+  };
+  // One pipeline step: MFMAs of stage gs from `cur`, with the barrier for
+  // stage gs+1, the refill of the buffer stage gs occupied and (if `read`)
+  // the LDS reads of stage gs+1 into `nxt` placed between its k-fragments.
+  auto step = [&](int gs, const Frags& cur, Frags& nxt, bool read) {
+    mma(cur, 0);
+    if (gs + 1 < total) {
+      wait_and_sync(gs + 1);
+      if (gs + STAGES < total) issue();
+      if (read) lds_read(gs + 1, nxt);
+    }
+#pragma unroll
+    for (int kk = 1; kk < KS; kk++) mma(cur, kk);
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES; s++)
+    if (s < total) issue();
+  if (STAGES - 1 < total)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
+  else
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  asm volatile("s_barrier" ::: "memory");
+  Frags f0, f1;
+  lds_read(0, f0);
+
+  // Epilogue memory goes through buffer descriptors too: masked lanes
+  // (outside M x N) get an offset beyond the descriptor's range, which the
+  // hardware drops on stores and reads as zero on loads.
+  constexpr int kOutOfRange = (int)0x80000000u;
+  constexpr int kBigRange = 0x7FFFFFF0;
+  // this wave's scratch slot for the staggered tile's partial sums
+  __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<char*>(partials) + ((int64_t)blockIdx.x * NW + w) * (FN * FM * 4) * 1024,
+      (short)0, FN * FM * 4 * 1024, kRsrcWord3);
+  const int nl0 = wn * FN * 32 + (lane >> 5) * 4;
+  const int ml0 = wm * FM * 32 + (lane & 31);
+  const int ldy4 = (int)N * 4;
+  int gs = 0;
+  for (int j = 0; j < nseg; j++) {
+#pragma unroll
+    for (int a = 0; a < FN; a++)
+#pragma unroll
+      for (int b = 0; b < FM; b++) acc[a][b] = v16i{};
+    const int nst = kend(j) - kbeg(j);  // even
+    for (int q = 0; q < nst; q += 2) {
+      step(gs, f0, f1, true);
+      // the next segment's first fragments are read after the epilogue
+      step(gs + 1, f1, f0, q + 2 < nst);
+      gs += 2;
+    }
+    // The staggered tile's first part parks its partial sums in this
+    // wave's slot; its last part adds them back before the epilogue.
+    const bool park = s0 > 0 && j == 0;
+    const bool unpark = s0 > 0 && j == nseg - 1;
+    // ---- epilogue of tile tseg(j)
+    int tm, tn;
+    coords(tseg(j), tm, tn);
+    const int par = j & 1;
+    const int64_t ybase = ((int64_t)tm * BM * N + (int64_t)tn * BN) * 4;
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char*>(Y) + ybase, (short)0, kBigRange, kRsrcWord3);
+    __amdgpu_buffer_rsrc_t rr = yr;
+    if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID)
+      rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(epi.resid) + (ybase >> 2),
+                                             (short)0, kBigRange, kRsrcWord3);
+    const int voff_lane = ml0 * ldy4 + nl0 * 4;
+    const int64_t mrow0 = (int64_t)tm * BM + ml0;
+    const int64_t ncol0 = (int64_t)tn * BN + nl0;
+#pragma unroll
+    for (int a = 0; a < FN; a++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int nl = nl0 + a * 32 + 8 * g;
+        const bool n_ok = ncol0 + a * 32 + 8 * g < N;
+        const float4 s4 = *reinterpret_cast<const float4*>(&colb[par][0][nl]);
+        const float4 b4 = *reinterpret_cast<const float4*>(&colb[par][1][nl]);
+        const float4 g4 = *reinterpret_cast<const float4*>(&colb[par][2][nl]);
+#pragma unroll
+        for (int b = 0; b < FM; b++) {
+          const int idx = (a * FM + b) * 4 + g;
+          const v16i& cc = acc[a][b];
+          v4i c4 = {cc[4 * g], cc[4 * g + 1], cc[4 * g + 2], cc[4 * g + 3]};
+          if (park) {
+            __builtin_amdgcn_raw_buffer_store_b128(c4, pr, (int)lane_off, idx * 1024, 0);
+            continue;
+          }
+          if (unpark) c4 += __builtin_amdgcn_raw_buffer_load_b128(pr, (int)lane_off, idx * 1024, 0);
+          const bool ok = n_ok && (mrow0 + b * 32 < M);
+          const int voff = ok ? voff_lane : kOutOfRange;
+          const int soff = b * 32 * ldy4 + (a * 32 + 8 * g) * 4;
+          if constexpr (EPI == SDQ_EPI_ACC) {
+            __builtin_amdgcn_raw_buffer_store_b128(c4, yr, voff, soff, 0);
+          } else {
+            const float as_m = rowb[par][ml0 + b * 32];
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+            const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const float sc = as_m * sv[r];
+              const float af = (float)c4[r];
+              v[r] = epi.kzero ? 0.f : af * sc;
+            }
+            if (epi.bias) {
+#pragma unroll
+              for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
+            }
+            if constexpr (EPI == SDQ_EPI_GELU) {
+#pragma unroll
+              for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
+            } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
+              const v4f x = __builtin_amdgcn_raw_buffer_load_b128(rr, voff, soff, 0);
+              if constexpr (EPI == SDQ_EPI_RESID) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
+              } else if (epi.gate_fma) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = __builtin_fmaf(v[r], gv[r], x[r]);
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                  const float p = v[r] * gv[r];
+                  v[r] = x[r] + p;
+                }
+              }
+            }
+            const v4f out = {v[0], v[1], v[2], v[3]};
+            __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, soff, 0);
+          }
+        }
+        // keep the scheduler from hoisting every group's operands at once
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // The next segment's first stage stays in its buffer until the next
+    // barrier; read it now that the epilogue's registers are free.
+    if (gs < total) lds_read(gs, f0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny kernel (M <= 32*FMS): one workgroup per 32 weight rows; its SPLIT
 // waves stride over K, each streaming 1 KB weight fragments straight from
 // HBM into VGPRs, then the partial int32 accumulators are summed through LDS
-// (exact, so the order does not matter).
+// in a fixed order (exact, so the order does not matter anyway).
 template <int FMS, int SPLIT>
 __global__ void __launch_bounds__(SPLIT * 64)
 qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
@@ -231,9 +703,9 @@ qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
   const int8_t* wp = wt + rb * KFp * 1024 + lane * 16;
   const int8_t* ap = at + lane * 16;
 
-  v4i acc[FMS];
+  v16i acc[FMS];
 #pragma unroll
-  for (int j = 0; j < FMS; j++) acc[j] = v4i{0, 0, 0, 0};
+  for (int j = 0; j < FMS; j++) acc[j] = v16i{};
 
   constexpr int U = 4;
   int64_t kb = w;
@@ -251,43 +723,79 @@ qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
     for (int u = 0; u < U; u++)
 #pragma unroll
       for (int j = 0; j < FMS; j++)
-        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u][j], acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u], b[u][j], acc[j], 0, 0, 0);
   }
   for (; kb < KFp; kb += SPLIT) {
     const v4i a = *reinterpret_cast<const v4i*>(wp + kb * 1024);
 #pragma unroll
     for (int j = 0; j < FMS; j++) {
       const v4i b = *reinterpret_cast<const v4i*>(ap + (j * KFp + kb) * 1024);
-      acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
     }
   }
 
-  __shared__ v4i red[SPLIT][FMS][64];
-#pragma unroll
-  for (int j = 0; j < FMS; j++) red[w][j][lane] = acc[j];
-  __syncthreads();
-  if (w != 0) return;
-  const int64_t n0 = rb * 16 + (lane >> 4) * 4;
+  __shared__ int red[SPLIT][16][64];
+  const int64_t n_lane = rb * 32 + (lane >> 5) * 4;
 #pragma unroll
   for (int j = 0; j < FMS; j++) {
-    v4i s = red[0][j][lane];
 #pragma unroll
-    for (int ww = 1; ww < SPLIT; ww++) s += red[ww][j][lane];
-    const int64_t m = j * 16 + (lane & 15);
-    const float as_m = (m < M) ? as[m] : 0.f;
-    store_out(s, m, n0, M, N, as_m, bs, epi, Y, vec);
+    for (int r = 0; r < 16; r++) red[w][r][lane] = acc[j][r];
+    __syncthreads();
+    if (w == 0) {
+      v16i s;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        int t = red[0][r][lane];
+#pragma unroll
+        for (int ww = 1; ww < SPLIT; ww++) t += red[ww][r][lane];
+        s[r] = t;
+      }
+      const int64_t m = j * 32 + (lane & 31);
+      const float as_m = (m < M) ? as[m] : 0.f;
+      store_block(s, m, n_lane, M, N, as_m, bs, epi, Y, vec);
+    }
+    __syncthreads();
   }
 }
 
-template <int BN, int BM, int WN, int WM, int KS>
+template <int BN, int BM, int WN, int WM, int KS, int STAGES>
 hipError_t run_tiled(const int8_t* wt, const float* bs, const int8_t* at, const float* as,
                      int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y, int vec,
                      hipStream_t s) {
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m;
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL((qgemm_tiled<BN, BM, WN, WM, KS>), dim3((unsigned)T), dim3(WN * WM * 64), 0,
-                     s, wt, bs, at, as, M, N, KFp, tiles_n, tiles_m, epi, Y, vec);
+  if (KFp % KS != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((qgemm_tiled<BN, BM, WN, WM, KS, STAGES>), dim3((unsigned)T),
+                     dim3(WN * WM * 64), 0, s, wt, bs, at, as, M, N, KFp, tiles_n, tiles_m, epi, Y,
+                     vec);
+  return hipGetLastError();
+}
+
+template <int BN, int BM, int WN, int WM, int KS, int STAGES>
+hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, const float* as,
+                       int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
+                       const GemmAux& aux, int max_groups, hipStream_t s) {
+  const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
+  const int64_t T = (int64_t)tiles_n * tiles_m;
+  if (T <= 0) return hipSuccess;
+  if (KFp % KS != 0 || (KFp / KS) % 2 != 0 || KFp / KS < STAGES) return hipErrorInvalidValue;
+  int G = (int)(T < max_groups ? T : max_groups);
+  if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
+  if ((size_t)G * BN * BM * 4 > aux.partials_bytes) return hipErrorInvalidValue;
+#define SDQ_LAUNCH_PERSIST(K)                                                                    \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, K>), dim3((unsigned)G),          \
+                     dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
+                     epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger)
+  switch (epi.kind) {
+    case SDQ_EPI_NONE: SDQ_LAUNCH_PERSIST(SDQ_EPI_NONE); break;
+    case SDQ_EPI_GELU: SDQ_LAUNCH_PERSIST(SDQ_EPI_GELU); break;
+    case SDQ_EPI_GATED: SDQ_LAUNCH_PERSIST(SDQ_EPI_GATED); break;
+    case SDQ_EPI_RESID: SDQ_LAUNCH_PERSIST(SDQ_EPI_RESID); break;
+    case SDQ_EPI_ACC: SDQ_LAUNCH_PERSIST(SDQ_EPI_ACC); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef SDQ_LAUNCH_PERSIST
   return hipGetLastError();
 }
 
@@ -296,7 +804,7 @@ hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const
                       int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y, int vec,
                       hipStream_t s) {
   constexpr int SPLIT = 4;
-  const int64_t blocks = ceil_div(N, 16);
+  const int64_t blocks = ceil_div(N, 32);
   if (blocks <= 0) return hipSuccess;
   hipLaunchKernelGGL((qgemm_skinny<FMS, SPLIT>), dim3((unsigned)blocks), dim3(SPLIT * 64), 0, s,
                      wt, bs, at, as, M, N, KFp, epi, Y, vec);
@@ -307,9 +815,9 @@ hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const
 
 int gemm_cfg_bm(int cfg) {
   switch (cfg) {
-    case kCfgSkinny1: return 16;
-    case kCfgSkinny2: return 32;
-    case kCfgSkinny4: return 64;
+    case kCfgSkinny1: return 32;
+    case kCfgSkinny2: return 64;
+    case kCfgSkinny4: return 128;
     case kCfg128x128: return 128;
     case kCfg256x256: return 256;
     default: return 256;
@@ -318,9 +826,9 @@ int gemm_cfg_bm(int cfg) {
 
 const char* gemm_cfg_name(int cfg) {
   switch (cfg) {
-    case kCfgSkinny1: return "skinny16";
-    case kCfgSkinny2: return "skinny32";
-    case kCfgSkinny4: return "skinny64";
+    case kCfgSkinny1: return "skinny32";
+    case kCfgSkinny2: return "skinny64";
+    case kCfgSkinny4: return "skinny128";
     case kCfg128x128: return "tile128x128";
     case kCfg256x256: return "tile256x256";
     default: return "?";
@@ -328,9 +836,8 @@ const char* gemm_cfg_name(int cfg) {
 }
 
 int choose_gemm_cfg(int64_t M, int64_t N, int cu_count) {
-  if (M <= 16) return kCfgSkinny1;
-  if (M <= 32) return kCfgSkinny2;
-  if (M <= 64) return kCfgSkinny4;
+  if (M <= 32) return kCfgSkinny1;
+  if (M <= 64) return kCfgSkinny2;
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
   if (t256 >= 2 * (int64_t)(cu_count > 0 ? cu_count : 256)) return kCfg256x256;
   return kCfg128x128;
@@ -338,15 +845,22 @@ int choose_gemm_cfg(int64_t M, int64_t N, int cu_count) {
 
 hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,
                         const float* as, int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi,
-                        void* Y, int vec, hipStream_t s) {
+                        void* Y, int vec, const GemmAux& aux, hipStream_t s) {
+  const ColOps cols{bs, aux.bias_pad, aux.gate_pad};
   switch (cfg) {
     case kCfgSkinny1: return run_skinny<1>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfgSkinny2: return run_skinny<2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfgSkinny4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg128x128:
-      return run_tiled<128, 128, 2, 2, 2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+      if (vec && aux.sink && aux.partials)
+        return run_persist<128, 128, 2, 2, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                 2 * aux.cu_count, s);
+      return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
-      return run_tiled<256, 256, 2, 4, 2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+      if (vec && aux.sink && aux.partials)
+        return run_persist<256, 256, 2, 4, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                 aux.cu_count, s);
+      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,15 +1,17 @@
 // Internal declarations shared by the sdq HIP translation units.
 //
 // Fragment layout ("frag layout") used for both operands in HBM:
-//   an operand with R rows and K int8 columns is cut into 16-row x 64-byte
-//   fragments; fragment (rb, kb) covers rows [16rb, 16rb+16) and columns
-//   [64kb, 64kb+64). It occupies 1024 contiguous bytes at
+//   an operand with R rows and K int8 columns is cut into 32-row x 32-byte
+//   fragments; fragment (rb, kb) covers rows [32rb, 32rb+32) and columns
+//   [32kb, 32kb+32). It occupies 1024 contiguous bytes at
 //   ((rb * KFp) + kb) * 1024, and inside it lane l (0..63) owns the 16 bytes
-//   at l*16, holding row 16rb + (l & 15), columns 64kb + 16(l >> 4) .. +15.
-//   This is exactly the per-lane operand of v_mfma_i32_16x16x64_i8, so a
-//   1 KB fragment moves global -> LDS -> VGPRs as one linear, conflict-free
-//   wave-wide 16-byte-per-lane copy. Rows are padded to a multiple of the
-//   largest GEMM tile and KFp to a multiple of 4 fragments with zeros.
+//   at l*16, holding row 32rb + (l & 31), columns 32kb + 16(l >> 5) .. +15.
+//   This is the per-lane A/B operand of v_mfma_i32_32x32x32_i8 (A and B use
+//   the same k placement, so the exact int32 sum does not depend on which
+//   k the hardware assigns to a byte), so a 1 KB fragment moves
+//   global -> LDS -> VGPRs as one linear, conflict-free 16-byte-per-lane
+//   copy. Rows are padded to a multiple of the largest GEMM tile and KFp to
+//   a multiple of 8 fragments (256 bytes of K) with zeros.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -21,11 +23,12 @@
 
 namespace sdq {
 
-constexpr int kFragRows = 16;
-constexpr int kFragK = 64;
+constexpr int kFragRows = 32;
+constexpr int kFragK = 32;
 constexpr int kFragBytes = 1024;
-constexpr int kKFragAlign = 4;   // KFp is a multiple of this many fragments
+constexpr int kKFragAlign = 8;   // KFp is a multiple of this many fragments
 constexpr int kRowAlign = 256;   // weight rows padded to this (largest BN)
+constexpr int kColPad = 256;     // extra zero floats after padded column arrays
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
@@ -54,9 +57,18 @@ struct EpiArgs {
 
 // ---- launchers (return hipError_t of the launch) -------------------------
 // Activation quantizer: A [M,K] f32 row-major -> frag layout (rows padded to
-// Mp, zero rows beyond M) + as[M].
+// Mp, zero rows beyond M) + as[M]. The same launch copies bias / gate (when
+// non-null) into the zero-padded column buffers bias_pad / gate_pad of CP
+// floats that the persistent GEMM moves by LDS-DMA.
+struct ColCopy {
+  const float* bias;
+  const float* gate;
+  float* bias_pad;
+  float* gate_pad;
+  int64_t N, CP;
+};
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
-                                  int8_t* at, float* as, hipStream_t s);
+                                  int8_t* at, float* as, const ColCopy& cc, hipStream_t s);
 // Same quantizer, row-major int8 output [M,K] (parity API).
 hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
                                      hipStream_t s);
@@ -71,9 +83,9 @@ hipError_t launch_unpack_weight(const int8_t* frags, int64_t N, int64_t K, int64
 
 // GEMM tile configurations.
 enum GemmCfg : int {
-  kCfgSkinny1 = 0,  // M <= 16: one 16-row activation block, split-K waves
-  kCfgSkinny2,      // M <= 32
-  kCfgSkinny4,      // M <= 64
+  kCfgSkinny1 = 0,  // M <= 32: one 32-row activation block, split-K waves
+  kCfgSkinny2,      // M <= 64
+  kCfgSkinny4,      // M <= 128
   kCfg128x128,      // BN=128, BM=128
   kCfg256x256,      // BN=256, BM=256
   kCfgCount
@@ -82,8 +94,22 @@ int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
 const char* gemm_cfg_name(int cfg);
 int choose_gemm_cfg(int64_t M, int64_t N, int cu_count);
 
+// Extra buffers of the persistent GEMM path: bias / gate copied into
+// zero-padded buffers (nullptr when absent) so they can be moved by LDS-DMA,
+// and a >= 1 KB scratch sink for the stores of masked lanes. sink == nullptr
+// selects the non-persistent kernels.
+struct GemmAux {
+  const float* bias_pad;
+  const float* gate_pad;
+  float* sink;
+  void* partials;         // per-workgroup scratch for staggered partial sums
+  size_t partials_bytes;  // >= grid * BN * BM * 4
+  int stagger;            // tile phases per XCD (1 = none)
+  int cu_count;
+};
+
 hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,
                         const float* as, int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi,
-                        void* Y, int vec_ok, hipStream_t s);
+                        void* Y, int vec_ok, const GemmAux& aux, hipStream_t s);
 
 }  // namespace sdq

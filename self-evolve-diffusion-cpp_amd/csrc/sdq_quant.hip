@@ -8,10 +8,10 @@
 //         rounded result leaves int32 give -127 (x86 cvtss2si "indefinite"
 //         INT_MIN, then clamped), src/core/qgemm.cpp:62-69.
 //
-// One workgroup owns one 16-row block (one fragment row) so it can emit
+// One workgroup owns one 32-row block (one fragment row) so it can emit
 // whole 1 KB fragments: every lane loads the 16 floats it will own in the
 // fragment, keeps up to CACHE fragments in registers across the amax
-// reduction (single HBM read when K <= NW*CACHE*64), and re-reads only the
+// reduction (single HBM read when K <= NW*CACHE*32), and re-reads only the
 // tail beyond that.
 #include "sdq_internal.h"
 
@@ -20,8 +20,8 @@
 namespace sdq {
 namespace {
 
-constexpr int kQuantWaves = 8;
-constexpr int kQuantCache = 6;  // 8 waves x 6 frags x 64 = K <= 3072 in one pass
+constexpr int kQuantWaves = 16;
+constexpr int kQuantCache = 6;  // 16 waves x 6 frags x 32 = K <= 3072 in one pass
 
 __device__ __forceinline__ int quant_one(float v, float inv) {
   const float y = v * inv;
@@ -77,14 +77,20 @@ __device__ __forceinline__ uint4 pack16(const float v[16], float inv) {
 template <int NW, int CACHE, bool FRAG_OUT>
 __global__ void __launch_bounds__(NW * 64)
 act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, int64_t KFp,
-                 int vec, int8_t* __restrict__ out, float* __restrict__ as) {
+                 int vec, int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
+  // Side job: zero-padded copies of the GEMM's per-column bias / gate.
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (cc.bias_pad) cc.bias_pad[i] = i < cc.N ? cc.bias[i] : 0.f;
+    if (cc.gate_pad) cc.gate_pad[i] = i < cc.N ? cc.gate[i] : 0.f;
+  }
   const int w = threadIdx.x >> 6;
   const int l = threadIdx.x & 63;
   const int64_t rb = blockIdx.x;
-  const int64_t row = rb * 16 + (l & 15);
+  const int64_t row = rb * 32 + (l & 31);
   const bool row_ok = row < M;
   const float* rowp = A + (row_ok ? row : 0) * K;
-  const int kg = (l >> 4) * 16;
+  const int kg = (l >> 5) * 16;
 
   float cache[CACHE][16];
   float mx = 0.f;
@@ -92,40 +98,38 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
   for (int c = 0; c < CACHE; c++) {
     const int64_t kb = w + (int64_t)c * NW;
     if (kb < KL) {
-      load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, cache[c]);
+      load16(rowp, kb * 32 + kg, K, row_ok, vec != 0, cache[c]);
       mx = amax16(cache[c], mx);
     }
   }
   for (int64_t kb = w + (int64_t)CACHE * NW; kb < KL; kb += NW) {
     float t[16];
-    load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, t);
+    load16(rowp, kb * 32 + kg, K, row_ok, vec != 0, t);
     mx = amax16(t, mx);
   }
-  // Lanes l, l^16, l^32, l^48 hold the same row.
-  float o = __shfl_xor(mx, 16);
+  // Lanes l and l^32 hold the same row.
+  const float o = __shfl_xor(mx, 32);
   mx = (mx < o) ? o : mx;
-  o = __shfl_xor(mx, 32);
-  mx = (mx < o) ? o : mx;
-  __shared__ float red[NW][16];
-  if (l < 16) red[w][l] = mx;
+  __shared__ float red[NW][32];
+  if (l < 32) red[w][l] = mx;
   __syncthreads();
   mx = 0.f;
 #pragma unroll
   for (int i = 0; i < NW; i++) {
-    const float r = red[i][l & 15];
+    const float r = red[i][l & 31];
     mx = (mx < r) ? r : mx;
   }
   float sc = mx / 127.f;
   if (sc == 0.f) sc = 1.f;
   const float inv = 1.f / sc;
-  if (w == 0 && l < 16 && row_ok) as[row] = sc;
+  if (w == 0 && l < 32 && row_ok) as[row] = sc;
 
   auto emit = [&](int64_t kb, const float v[16]) {
     const uint4 q = pack16(v, inv);
     if (FRAG_OUT) {
       *reinterpret_cast<uint4*>(out + (rb * KFp + kb) * 1024 + l * 16) = q;
     } else if (row_ok) {
-      const int64_t k0 = kb * 64 + kg;
+      const int64_t k0 = kb * 32 + kg;
       int8_t* dst = out + row * K;
       const uint32_t wds[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -140,7 +144,7 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
   }
   for (int64_t kb = w + (int64_t)CACHE * NW; kb < KL; kb += NW) {
     float t[16];
-    load16(rowp, kb * 64 + kg, K, row_ok, vec != 0, t);
+    load16(rowp, kb * 32 + kg, K, row_ok, vec != 0, t);
     emit(kb, t);
   }
 }
@@ -150,21 +154,21 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 }  // namespace
 
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
-                                  int8_t* at, float* as, hipStream_t s) {
+                                  int8_t* at, float* as, const ColCopy& cc, hipStream_t s) {
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
-  const int64_t blocks = Mp / 16;
+  const int64_t blocks = Mp / kFragRows;
   hipLaunchKernelGGL((act_quant_kernel<kQuantWaves, kQuantCache, true>), dim3((unsigned)blocks),
-                     dim3(kQuantWaves * 64), 0, s, A, M, K, KFp, KFp, vec, at, as);
+                     dim3(kQuantWaves * 64), 0, s, A, M, K, KFp, KFp, vec, at, as, cc);
   return hipGetLastError();
 }
 
 hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
                                      hipStream_t s) {
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
-  const int64_t blocks = ceil_div(M, 16);
-  const int64_t KL = ceil_div(K, 64);
+  const int64_t blocks = ceil_div(M, kFragRows);
+  const int64_t KL = ceil_div(K, kFragK);
   hipLaunchKernelGGL((act_quant_kernel<kQuantWaves, kQuantCache, false>), dim3((unsigned)blocks),
-                     dim3(kQuantWaves * 64), 0, s, A, M, K, KL, KL, vec, aq, as);
+                     dim3(kQuantWaves * 64), 0, s, A, M, K, KL, KL, vec, aq, as, ColCopy{});
   return hipGetLastError();
 }
 

@@ -17,8 +17,8 @@ repack_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K, int64_t KFp, i
   if (f >= nfrags) return;
   const int l = threadIdx.x & 63;
   const int64_t rb = f / KFp, kb = f - rb * KFp;
-  const int64_t row = rb * 16 + (l & 15);
-  const int64_t k0 = kb * 64 + (l >> 4) * 16;
+  const int64_t row = rb * 32 + (l & 31);
+  const int64_t k0 = kb * 32 + (l >> 5) * 16;
   uint4 v = make_uint4(0, 0, 0, 0);
   if (row < N) {
     const int8_t* src = q + row * K;
@@ -41,8 +41,8 @@ unpack_kernel(const int8_t* __restrict__ frags, int64_t N, int64_t K, int64_t KF
   if (f >= nfrags) return;
   const int l = threadIdx.x & 63;
   const int64_t rb = f / KFp, kb = f - rb * KFp;
-  const int64_t row = rb * 16 + (l & 15);
-  const int64_t k0 = kb * 64 + (l >> 4) * 16;
+  const int64_t row = rb * 32 + (l & 31);
+  const int64_t k0 = kb * 32 + (l >> 5) * 16;
   if (row >= N) return;
   const uint4 v = *reinterpret_cast<const uint4*>(frags + f * 1024 + l * 16);
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -70,7 +70,7 @@ scale_pad_kernel(const uint8_t* __restrict__ scale, int64_t N, int64_t Np,
 hipError_t launch_repack_weight(const int8_t* q, const float* scale, int64_t N, int64_t K,
                                 int64_t Np, int64_t KFp, int8_t* frags, float* scale_out,
                                 hipStream_t s) {
-  const int64_t nfrags = (Np / 16) * KFp;
+  const int64_t nfrags = (Np / kFragRows) * KFp;
   const int vec = ((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (K % 16) == 0) ? 1 : 0;
   hipLaunchKernelGGL(repack_kernel, dim3((unsigned)ceil_div(nfrags, 4)), dim3(256), 0, s, q, N, K,
                      KFp, nfrags, vec, frags);
@@ -83,7 +83,7 @@ hipError_t launch_repack_weight(const int8_t* q, const float* scale, int64_t N, 
 
 hipError_t launch_unpack_weight(const int8_t* frags, int64_t N, int64_t K, int64_t KFp, int8_t* q,
                                 hipStream_t s) {
-  const int64_t nfrags = ceil_div(N, 16) * KFp;
+  const int64_t nfrags = ceil_div(N, kFragRows) * KFp;
   if (nfrags == 0) return hipSuccess;
   hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)ceil_div(nfrags, 4)), dim3(256), 0, s, frags, N,
                      K, KFp, nfrags, q);
