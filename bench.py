@@ -43,7 +43,30 @@ def parse():
     ap.add_argument("--cpu-sample-rows", type=int, default=4096)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 FETCH/WRITE_SIZE summary used for roofline.traffic")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="run a few steps plus a 1 GiB torch copy (the counter calibration "
+                         "kernel) and exit; used under rocprofv3 --pmc")
     return ap.parse_args()
+
+
+def profile_pass(torch, sdq, args):
+    """Workload for `rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -- python bench.py
+    --profile-pass`: a few qgemm steps, then a plain 1 GiB device copy whose
+    known traffic calibrates the counters."""
+    dev = torch.device("cuda:0")
+    sdq.init(0)
+    A, q, s, bias = make_inputs(torch, dev, args.M, args.K, args.N)
+    w = sdq.Weight.from_device(q, s)
+    Y = torch.empty((args.M, args.N), device=dev, dtype=torch.float32)
+    for _ in range(max(args.steps, 1)):
+        sdq.qlinear(w, A, Y, kind="none", bias=bias)
+    torch.cuda.synchronize()
+    src = torch.ones(1 << 28, device=dev, dtype=torch.float32)  # 1 GiB
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_pass": True, "copy_bytes": src.numel() * 4, "M": args.M,
+                      "K": args.K, "N": args.N}), flush=True)
 
 
 def make_inputs(torch, dev, M, K, N, seed=1234):
@@ -112,6 +135,9 @@ def main():
 
     import sdq
 
+    if args.profile_pass:
+        profile_pass(torch, sdq, args)
+        return
     M, K, N = args.M, args.K, args.N
     dev = torch.device("cuda:0")
     sdq.init(0)
@@ -156,7 +182,7 @@ def main():
             tj = json.load(f)
         key = f"{M}x{K}x{N}"
         if key in tj:
-            traffic = tj[key]["gemm_bytes_per_launch"]
+            traffic = tj[key]["qgemm_hbm_bytes_per_launch"]
     except (OSError, ValueError, KeyError):
         traffic = None
 
