@@ -35,6 +35,9 @@ def _load():
     lib.orc_act_quant.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
     lib.orc_qgemm_acc.argtypes = [_i8p, _i8p, _i64, _i64, _i64, _i32p, ctypes.c_int]
     lib.orc_rescale.argtypes = [_i32p, _f32p, _f32p, _i64, _i64, _f32p]
+    lib.orc_linear_at.argtypes = [_i8p, _f32p, _i8p, _f32p, ctypes.c_void_p, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, _i64, _i64,
+                                  ctypes.c_void_p, ctypes.c_void_p, _i64, _f32p]
     lib.orc_qgemm.argtypes = [_f32p, _i8p, _f32p, _i64, _i64, _i64, _f32p, ctypes.c_int]
     lib.orc_qgemm.restype = ctypes.c_int
     lib.orc_bias_add.argtypes = [_f32p, _f32p, _i64, _i64]
@@ -116,6 +119,41 @@ def qgemm(A, Bq, bs, nthreads: int | None = None):
     rc = lib().orc_qgemm(A, Bq, bs, M, K, N, out, nthreads or nthreads_default())
     if rc != 0:
         raise MemoryError("orc_qgemm allocation failed")
+    return out
+
+
+def linear_at(aq, asc, bq, bs, ms, ns, bias=None, epilogue="none", gate=None, resid=None,
+              use_fma=True):
+    """Outputs of qgemm (+ bias, + the gated / plain residual epilogue) at
+    positions (ms[i], ns[i]) only, from the quantized activations (act_quant)
+    and the packed weights; resid is the full [M, N] residual."""
+    aq = np.ascontiguousarray(aq, np.int8)
+    bq = np.ascontiguousarray(bq, np.int8)
+    asc = np.ascontiguousarray(asc, np.float32)
+    bs = np.ascontiguousarray(bs, np.float32)
+    ms = np.ascontiguousarray(ms, np.int64)
+    ns = np.ascontiguousarray(ns, np.int64)
+    K, N = aq.shape[1], bq.shape[0]
+    assert bq.shape[1] == K and ms.shape == ns.shape
+    assert ms.size == 0 or (0 <= ms.min() and ms.max() < aq.shape[0])
+    assert ns.size == 0 or (0 <= ns.min() and ns.max() < N)
+    epi = {"none": 0, "gated": 2, "resid": 3}[epilogue]
+    keep = []
+
+    def ptr(x, shape):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, np.float32)
+        assert x.shape == shape
+        keep.append(x)
+        return x.ctypes.data
+
+    b = ptr(bias, (N,))
+    g = ptr(gate, (N,)) if epi == 2 else None
+    r = ptr(resid, (aq.shape[0], N)) if epi in (2, 3) else None
+    out = np.empty(ms.shape, np.float32)
+    lib().orc_linear_at(aq, asc, bq, bs, b, epi, 1 if use_fma else 0, g, r, K, N, ms.ctypes.data,
+                        ns.ctypes.data, ms.size, out)
     return out
 
 

@@ -15,6 +15,9 @@
  *                          closed-form special cases (zero row, +-amax -> +-127,
  *                          NaN/Inf/denormal rows), brute-force numpy restatement.
  *   orc_qgemm_acc        - brute-force int64 numpy matmul (exact integer sum).
+ *   orc_linear_at        - equal to orc_qgemm + orc_bias_add / orc_gated_add /
+ *                          orc_add at every position of small products (so
+ *                          pinned through them).
  *   orc_qgemm            - compiled reference sd::qgemm (oracle/_ref) bit-exact on
  *                          many shapes incl. M>=2048 (widen path) and M<2048;
  *                          reference golden vectors (cosine > 0.999 vs fp32).
@@ -132,6 +135,41 @@ void orc_rescale(const int32_t* acc, const float* as, const float* bs, int64_t M
       float a = (float)acc[i * N + j];
       out[i * N + j] = a * s;
     }
+}
+
+/* orc_qgemm_acc + orc_rescale, then the mlin bias (src/model/ovi_dit.cpp:71-79,
+ * when b is non-null) and the consumer's epilogue, evaluated only at the
+ * `count` output positions (ms[i], ns[i]), for spot checks of full-size
+ * products. epi: 0 none, 2 gated residual x + y*g (fused multiply-add when
+ * gate_fma, as orc_gated_add), 3 plain residual x + y (orc_add); x is the
+ * residual row-major [*, N] at resid[m*N + n]. */
+void orc_linear_at(const int8_t* aq, const float* as, const int8_t* bq, const float* bs,
+                   const float* b, int epi, int gate_fma, const float* gate, const float* resid,
+                   int64_t K, int64_t N, const int64_t* ms, const int64_t* ns, int64_t count,
+                   float* out) {
+  for (int64_t i = 0; i < count; i++) {
+    const int64_t m = ms[i], n = ns[i];
+    const int8_t* ar = aq + m * K;
+    const int8_t* br = bq + n * K;
+    int32_t acc = 0;
+    for (int64_t k = 0; k < K; k++) acc += (int32_t)ar[k] * (int32_t)br[k];
+    float s = as[m] * bs[n];
+    float a = (float)acc;
+    float y = a * s;
+    if (b) y = y + b[n];
+    if (epi == 2) {
+      const float x = resid[m * N + n];
+      if (gate_fma) {
+        y = fmaf(y, gate[n], x);
+      } else {
+        float p = y * gate[n];
+        y = x + p;
+      }
+    } else if (epi == 3) {
+      y = resid[m * N + n] + y;
+    }
+    out[i] = y;
+  }
 }
 
 /* src/core/qgemm.cpp:73-142 sd::qgemm: out [M,N] (zero-filled first by the

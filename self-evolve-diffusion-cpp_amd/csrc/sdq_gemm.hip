@@ -382,18 +382,61 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // Persistent tiled kernel (the main path; needs 16-byte vector epilogue
 // access). gridDim.x workgroups walk the tile list with stride gridDim.x,
 // and the LDS pipeline runs straight across tile boundaries: the next
-// tile's first STAGES stages are prefetched while the current tile's last
-// stages compute, so the epilogue of one tile overlaps the loads of the
-// next. On this GPU family one counter (vmcnt) tracks loads and stores and
-// a store may complete before an older load, so after an epilogue the
-// first wait drains everything (vmcnt(0)); later waits count loads only.
-// Per-tile weight scales, bias, gate and activation scales arrive by
-// LDS-DMA into a double buffer alongside stage 0.
-template <int BN, int BM, int WN, int WM, int KS, int STAGES, int EPI>
+// tile's first stages are prefetched while the current tile's last stages
+// compute, so the epilogue of one tile overlaps the loads of the next.
+//
+// A pipeline stage holds two k-fragments (64 bytes of K) of the tile's
+// weight and activation panels. Each step (one stage) runs in two halves:
+//   half 0: the 8 MFMAs of k-fragment 0 from registers, interleaved with
+//           the LDS reads of k-fragment 1 of the same stage;
+//   wait until this wave's loads of the next stage have landed, barrier;
+//   half 1: the 8 MFMAs of k-fragment 1, interleaved with the LDS-DMA of
+//           the stage STAGES ahead (into the buffer this stage used) and
+//           the LDS reads of the next stage's k-fragment 0.
+// The steady state is branch-free: past the last stage the issue cursor
+// uses zero-range buffer descriptors, so its loads fetch nothing and land
+// in a buffer no remaining stage reads, and every wait keeps the same
+// count. On this GPU family one counter (vmcnt) tracks loads and stores;
+// a wait counts younger loads only, so pending epilogue stores can only
+// make a wait longer. Per-tile weight scales, bias, gate and activation
+// scales arrive by LDS-DMA into a double buffer after the tile's first
+// stage.
+// Raw buffer descriptor as an SGPR quad (base, range, 32-bit format) and
+// the 16-byte-per-lane LDS-DMA load, written as inline asm so that the
+// compiler does not track it: it would otherwise assume every LDS read may
+// alias every LDS-DMA in flight and drain vmcnt before each read. The
+// kernel orders these loads itself (explicit vmcnt waits + barriers).
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4u raw_rsrc(const void* base, uint32_t range) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  v4u r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane(range);
+  r.w = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
+  return r;
+}
+__device__ __forceinline__ void dma16(v4u rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
+}
+__device__ __forceinline__ uint32_t lds_addr32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// A 16-byte store reads its data VGPRs after issue; a VALU write to them
+// needs wait states in between. The compiler inserts them, but counts a
+// scheduling fence (sched_barrier, which emits no code) as one, so the
+// epilogue's fenced groups give each store an explicit gap.
+__device__ __forceinline__ void store_data_gap() { asm volatile("s_nop 1"); }
+
+template <int BN, int BM, int WN, int WM, int STAGES, int EPI>
 __global__ void __launch_bounds__(WN* WM * 64, 1)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
               int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger) {
+  constexpr int KS = 2;
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -403,8 +446,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(WFR % NW == 0 && AFR % NW == 0, "stage fragments must split evenly over waves");
   static_assert(NW % KS == 0, "waves must be a multiple of k-fragments per stage");
   static_assert(NW >= 4, "four waves load the per-tile operands");
-  static_assert((STAGES - 1) * LPW < 64, "vmcnt range");
+  static_assert(STAGES >= 3 && (STAGES - 1) * LPW < 64, "vmcnt range");
+  static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
+  static_assert((STAGES & (STAGES - 1)) == 0, "ring index by mask");
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
@@ -418,11 +463,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int G = gridDim.x;
   const int ntile = (T - (int)blockIdx.x + G - 1) / G;
   const int nks = (int)(KFp / KS);
-  const int total = ntile * nks;
 
-  // Tile i of this workgroup -> (tm, tn): the XCD-aware grouped order used
-  // by the non-persistent kernel, applied to the virtual block id
-  // blockIdx.x + i*G (G is a multiple of 8, so it stays on this XCD).
+  // Tile i of this workgroup -> (tm, tn): XCD-aware grouped order applied
+  // to the virtual block id blockIdx.x + i*G (G is a multiple of 8, so it
+  // stays on this XCD).
   auto coords = [&](int i, int& tm, int& tn) {
     const int bid = (int)blockIdx.x + i * G;
     const int xcd = bid & 7, jx = bid >> 3, q8 = T >> 3, r8 = T & 7;
@@ -458,30 +502,43 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // ---- issue cursor: the next stage to load (segment cj, stage cks), with
   // buffer descriptors over that tile's weight / activation panels (raw
   // buffers: out-of-range reads return 0) so every load is one SGPR
-  // descriptor + SGPR offset + the lane's 16-byte VGPR offset.
+  // descriptor + SGPR offset + the lane's 16-byte VGPR offset. Past the
+  // last segment the descriptors have zero range.
   constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, valid
-  const int64_t wpanel = (int64_t)RBN * KFp * 1024, apanel = (int64_t)RBM * KFp * 1024;
+  const int wpanel = RBN * (int)KFp * 1024, apanel = RBM * (int)KFp * 1024;
+  const int wso0 = ((w / KS) * (int)KFp + (w % KS)) * 1024;
+  const int tso = (NW / KS) * (int)KFp * 1024;
+  const uint32_t lds0 = lds_addr32(lds) + (uint32_t)w * 1024u;
   int cj = 0, cks = s0, cend = kend(0), ctm = 0, ctn = 0, cgs = 0;
-  __amdgpu_buffer_rsrc_t wr, ar;
+  int wso = wso0 + s0 * KS * 1024;
+  bool col_due = true;  // the segment's first stage was issued; its column loads follow
+  v4u wr, ar;
   auto set_tile = [&](int i) {
     coords(i, ctm, ctn);
-    wr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(wt) + (int64_t)ctn * wpanel, (short)0, (int)wpanel, kRsrcWord3);
-    ar = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(at) + (int64_t)ctm * apanel, (short)0, (int)apanel, kRsrcWord3);
+    wr = raw_rsrc(wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
+    ar = raw_rsrc(at + (int64_t)ctm * apanel, (uint32_t)apanel);
   };
   set_tile(tseg(0));
-  typedef __attribute__((address_space(3))) void* lds_ptr_t;
-  auto dma_row = [&](const float* src, int64_t off, int count, float* dst) {
-    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(src) + off, (short)0, count * 4, kRsrcWord3);
-    if (lane * 4 < count)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, lane_off, 0, 0, 0);
+  // Load t (0..LPW-1) of the cursor's stage: WLD weight, then ALD
+  // activation fragments, 1 KB each.
+  auto dma_stage = [&](int t) {
+    const uint32_t buf = lds0 + (uint32_t)((cgs & (STAGES - 1)) * STAGE);
+    if (t < WLD)
+      dma16(wr, lane_off, (uint32_t)(wso + t * tso), buf + (uint32_t)(t * NW * 1024));
+    else
+      dma16(ar, lane_off, (uint32_t)(wso + (t - WLD) * tso),
+            buf + (uint32_t)((WFR + (t - WLD) * NW) * 1024));
   };
-  // Loads the next stage in issue order (global stage cgs).
-  auto issue = [&]() {
-    const int par = cj & 1;
-    if (cks == kbeg(cj)) {
+  auto dma_row = [&](const float* src, int64_t off, int count, const float* dst) {
+    if (lane * 4 < count)
+      dma16(raw_rsrc(src + off, (uint32_t)count * 4u), lane_off, 0u, lds_addr32(dst));
+  };
+  // After a stage's loads: the per-tile column operands (once per segment,
+  // younger than the segment's first stage), then the cursor moves on.
+  auto advance = [&]() {
+    if (col_due) {
+      col_due = false;
+      const int par = cj & 1;
       if (w < 3) {
         const float* src = w == 0 ? cols.scale : (w == 1 ? cols.bias : cols.gate);
         if (src) dma_row(src, (int64_t)ctn * BN, BN, &colb[par][w][0]);
@@ -489,87 +546,79 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
         dma_row(as, (int64_t)ctm * BM, BM, &rowb[par][0]);
       }
     }
-    char* buf = lds + (cgs % STAGES) * STAGE;
-    const int kb = cks * KS + (w % KS);
-    const int wso = ((w / KS) * (int)KFp + kb) * 1024;
-    const int tso = (NW / KS) * (int)KFp * 1024;
-#pragma unroll
-    for (int t = 0; t < WLD; t++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_ptr_t)(buf + (t * NW + w) * 1024), 16,
-                                               lane_off, wso + t * tso, 0, 0);
-#pragma unroll
-    for (int t = 0; t < ALD; t++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ar, (lds_ptr_t)(buf + WFR * 1024 + (t * NW + w) * 1024), 16, lane_off, wso + t * tso, 0,
-          0);
     cgs++;
+    wso += KS * 1024;
     if (++cks == cend) {
       if (++cj < nseg) {
         cks = kbeg(cj);
         cend = kend(cj);
+        wso = wso0 + cks * KS * 1024;
         set_tile(tseg(cj));
+        col_due = true;
+      } else {
+        wr = raw_rsrc(wt, 0u);
+        ar = raw_rsrc(at, 0u);
+        cend = -1;
       }
     }
   };
 
-  struct Frags {
-    v4i a[KS][FN], b[KS][FM];
+  struct Half {
+    v4i a[FN], b[FM];
   };
-  auto lds_read = [&](int gs, Frags& f) {
-    const char* cb = lds + (gs % STAGES) * STAGE;
-#pragma unroll
-    for (int kk = 0; kk < KS; kk++) {
-#pragma unroll
-      for (int i = 0; i < FN; i++)
-        f.a[kk][i] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + i) * KS + kk) * 1024 + lane_off);
-#pragma unroll
-      for (int j = 0; j < FM; j++)
-        f.b[kk][j] = *reinterpret_cast<const v4i*>(cb + WFR * 1024 +
-                                                   ((wm * FM + j) * KS + kk) * 1024 + lane_off);
-    }
+  // Fragment f (0..FN+FM-1: FN weight, then FM activation) of k-fragment
+  // kk of the stage held in LDS buffer `buf`.
+  auto read_frag = [&](const char* cb, int kk, int f, Half& h) {
+    if (f < FN)
+      h.a[f] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + f) * KS + kk) * 1024 + lane_off);
+    else
+      h.b[f - FN] = *reinterpret_cast<const v4i*>(
+          cb + WFR * 1024 + ((wm * FM + (f - FN)) * KS + kk) * 1024 + lane_off);
   };
   v16i acc[FN][FM];
-  auto mma = [&](const Frags& f, int kk) {
-#pragma unroll
-    for (int i = 0; i < FN; i++)
-#pragma unroll
-      for (int j = 0; j < FM; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[kk][i], f.b[kk][j], acc[i][j], 0, 0, 0);
+  auto mfma = [&](const Half& h, int i) {
+    const int a = i / FM, b = i % FM;
+    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], acc[a][b], 0, 0, 0);
   };
-  // Waits until this wave's loads of stage `next` have landed: at most the
-  // loads of the STAGES-2 later stages may be outstanding. Stores do not
-  // enter the count; a pending store only makes the wait longer.
-  auto wait_and_sync = [&](int next) {
-    if (next + STAGES - 2 < total)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW));
-    else
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    asm volatile("s_barrier" ::: "memory");
-  };
-  // One pipeline step: MFMAs of stage gs from `cur`, with the barrier for
-  // stage gs+1, the refill of the buffer stage gs occupied and (if `read`)
-  // the LDS reads of stage gs+1 into `nxt` placed between its k-fragments.
-  auto step = [&](int gs, const Frags& cur, Frags& nxt, bool read) {
-    mma(cur, 0);
-    if (gs + 1 < total) {
-      wait_and_sync(gs + 1);
-      if (gs + STAGES < total) issue();
-      if (read) lds_read(gs + 1, nxt);
+  // One pipeline step (stage gs, k-fragment 0 in `k0`): `k1` receives
+  // k-fragment 1 of stage gs, `nk0` k-fragment 0 of stage gs + 1. Each
+  // MFMA slot is fenced with the memory instructions issued behind it.
+  auto step = [&](int gs, const Half& k0, Half& k1, Half& nk0) {
+    const char* cb = lds + (gs & (STAGES - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < FN * FM; i++) {
+      mfma(k0, i);
+      if (i < FN + FM) read_frag(cb, 1, i, k1);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // this wave's loads of stage gs+1 landed; every wave finished reading
+    // buffer gs, so it can be refilled
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW) & ~(15 << 8));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const char* nb = lds + ((gs + 1) & (STAGES - 1)) * STAGE;
 #pragma unroll
-    for (int kk = 1; kk < KS; kk++) mma(cur, kk);
+    for (int i = 0; i < FN * FM; i++) {
+      mfma(k1, i);
+      if (i < LPW) dma_stage(i);
+      if (i < FN + FM) read_frag(nb, 0, i, nk0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    advance();
   };
 
+  // prologue: STAGES stages in flight, stage 0 landed
 #pragma unroll
-  for (int s = 0; s < STAGES; s++)
-    if (s < total) issue();
-  if (STAGES - 1 < total)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
-  else
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  for (int s = 0; s < STAGES; s++) {
+#pragma unroll
+    for (int t = 0; t < LPW; t++) dma_stage(t);
+    advance();
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
   asm volatile("s_barrier" ::: "memory");
-  Frags f0, f1;
-  lds_read(0, f0);
+  Half hx, hy, hz;
+#pragma unroll
+  for (int f = 0; f < FN + FM; f++) read_frag(lds, 0, f, hx);
 
   // Epilogue memory goes through buffer descriptors too: masked lanes
   // (outside M x N) get an offset beyond the descriptor's range, which the
@@ -591,9 +640,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       for (int b = 0; b < FM; b++) acc[a][b] = v16i{};
     const int nst = kend(j) - kbeg(j);  // even
     for (int q = 0; q < nst; q += 2) {
-      step(gs, f0, f1, true);
-      // the next segment's first fragments are read after the epilogue
-      step(gs + 1, f1, f0, q + 2 < nst);
+      step(gs, hx, hz, hy);
+      step(gs + 1, hy, hz, hx);
       gs += 2;
     }
     // The staggered tile's first part parks its partial sums in this
@@ -630,6 +678,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
           v4i c4 = {cc[4 * g], cc[4 * g + 1], cc[4 * g + 2], cc[4 * g + 3]};
           if (park) {
             __builtin_amdgcn_raw_buffer_store_b128(c4, pr, (int)lane_off, idx * 1024, 0);
+            store_data_gap();
             continue;
           }
           if (unpark) c4 += __builtin_amdgcn_raw_buffer_load_b128(pr, (int)lane_off, idx * 1024, 0);
@@ -638,6 +687,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
           const int soff = b * 32 * ldy4 + (a * 32 + 8 * g) * 4;
           if constexpr (EPI == SDQ_EPI_ACC) {
             __builtin_amdgcn_raw_buffer_store_b128(c4, yr, voff, soff, 0);
+            store_data_gap();
           } else {
             const float as_m = rowb[par][ml0 + b * 32];
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
@@ -675,16 +725,16 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
             }
             const v4f out = {v[0], v[1], v[2], v[3]};
             __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, soff, 0);
+            store_data_gap();
           }
         }
         // keep the scheduler from hoisting every group's operands at once
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // The next segment's first stage stays in its buffer until the next
-    // barrier; read it now that the epilogue's registers are free.
-    if (gs < total) lds_read(gs, f0);
   }
+  // the cursor's zero-range loads past the end still land in LDS
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 }
 
 // ---------------------------------------------------------------------------
@@ -779,12 +829,13 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m;
   if (T <= 0) return hipSuccess;
+  static_assert(KS == 2, "the persistent pipeline moves two k-fragments per stage");
   if (KFp % KS != 0 || (KFp / KS) % 2 != 0 || KFp / KS < STAGES) return hipErrorInvalidValue;
   int G = (int)(T < max_groups ? T : max_groups);
   if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
   if ((size_t)G * BN * BM * 4 > aux.partials_bytes) return hipErrorInvalidValue;
 #define SDQ_LAUNCH_PERSIST(K)                                                                    \
-  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, K>), dim3((unsigned)G),          \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, STAGES, K>), dim3((unsigned)G),          \
                      dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
                      epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger)
   switch (epi.kind) {
@@ -847,17 +898,21 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
                         const float* as, int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi,
                         void* Y, int vec, const GemmAux& aux, hipStream_t s) {
   const ColOps cols{bs, aux.bias_pad, aux.gate_pad};
+  // The persistent kernel addresses a tile's panels and output rows with
+  // 32-bit buffer offsets.
+  const bool persist = vec && aux.sink && aux.partials && KFp * 1024 * 8 <= 0x7FFFFFFF &&
+                       N * 4 * 256 <= 0x7FFFFFF0;
   switch (cfg) {
     case kCfgSkinny1: return run_skinny<1>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfgSkinny2: return run_skinny<2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfgSkinny4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg128x128:
-      if (vec && aux.sink && aux.partials)
+      if (persist)
         return run_persist<128, 128, 2, 2, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
                                                  2 * aux.cu_count, s);
       return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
-      if (vec && aux.sink && aux.partials)
+      if (persist)
         return run_persist<256, 256, 2, 4, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
                                                  aux.cu_count, s);
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);

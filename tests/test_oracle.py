@@ -142,6 +142,30 @@ def test_qgemm_acc_brute_force(oracle):
     assert oracle.qgemm_acc(aq, bq)[0, 0] == -127 * 127 * 14336
 
 
+def test_linear_at_equals_full_product(oracle):
+    """The spot-check form gives the full product's value at every position
+    (with and without bias), so it inherits orc_qgemm's pins."""
+    M, K, N = 37, 300, 45
+    A = oracle.randn(M * K, 71).reshape(M, K)
+    q, s = oracle.quant_rows(oracle.randn(N * K, 72).reshape(N, K) * np.float32(0.02))
+    bias = oracle.randn(N, 73) * np.float32(0.01)
+    aq, asc = oracle.act_quant(A)
+    mm, nn = np.meshgrid(np.arange(M), np.arange(N), indexing="ij")
+    full = oracle.qgemm(A, q, s)
+    assert_bitexact(oracle.linear_at(aq, asc, q, s, mm.ravel(), nn.ravel()).reshape(M, N),
+                    full, "linear_at")
+    yb = oracle.bias_add(full, bias)
+    assert_bitexact(oracle.linear_at(aq, asc, q, s, mm.ravel(), nn.ravel(), bias).reshape(M, N),
+                    yb, "linear_at+bias")
+    x = oracle.randn(M * N, 74).reshape(M, N)
+    g = oracle.randn(N, 75)
+    for fma in (True, False):
+        got = oracle.linear_at(aq, asc, q, s, mm.ravel(), nn.ravel(), bias, "gated", g, x, fma)
+        assert_bitexact(got.reshape(M, N), oracle.gated_add(x, yb, g, fma), f"gated fma={fma}")
+    got = oracle.linear_at(aq, asc, q, s, mm.ravel(), nn.ravel(), bias, "resid", resid=x)
+    assert_bitexact(got.reshape(M, N), oracle.add(x, yb), "resid")
+
+
 def test_rescale_two_roundings(oracle):
     """out = fl(fl(acc) * fl(as*bs)), no FMA: differs from the one-rounding
     (double) product on some inputs, which a dropped rounding would fail."""
