@@ -17,6 +17,8 @@
 // row-contiguous stores of Y[m, n..n+3] per 32x32 block.
 #include "sdq_internal.h"
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace sdq {
@@ -416,20 +418,18 @@ __device__ __forceinline__ v4u raw_rsrc(const void* base, uint32_t range) {
   r.w = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
   return r;
 }
+// The compiler does not see hazards on inline-asm operands: a VALU write of
+// an SGPR (v_readfirstlane, or v_readlane reloading a spilled SGPR) needs 5
+// wait states before a vector-memory instruction reads that SGPR, and an
+// M0 write 1 before an LDS-DMA, so the asm starts with them.
 __device__ __forceinline__ void dma16(v4u rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
 }
 __device__ __forceinline__ uint32_t lds_addr32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
 }
-
-// A 16-byte store reads its data VGPRs after issue; a VALU write to them
-// needs wait states in between. The compiler inserts them, but counts a
-// scheduling fence (sched_barrier, which emits no code) as one, so the
-// epilogue's fenced groups give each store an explicit gap.
-__device__ __forceinline__ void store_data_gap() { asm volatile("s_nop 1"); }
 
 template <int BN, int BM, int WN, int WM, int STAGES, int EPI>
 __global__ void __launch_bounds__(WN* WM * 64, 1)
@@ -583,7 +583,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // One pipeline step (stage gs, k-fragment 0 in `k0`): `k1` receives
   // k-fragment 1 of stage gs, `nk0` k-fragment 0 of stage gs + 1. Each
   // MFMA slot is fenced with the memory instructions issued behind it.
-  auto step = [&](int gs, const Half& k0, Half& k1, Half& nk0) {
+  // Without `Dma`, the refill of buffer gs is left to the caller (a tile's
+  // last step: the buffer serves the epilogue first).
+  auto step = [&](auto dma_tag, int gs, const Half& k0, Half& k1, Half& nk0) {
+    constexpr bool Dma = decltype(dma_tag)::value;
     const char* cb = lds + (gs & (STAGES - 1)) * STAGE;
 #pragma unroll
     for (int i = 0; i < FN * FM; i++) {
@@ -600,12 +603,14 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
     for (int i = 0; i < FN * FM; i++) {
       mfma(k1, i);
-      if (i < LPW) dma_stage(i);
+      if (Dma && i < LPW) dma_stage(i);
       if (i < FN + FM) read_frag(nb, 0, i, nk0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    advance();
+    if (Dma) advance();
   };
+  const std::true_type with_dma;
+  const std::false_type defer_dma;
 
   // prologue: STAGES stages in flight, stage 0 landed
 #pragma unroll
@@ -629,21 +634,37 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       reinterpret_cast<char*>(partials) + ((int64_t)blockIdx.x * NW + w) * (FN * FM * 4) * 1024,
       (short)0, FN * FM * 4 * 1024, kRsrcWord3);
-  const int nl0 = wn * FN * 32 + (lane >> 5) * 4;
-  const int ml0 = wm * FM * 32 + (lane & 31);
+  // Epilogue lane roles. MFMA layout: lane holds row lr of a 32x32 block,
+  // 4-column chunks 2g + lh (g = 0..3). Row layout, after the transpose
+  // through LDS: lane holds rows rr + 8i (i = 0..3), chunk rc, so eight
+  // consecutive lanes store one 128-byte row segment.
+  const int lr = lane & 31, lh = lane >> 5;
+  const int rr = lane >> 3, rc = lane & 7;
   const int ldy4 = (int)N * 4;
+  const int wrow = wm * FM * 32, wcol = wn * FN * 32;  // this wave's block in the tile
+  const int voff_lane = (wrow + rr) * ldy4 + (wcol + 4 * rc) * 4;
   int gs = 0;
   for (int j = 0; j < nseg; j++) {
 #pragma unroll
     for (int a = 0; a < FN; a++)
 #pragma unroll
       for (int b = 0; b < FM; b++) acc[a][b] = v16i{};
-    const int nst = kend(j) - kbeg(j);  // even
-    for (int q = 0; q < nst; q += 2) {
-      step(gs, hx, hz, hy);
-      step(gs + 1, hy, hz, hx);
+    const int nst = kend(j) - kbeg(j);  // even, >= 2
+    for (int q = 2; q < nst; q += 2) {
+      step(with_dma, gs, hx, hz, hy);
+      step(with_dma, gs + 1, hy, hz, hx);
       gs += 2;
     }
+    step(with_dma, gs, hx, hz, hy);
+    step(defer_dma, gs + 1, hy, hz, hx);
+    // The buffer of the tile's last stage is free (every wave read it before
+    // the last barrier) and its refill is deferred: this wave's four 1 KB
+    // DMA slots in it are the wave's transpose scratch, slot t holding
+    // block rows 8t..8t+7 (128 bytes each, 16-byte chunks XOR-swizzled by
+    // the row so both access patterns are bank-conflict free). Only this
+    // wave writes these slots, now and in the deferred refill.
+    char* scr = lds + ((gs + 1) & (STAGES - 1)) * STAGE + w * 1024;
+    gs += 2;
     // The staggered tile's first part parks its partial sums in this
     // wave's slot; its last part adds them back before the epilogue.
     const bool park = s0 > 0 && j == 0;
@@ -655,41 +676,62 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int64_t ybase = ((int64_t)tm * BM * N + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<char*>(Y) + ybase, (short)0, kBigRange, kRsrcWord3);
-    __amdgpu_buffer_rsrc_t rr = yr;
-    if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID)
-      rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(epi.resid) + (ybase >> 2),
-                                             (short)0, kBigRange, kRsrcWord3);
-    const int voff_lane = ml0 * ldy4 + nl0 * 4;
-    const int64_t mrow0 = (int64_t)tm * BM + ml0;
-    const int64_t ncol0 = (int64_t)tn * BN + nl0;
+    const bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        has_x ? const_cast<float*>(epi.resid) + (ybase >> 2) : static_cast<float*>(Y), (short)0,
+        has_x ? kBigRange : 0, kRsrcWord3);
+    const int64_t mrow0 = (int64_t)tm * BM + wrow + rr;
+    const int64_t ncol0 = (int64_t)tn * BN + wcol + 4 * rc;
 #pragma unroll
     for (int a = 0; a < FN; a++) {
+      const int cl = wcol + a * 32 + 4 * rc;  // tile column of this lane's chunk
+      const bool n_ok = ncol0 + a * 32 < N;
+      const float4 s4 = *reinterpret_cast<const float4*>(&colb[par][0][cl]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&colb[par][1][cl]);
+      const float4 g4 = *reinterpret_cast<const float4*>(&colb[par][2][cl]);
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int nl = nl0 + a * 32 + 8 * g;
-        const bool n_ok = ncol0 + a * 32 + 8 * g < N;
-        const float4 s4 = *reinterpret_cast<const float4*>(&colb[par][0][nl]);
-        const float4 b4 = *reinterpret_cast<const float4*>(&colb[par][1][nl]);
-        const float4 g4 = *reinterpret_cast<const float4*>(&colb[par][2][nl]);
+      for (int b = 0; b < FM; b++) {
+        v16i c = acc[a][b];
+        if (park) {
 #pragma unroll
-        for (int b = 0; b < FM; b++) {
-          const int idx = (a * FM + b) * 4 + g;
-          const v16i& cc = acc[a][b];
-          v4i c4 = {cc[4 * g], cc[4 * g + 1], cc[4 * g + 2], cc[4 * g + 3]};
-          if (park) {
-            __builtin_amdgcn_raw_buffer_store_b128(c4, pr, (int)lane_off, idx * 1024, 0);
-            store_data_gap();
-            continue;
+          for (int g = 0; g < 4; g++) {
+            const v4i c4 = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(c4, pr, (int)lane_off + ((a * FM + b) * 4 + g) * 1024,
+                                                   0, 0);
           }
-          if (unpark) c4 += __builtin_amdgcn_raw_buffer_load_b128(pr, (int)lane_off, idx * 1024, 0);
-          const bool ok = n_ok && (mrow0 + b * 32 < M);
-          const int voff = ok ? voff_lane : kOutOfRange;
-          const int soff = b * 32 * ldy4 + (a * 32 + 8 * g) * 4;
+          continue;
+        }
+        if (unpark) {
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const v4i p4 = __builtin_amdgcn_raw_buffer_load_b128(
+                pr, (int)lane_off + ((a * FM + b) * 4 + g) * 1024, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) c[4 * g + r] += p4[r];
+          }
+        }
+        // transpose the block: MFMA layout -> scratch -> row layout
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const v4i c4 = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+          *reinterpret_cast<v4i*>(scr + (lr >> 3) * NW * 1024 + (lr & 7) * 128 +
+                                  (((2 * g + lh) ^ (lr & 7)) * 16)) = c4;
+        }
+        v4i t4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          t4[i] = *reinterpret_cast<const v4i*>(scr + i * NW * 1024 + rr * 128 + ((rc ^ rr) * 16));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int rl = b * 32 + 8 * i;  // block row offset of this store
+          const bool ok = n_ok && (mrow0 + rl < M);
+          // All offsets in the VGPR, soffset 0: the compiler then inserts
+          // the wait states a wide store's data VGPRs need before reuse.
+          const int voff = ok ? voff_lane + rl * ldy4 + a * 128 : kOutOfRange;
           if constexpr (EPI == SDQ_EPI_ACC) {
-            __builtin_amdgcn_raw_buffer_store_b128(c4, yr, voff, soff, 0);
-            store_data_gap();
+            __builtin_amdgcn_raw_buffer_store_b128(t4[i], yr, voff, 0, 0);
           } else {
-            const float as_m = rowb[par][ml0 + b * 32];
+            const float as_m = rowb[par][wrow + rl + rr];
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
             const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
             const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
@@ -697,7 +739,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
             for (int r = 0; r < 4; r++) {
               const float sc = as_m * sv[r];
-              const float af = (float)c4[r];
+              const float af = (float)t4[i][r];
               v[r] = epi.kzero ? 0.f : af * sc;
             }
             if (epi.bias) {
@@ -708,7 +750,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
               for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
             } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
-              const v4f x = __builtin_amdgcn_raw_buffer_load_b128(rr, voff, soff, 0);
+              const v4f x = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, 0, 0);
               if constexpr (EPI == SDQ_EPI_RESID) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
@@ -724,14 +766,18 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
               }
             }
             const v4f out = {v[0], v[1], v[2], v[3]};
-            __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, soff, 0);
-            store_data_gap();
+            __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, 0, 0);
           }
         }
-        // keep the scheduler from hoisting every group's operands at once
+        // keep the scheduler from hoisting every block's operands at once
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // this wave's scratch reads are done: the deferred refill may land
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(63) & ~(15 << 8));
+#pragma unroll
+    for (int t = 0; t < LPW; t++) dma_stage(t);
+    advance();
   }
   // the cursor's zero-range loads past the end still land in LDS
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
