@@ -630,6 +630,9 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // hardware drops on stores and reads as zero on loads.
   constexpr int kOutOfRange = (int)0x80000000u;
   constexpr int kBigRange = 0x7FFFFFF0;
+  // Output rows are written once, in whole 128-byte segments: streaming
+  // (non-temporal) stores keep them from displacing the operand panels in L2.
+  constexpr int kStreamStore = 2;
   // this wave's scratch slot for the staggered tile's partial sums
   __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       reinterpret_cast<char*>(partials) + ((int64_t)blockIdx.x * NW + w) * (FN * FM * 4) * 1024,
@@ -729,7 +732,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
           // the wait states a wide store's data VGPRs need before reuse.
           const int voff = ok ? voff_lane + rl * ldy4 + a * 128 : kOutOfRange;
           if constexpr (EPI == SDQ_EPI_ACC) {
-            __builtin_amdgcn_raw_buffer_store_b128(t4[i], yr, voff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(t4[i], yr, voff, 0, kStreamStore);
           } else {
             const float as_m = rowb[par][wrow + rl + rr];
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
@@ -766,7 +769,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
               }
             }
             const v4f out = {v[0], v[1], v[2], v[3]};
-            __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(out, yr, voff, 0, kStreamStore);
           }
         }
         // keep the scheduler from hoisting every block's operands at once

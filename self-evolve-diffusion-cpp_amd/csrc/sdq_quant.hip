@@ -8,11 +8,12 @@
 //         rounded result leaves int32 give -127 (x86 cvtss2si "indefinite"
 //         INT_MIN, then clamped), src/core/qgemm.cpp:62-69.
 //
-// One workgroup owns one 32-row block (one fragment row) so it can emit
-// whole 1 KB fragments: every lane loads the 16 floats it will own in the
-// fragment, keeps up to CACHE fragments in registers across the amax
-// reduction (single HBM read when K <= NW*CACHE*32), and re-reads only the
-// tail beyond that.
+// Every lane loads the 16 floats it will own in a fragment slot (16 bytes of
+// one row), keeps up to CACHE such slices in registers across the amax
+// reduction (a single HBM read when the row fits), and re-reads only the
+// part of the row beyond that. The fragment-layout kernel works on 8-row
+// units (a quarter of a fragment row per workgroup) for a fine grid; the
+// row-major kernel (parity API) on 32-row blocks.
 #include "sdq_internal.h"
 
 #pragma clang fp contract(off)
@@ -22,6 +23,12 @@ namespace {
 
 constexpr int kQuantWaves = 16;
 constexpr int kQuantCache = 6;  // 16 waves x 6 frags x 32 = K <= 3072 in one pass
+// Fragment-layout quantizer: 8-row units, 8 waves, 3 fragment groups (of 4
+// fragments) cached per lane = K <= 3072 read once (measured 5.2 TB/s at
+// M=27280, K=3072 on MI355X vs 3.2 TB/s for whole 32-row fragment rows).
+constexpr int kQuantRows = 8;
+constexpr int kQuantUnitWaves = 8;
+constexpr int kQuantUnitCache = 3;
 
 __device__ __forceinline__ int quant_one(float v, float inv) {
   const float y = v * inv;
@@ -74,6 +81,7 @@ __device__ __forceinline__ uint4 pack16(const float v[16], float inv) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Row-major output variant (the parity API): one workgroup per 32 rows.
 template <int NW, int CACHE, bool FRAG_OUT>
 __global__ void __launch_bounds__(NW * 64)
 act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, int64_t KFp,
@@ -149,6 +157,86 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
   }
 }
 
+// Fragment-layout quantizer over R-row units (R = 8 or 16: a quarter or half
+// of a fragment row), for a finer grid than one 32-row fragment row per
+// workgroup (fewer idle CUs in the last wave of workgroups). Lane l owns
+// row unit*R + (l % R), half h = (l / R) & 1 of fragment g*F + l / (2R),
+// F = 32 / R fragments per group: the fragment slot (row & 31) + 32h, 16
+// bytes, so each fragment is written as two contiguous runs of 16R bytes.
+template <int R, int NW, int CACHE>
+__global__ void __launch_bounds__(NW * 64)
+act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
+                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
+  static_assert(R == 8 || R == 16, "unit height");
+  constexpr int F = 32 / R;  // fragments per lane group
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (cc.bias_pad) cc.bias_pad[i] = i < cc.N ? cc.bias[i] : 0.f;
+    if (cc.gate_pad) cc.gate_pad[i] = i < cc.N ? cc.gate[i] : 0.f;
+  }
+  const int w = threadIdx.x >> 6;
+  const int l = threadIdx.x & 63;
+  const int64_t unit = blockIdx.x;
+  const int64_t row = unit * R + (l % R);
+  const bool row_ok = row < M;
+  const float* rowp = A + (row_ok ? row : 0) * K;
+  const int sub = l / (2 * R);         // fragment within the group
+  const int half = (l / R) & 1;
+  const int kg = half * 16;            // k offset inside the fragment
+  const int64_t ng = KFp / F;          // fragment groups (KFp is a multiple of 8)
+  const int slot = (int)((row & 31) + half * 32) * 16;
+
+  float cache[CACHE][16];
+  float mx = 0.f;
+#pragma unroll
+  for (int c = 0; c < CACHE; c++) {
+    const int64_t g = w + (int64_t)c * NW;
+    if (g < ng) {
+      load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, cache[c]);
+      mx = amax16(cache[c], mx);
+    }
+  }
+  for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
+    float t[16];
+    load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
+    mx = amax16(t, mx);
+  }
+  // the lanes l + R*j (j = 0 .. 64/R - 1) hold the same row
+#pragma unroll
+  for (int d = R; d < 64; d *= 2) {
+    const float o = __shfl_xor(mx, d);
+    mx = (mx < o) ? o : mx;
+  }
+  __shared__ float red[NW][R];
+  if (l < R) red[w][l] = mx;
+  __syncthreads();
+  mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; i++) {
+    const float r = red[i][l % R];
+    mx = (mx < r) ? r : mx;
+  }
+  float sc = mx / 127.f;
+  if (sc == 0.f) sc = 1.f;
+  const float inv = 1.f / sc;
+  if (w == 0 && l < R && row_ok) as[row] = sc;
+
+  int8_t* base = out + (unit / F) * KFp * 1024 + slot;
+  auto emit = [&](int64_t g, const float v[16]) {
+    *reinterpret_cast<uint4*>(base + (g * F + sub) * 1024) = pack16(v, inv);
+  };
+#pragma unroll
+  for (int c = 0; c < CACHE; c++) {
+    const int64_t g = w + (int64_t)c * NW;
+    if (g < ng) emit(g, cache[c]);
+  }
+  for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
+    float t[16];
+    load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
+    emit(g, t);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -156,9 +244,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
                                   int8_t* at, float* as, const ColCopy& cc, hipStream_t s) {
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
-  const int64_t blocks = Mp / kFragRows;
-  hipLaunchKernelGGL((act_quant_kernel<kQuantWaves, kQuantCache, true>), dim3((unsigned)blocks),
-                     dim3(kQuantWaves * 64), 0, s, A, M, K, KFp, KFp, vec, at, as, cc);
+  const int64_t units = Mp / kQuantRows;
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache>),
+                     dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
+                     at, as, cc);
   return hipGetLastError();
 }
 
