@@ -431,12 +431,11 @@ __device__ __forceinline__ uint32_t lds_addr32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
 }
 
-template <int BN, int BM, int WN, int WM, int STAGES, int EPI>
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int EPI>
 __global__ void __launch_bounds__(WN* WM * 64, 1)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
               int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger) {
-  constexpr int KS = 2;
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -446,13 +445,20 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(WFR % NW == 0 && AFR % NW == 0, "stage fragments must split evenly over waves");
   static_assert(NW % KS == 0, "waves must be a multiple of k-fragments per stage");
   static_assert(NW >= 4, "four waves load the per-tile operands");
-  static_assert(STAGES >= 3 && (STAGES - 1) * LPW < 64, "vmcnt range");
+  static_assert(KS == 2 || KS == 4, "k-fragments alternate between two register sets");
+  static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
   static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
   static_assert((STAGES & (STAGES - 1)) == 0, "ring index by mask");
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
+  // Epilogue transpose scratch: 4 KB per wave of its own when LDS has room,
+  // else the wave's DMA slots in the tile's last stage buffer (whose refill
+  // is then deferred until after the epilogue).
+  constexpr int kLdsPipe = STAGES * STAGE + (2 * 3 * BN + 2 * BM) * 4;
+  constexpr bool kOwnScratch = kLdsPipe + NW * 4096 <= 160 * 1024;
+  __shared__ __attribute__((aligned(1024))) char escr[kOwnScratch ? NW * 4096 : 16];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -580,34 +586,46 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int a = i / FM, b = i % FM;
     acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], acc[a][b], 0, 0, 0);
   };
-  // One pipeline step (stage gs, k-fragment 0 in `k0`): `k1` receives
-  // k-fragment 1 of stage gs, `nk0` k-fragment 0 of stage gs + 1. Each
-  // MFMA slot is fenced with the memory instructions issued behind it.
-  // Without `Dma`, the refill of buffer gs is left to the caller (a tile's
-  // last step: the buffer serves the epilogue first).
-  auto step = [&](auto dma_tag, int gs, const Half& k0, Half& k1, Half& nk0) {
+  // One pipeline step (stage gs) in KS sub-steps: sub-step j runs the MFMAs
+  // of k-fragment j from register set h0 / h1 (alternating), interleaved
+  // with the LDS reads of k-fragment j + 1 into the other set; the last
+  // sub-step reads the next stage's k-fragment 0 (into h0, as KS is even). Before the
+  // last sub-step: this wave's loads of stage gs+1 landed (vmcnt), every
+  // wave finished reading buffer gs (lgkmcnt 0 + barrier), so the last
+  // sub-step also refills buffer gs with the stage STAGES ahead. Each MFMA
+  // slot is fenced with the memory instructions issued behind it. Without
+  // `Dma`, the refill is left to the caller (a tile's last step, whose
+  // buffer serves the epilogue first).
+  Half h0, h1;
+  auto sub = [&](auto dma_tag, auto j_tag, int gs, const Half& cur, Half& nxt) {
     constexpr bool Dma = decltype(dma_tag)::value;
-    const char* cb = lds + (gs & (STAGES - 1)) * STAGE;
-#pragma unroll
-    for (int i = 0; i < FN * FM; i++) {
-      mfma(k0, i);
-      if (i < FN + FM) read_frag(cb, 1, i, k1);
+    constexpr int j = decltype(j_tag)::value;
+    if constexpr (j == KS - 1) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW) & ~(15 << 8));
+      asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     }
-    // this wave's loads of stage gs+1 landed; every wave finished reading
-    // buffer gs, so it can be refilled
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW) & ~(15 << 8));
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    const char* nb = lds + ((gs + 1) & (STAGES - 1)) * STAGE;
+    const char* cb = lds + ((j == KS - 1 ? gs + 1 : gs) & (STAGES - 1)) * STAGE;
 #pragma unroll
     for (int i = 0; i < FN * FM; i++) {
-      mfma(k1, i);
-      if (Dma && i < LPW) dma_stage(i);
-      if (i < FN + FM) read_frag(nb, 0, i, nk0);
+      mfma(cur, i);
+      if constexpr (j == KS - 1) {
+        if (Dma && i < LPW) dma_stage(i);
+        if (i < FN + FM) read_frag(cb, 0, i, nxt);
+      } else {
+        if (i < FN + FM) read_frag(cb, j + 1, i, nxt);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (Dma) advance();
+  };
+  auto step = [&](auto dma_tag, int gs) {
+    sub(dma_tag, std::integral_constant<int, 0>{}, gs, h0, h1);
+    sub(dma_tag, std::integral_constant<int, 1>{}, gs, h1, h0);
+    if constexpr (KS == 4) {
+      sub(dma_tag, std::integral_constant<int, 2>{}, gs, h0, h1);
+      sub(dma_tag, std::integral_constant<int, 3>{}, gs, h1, h0);
+    }
+    if (decltype(dma_tag)::value) advance();
   };
   const std::true_type with_dma;
   const std::false_type defer_dma;
@@ -621,9 +639,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
   asm volatile("s_barrier" ::: "memory");
-  Half hx, hy, hz;
 #pragma unroll
-  for (int f = 0; f < FN + FM; f++) read_frag(lds, 0, f, hx);
+  for (int f = 0; f < FN + FM; f++) read_frag(lds, 0, f, h0);
 
   // Epilogue memory goes through buffer descriptors too: masked lanes
   // (outside M x N) get an offset beyond the descriptor's range, which the
@@ -652,22 +669,25 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     for (int a = 0; a < FN; a++)
 #pragma unroll
       for (int b = 0; b < FM; b++) acc[a][b] = v16i{};
-    const int nst = kend(j) - kbeg(j);  // even, >= 2
-    for (int q = 2; q < nst; q += 2) {
-      step(with_dma, gs, hx, hz, hy);
-      step(with_dma, gs + 1, hy, hz, hx);
-      gs += 2;
-    }
-    step(with_dma, gs, hx, hz, hy);
-    step(defer_dma, gs + 1, hy, hz, hx);
-    // The buffer of the tile's last stage is free (every wave read it before
-    // the last barrier) and its refill is deferred: this wave's four 1 KB
-    // DMA slots in it are the wave's transpose scratch, slot t holding
-    // block rows 8t..8t+7 (128 bytes each, 16-byte chunks XOR-swizzled by
-    // the row so both access patterns are bank-conflict free). Only this
+    const int nst = kend(j) - kbeg(j);  // >= 1
+    // Transpose scratch of this wave: four 1 KB slots (stride kSlot), slot
+    // t holding block rows 8t..8t+7 (128 bytes each, 16-byte chunks
+    // XOR-swizzled by the row so both access patterns are bank-conflict
+    // free). Without room of its own, the slots are this wave's four DMA
+    // slots in the buffer of the tile's last stage: every wave read that
+    // buffer before the last barrier, its refill is deferred, and only this
     // wave writes these slots, now and in the deferred refill.
-    char* scr = lds + ((gs + 1) & (STAGES - 1)) * STAGE + w * 1024;
-    gs += 2;
+    char* scr;
+    if constexpr (kOwnScratch) {
+      for (int q = 0; q < nst; q++) step(with_dma, gs++);
+      scr = escr + w * 4096;
+    } else {
+      for (int q = 1; q < nst; q++) step(with_dma, gs++);
+      step(defer_dma, gs);
+      scr = lds + (gs & (STAGES - 1)) * STAGE + w * 1024;
+      gs++;
+    }
+    constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
     // The staggered tile's first part parks its partial sums in this
     // wave's slot; its last part adds them back before the epilogue.
     const bool park = s0 > 0 && j == 0;
@@ -685,6 +705,11 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
         has_x ? kBigRange : 0, kRsrcWord3);
     const int64_t mrow0 = (int64_t)tm * BM + wrow + rr;
     const int64_t ncol0 = (int64_t)tn * BN + wcol + 4 * rc;
+    // Opaque copy of the lane's offset: keeps the compiler from hoisting the
+    // per-row output offsets out of the tile loop (they would stay live
+    // across the main loop and spill).
+    int vlane = voff_lane;
+    asm volatile("" : "+v"(vlane));
 #pragma unroll
     for (int a = 0; a < FN; a++) {
       const int cl = wcol + a * 32 + 4 * rc;  // tile column of this lane's chunk
@@ -717,20 +742,20 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const v4i c4 = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-          *reinterpret_cast<v4i*>(scr + (lr >> 3) * NW * 1024 + (lr & 7) * 128 +
+          *reinterpret_cast<v4i*>(scr + (lr >> 3) * kSlot + (lr & 7) * 128 +
                                   (((2 * g + lh) ^ (lr & 7)) * 16)) = c4;
         }
         v4i t4[4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          t4[i] = *reinterpret_cast<const v4i*>(scr + i * NW * 1024 + rr * 128 + ((rc ^ rr) * 16));
+          t4[i] = *reinterpret_cast<const v4i*>(scr + i * kSlot + rr * 128 + ((rc ^ rr) * 16));
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int rl = b * 32 + 8 * i;  // block row offset of this store
           const bool ok = n_ok && (mrow0 + rl < M);
           // All offsets in the VGPR, soffset 0: the compiler then inserts
           // the wait states a wide store's data VGPRs need before reuse.
-          const int voff = ok ? voff_lane + rl * ldy4 + a * 128 : kOutOfRange;
+          const int voff = ok ? vlane + rl * ldy4 + a * 128 : kOutOfRange;
           if constexpr (EPI == SDQ_EPI_ACC) {
             __builtin_amdgcn_raw_buffer_store_b128(t4[i], yr, voff, 0, kStreamStore);
           } else {
@@ -776,11 +801,13 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // this wave's scratch reads are done: the deferred refill may land
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(63) & ~(15 << 8));
+    if constexpr (!kOwnScratch) {
+      // this wave's scratch reads are done: the deferred refill may land
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(63) & ~(15 << 8));
 #pragma unroll
-    for (int t = 0; t < LPW; t++) dma_stage(t);
-    advance();
+      for (int t = 0; t < LPW; t++) dma_stage(t);
+      advance();
+    }
   }
   // the cursor's zero-range loads past the end still land in LDS
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -878,13 +905,12 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m;
   if (T <= 0) return hipSuccess;
-  static_assert(KS == 2, "the persistent pipeline moves two k-fragments per stage");
   if (KFp % KS != 0 || (KFp / KS) % 2 != 0 || KFp / KS < STAGES) return hipErrorInvalidValue;
   int G = (int)(T < max_groups ? T : max_groups);
   if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
   if ((size_t)G * BN * BM * 4 > aux.partials_bytes) return hipErrorInvalidValue;
 #define SDQ_LAUNCH_PERSIST(K)                                                                    \
-  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, STAGES, K>), dim3((unsigned)G),          \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, K>), dim3((unsigned)G),          \
                      dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
                      epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger)
   switch (epi.kind) {
