@@ -41,6 +41,8 @@ struct DevState {
   // is fastest: phase-shifted workgroups of one XCD re-fetch the weight
   // panels they share into L2 (3.5 GB instead of 2.0 GB per north-star call).
   int stagger = 1;
+  int stagger_spread = 0;  // SDQ_STAGGER_SPREAD: stages the phases span (0 = whole tile)
+  int stagger_xcd = 0;     // SDQ_STAGGER_XCD=1: phase per XCD
   hipDeviceProp_t prop{};
 };
 
@@ -102,6 +104,11 @@ int ensure_device(int dev) {
     const int v = std::atoi(st);
     if (v >= 1 && v <= 64) d.stagger = v;
   }
+  if (const char* st = std::getenv("SDQ_STAGGER_SPREAD")) {
+    const int v = std::atoi(st);
+    if (v >= 0 && v <= 4096) d.stagger_spread = v;
+  }
+  if (const char* st = std::getenv("SDQ_STAGGER_XCD")) d.stagger_xcd = std::atoi(st) ? 1 : 0;
   d.ready = true;
   return SDQ_OK;
 }
@@ -264,6 +271,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (ea.resid) vec = vec && aligned16(ea.resid);
   GemmAux aux{cc.bias_pad,    cc.gate_pad,          ws->sink,
               ws->partials,   ws->partials_bytes,   g_dev[w->device].stagger,
+              g_dev[w->device].stagger_spread, g_dev[w->device].stagger_xcd,
               g_dev[w->device].cu_count};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) return hip_error(e, "qgemm launch");

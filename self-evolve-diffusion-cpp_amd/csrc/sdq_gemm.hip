@@ -17,6 +17,7 @@
 // row-contiguous stores of Y[m, n..n+3] per 32x32 block.
 #include "sdq_internal.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 #pragma clang fp contract(off)
@@ -431,11 +432,12 @@ __device__ __forceinline__ uint32_t lds_addr32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
 }
 
-template <int BN, int BM, int WN, int WM, int KS, int STAGES, int EPI>
-__global__ void __launch_bounds__(WN* WM * 64, 1)
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI>
+__global__ void __launch_bounds__(WN* WM * 64, OCC)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
-              int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger) {
+              int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger,
+              int spread, int stagger_xcd) {
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -449,7 +451,6 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
   static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
-  static_assert((STAGES & (STAGES - 1)) == 0, "ring index by mask");
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
@@ -457,7 +458,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // else the wave's DMA slots in the tile's last stage buffer (whose refill
   // is then deferred until after the epilogue).
   constexpr int kLdsPipe = STAGES * STAGE + (2 * 3 * BN + 2 * BM) * 4;
-  constexpr bool kOwnScratch = kLdsPipe + NW * 4096 <= 160 * 1024;
+  constexpr bool kOwnScratch = OCC * (kLdsPipe + NW * 4096) <= 160 * 1024;
   __shared__ __attribute__((aligned(1024))) char escr[kOwnScratch ? NW * 4096 : 16];
 
   const int lane = threadIdx.x & 63;
@@ -495,10 +496,14 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // finishes the first tile's stages [0, s0) last, adding the saved
   // partial back (integer addition: exact). Segment j covers tile tseg(j),
   // stages [kbeg(j), kend(j)).
+  // The phases spread over `spread` stages (whole tile when 0); with
+  // stagger_xcd the phase is the XCD's (all workgroups of one XCD in step,
+  // sharing their L2) instead of the workgroup's within its XCD.
   int s0 = 0;
   if (ntile > 1 && stagger > 1) {
-    const int phase = ((int)blockIdx.x >> 3) % stagger;
-    s0 = ((phase * nks / stagger) / 2) * 2;  // even: stages run in pairs
+    const int phase = (stagger_xcd ? ((int)blockIdx.x & 7) : ((int)blockIdx.x >> 3)) % stagger;
+    const int span = (spread > 0 && spread < nks) ? spread : nks;
+    s0 = ((phase * span / stagger) / 2) * 2;  // even: stages run in pairs
   }
   const int nseg = s0 > 0 ? ntile + 1 : ntile;
   auto tseg = [&](int j) { return (s0 > 0 && j == ntile) ? 0 : j; };
@@ -528,7 +533,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // Load t (0..LPW-1) of the cursor's stage: WLD weight, then ALD
   // activation fragments, 1 KB each.
   auto dma_stage = [&](int t) {
-    const uint32_t buf = lds0 + (uint32_t)((cgs & (STAGES - 1)) * STAGE);
+    const uint32_t buf = lds0 + (uint32_t)(((unsigned)cgs % STAGES) * STAGE);
     if (t < WLD)
       dma16(wr, lane_off, (uint32_t)(wso + t * tso), buf + (uint32_t)(t * NW * 1024));
     else
@@ -605,7 +610,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
     }
-    const char* cb = lds + ((j == KS - 1 ? gs + 1 : gs) & (STAGES - 1)) * STAGE;
+    const char* cb = lds + ((unsigned)(j == KS - 1 ? gs + 1 : gs) % STAGES) * STAGE;
 #pragma unroll
     for (int i = 0; i < FN * FM; i++) {
       mfma(cur, i);
@@ -684,7 +689,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     } else {
       for (int q = 1; q < nst; q++) step(with_dma, gs++);
       step(defer_dma, gs);
-      scr = lds + (gs & (STAGES - 1)) * STAGE + w * 1024;
+      scr = lds + ((unsigned)gs % STAGES) * STAGE + w * 1024;
       gs++;
     }
     constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
@@ -898,7 +903,7 @@ hipError_t run_tiled(const int8_t* wt, const float* bs, const int8_t* at, const 
   return hipGetLastError();
 }
 
-template <int BN, int BM, int WN, int WM, int KS, int STAGES>
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC>
 hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, const float* as,
                        int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
                        const GemmAux& aux, int max_groups, hipStream_t s) {
@@ -910,9 +915,10 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
   if ((size_t)G * BN * BM * 4 > aux.partials_bytes) return hipErrorInvalidValue;
 #define SDQ_LAUNCH_PERSIST(K)                                                                    \
-  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, K>), dim3((unsigned)G),          \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K>), dim3((unsigned)G),     \
                      dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
-                     epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger)
+                     epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger,            \
+                     aux.stagger_spread, aux.stagger_xcd)
   switch (epi.kind) {
     case SDQ_EPI_NONE: SDQ_LAUNCH_PERSIST(SDQ_EPI_NONE); break;
     case SDQ_EPI_GELU: SDQ_LAUNCH_PERSIST(SDQ_EPI_GELU); break;
@@ -946,6 +952,9 @@ int gemm_cfg_bm(int cfg) {
     case kCfgSkinny4: return 128;
     case kCfg128x128: return 128;
     case kCfg256x256: return 256;
+    case kCfg256x256k4: return 256;
+    case kCfg256x128: return 256;  // activation rows padded to 256 either way
+    case kCfg128x256: return 256;
     default: return 256;
   }
 }
@@ -957,11 +966,18 @@ const char* gemm_cfg_name(int cfg) {
     case kCfgSkinny4: return "skinny128";
     case kCfg128x128: return "tile128x128";
     case kCfg256x256: return "tile256x256";
+    case kCfg256x256k4: return "tile256x256k4";
+    case kCfg256x128: return "tile256x128x2";
+    case kCfg128x256: return "tile128x256x2";
     default: return "?";
   }
 }
 
 int choose_gemm_cfg(int64_t M, int64_t N, int cu_count) {
+  if (const char* f = std::getenv("SDQ_FORCE_CFG")) {
+    const int c = std::atoi(f);
+    if (c >= kCfg128x128 && c < kCfgCount && M > 128) return c;
+  }
   if (M <= 32) return kCfgSkinny1;
   if (M <= 64) return kCfgSkinny2;
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
@@ -983,13 +999,28 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
     case kCfgSkinny4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg128x128:
       if (persist)
-        return run_persist<128, 128, 2, 2, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
-                                                 2 * aux.cu_count, s);
+        return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                    2 * aux.cu_count, s);
       return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
       if (persist)
-        return run_persist<256, 256, 2, 4, 2, 4>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
-                                                 aux.cu_count, s);
+        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                    aux.cu_count, s);
+      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case kCfg256x256k4:
+      if (persist)
+        return run_persist<256, 256, 2, 4, 4, 2, 1>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                    aux.cu_count, s);
+      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case kCfg256x128:
+      if (persist)
+        return run_persist<256, 128, 2, 2, 2, 3, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                    2 * aux.cu_count, s);
+      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case kCfg128x256:
+      if (persist)
+        return run_persist<128, 256, 2, 2, 2, 3, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+                                                    2 * aux.cu_count, s);
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;
   }
