@@ -43,6 +43,11 @@ def parse():
     ap.add_argument("--cpu-sample-rows", type=int, default=4096)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 FETCH/WRITE_SIZE summary used for roofline.traffic")
+    ap.add_argument("--config", default="ns", choices=["ns", "block", "ffn", "cross", "twin"],
+                    help="ns: the north-star qGEMM (the driver's bench line); block: one DiT "
+                         "block's linear stack at 720p/121f; ffn: the 256x256/9f FFN pair; "
+                         "cross: text/cross-attention and AdaLN projections; twin: the "
+                         "full twin-backbone linear stack (28 and 30 layers)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run a few steps plus a 1 GiB torch copy (the counter calibration "
                          "kernel) and exit; used under rocprofv3 --pmc")
@@ -82,6 +87,166 @@ def make_inputs(torch, dev, M, K, N, seed=1234):
     s = (amax / 127.0).to(torch.float32)
     del W
     return A, q.contiguous(), s.contiguous(), bias
+
+
+def _dev_weights(torch, dev, out, inp, seed):
+    """Synthetic packed int8 weights on the device: values in [-127, 127] and
+    per-row scales ~ 0.02*max|N(0,1)|/127 (timing only; parity is tested)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randint(-127, 128, (out, inp), generator=g, device=dev, dtype=torch.int8)
+    s = (torch.rand((out,), generator=g, device=dev) * 2e-4 + 4e-4).float()
+    b = torch.randn((out,), generator=g, device=dev) * 0.01
+    return q, s, b
+
+
+def _block_weights(torch, dev, dim, ffn, seed, fusion=True):
+    names = ("q", "k", "v", "o", "cq", "ck", "cv", "co", "kf", "vf", "fc1", "fc2")
+    lin = {}
+    for i, n in enumerate(names):
+        if n in ("kf", "vf") and not fusion:
+            continue
+        out, inp = (ffn, dim) if n == "fc1" else ((dim, ffn) if n == "fc2" else (dim, dim))
+        lin[n] = _dev_weights(torch, dev, out, inp, seed + i)
+    return lin
+
+
+def _block_io(torch, dev, M, Mc, Mt, dim, ffn):
+    r = lambda rows: torch.randn((rows, dim), device=dev)  # noqa: E731
+    return dict(M=M, Mc=Mc, Mt=Mt, h_sa=r(M), att=r(M), xq=r(M), ctx=r(Mc), tn=r(max(Mt, 1)),
+                xt=r(M), h_ffn=r(M), x=r(M), gate_sa=torch.randn(dim, device=dev),
+                gate_ffn=torch.randn(dim, device=dev),
+                qkv=torch.empty((M, 3 * dim), device=dev), cq=torch.empty((M, dim), device=dev),
+                ckv=torch.empty((Mc, 2 * dim), device=dev),
+                kvt=torch.empty((max(Mt, 1), 2 * dim), device=dev),
+                hid=torch.empty((M, ffn), device=dev))
+
+
+def _timed(torch, fn, warmup, steps):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _kernel_split(sdq, fn, steps):
+    sdq.profile_begin()
+    for _ in range(steps):
+        fn()
+    prof = sdq.profile_end()
+    return {k: round(t / steps, 5) for k, (n, t) in prof.items()}
+
+
+def bench_block(torch, sdq, args):
+    """Config 3: one DiT block's linear stack at 720p/121 frames (M=27280
+    video tokens, dim 3072, FFN 14336), text context 512 rows, fusion target
+    157 audio rows; q|k|v, cross k|v and k_fusion|v_fusion as single GEMMs."""
+    dev = torch.device("cuda:0")
+    dim, ffn, M, Mc, Mt = 3072, 14336, 27280, 512, 157
+    blk = sdq.DitBlock(_block_weights(torch, dev, dim, ffn, 11), True)
+    io = _block_io(torch, dev, M, Mc, Mt, dim, ffn)
+    fn = lambda: blk.forward(**io)  # noqa: E731
+    ms = _timed(torch, fn, max(args.warmup // 5, 2), max(args.steps // 10, 3))
+    ops = blk.ops(M, Mc, Mt)
+    split = _kernel_split(sdq, fn, 2)
+    return {"metric": "DiT block int8 linear stack (config 3), TOPS", "value": round(ops / ms / 1e9, 2),
+            "unit": "TOPS", "ms_per_block": round(ms, 4), "ops": ops, "dtype": "int8",
+            "config": {"workload": "DiT block linears M=27280 dim=3072 ffn=14336 ctx=512 "
+                                   "fusion=157", "kernel_ms_per_block": split}}
+
+
+def bench_ffn(torch, sdq, args):
+    """Config 2: the FFN pair at 256x256/9 frames as the config states it
+    (M=768): up 14336x3072 + GELU, then down 3072x14336 + gated residual."""
+    dev = torch.device("cuda:0")
+    M, dim, ffn = 768, 3072, 14336
+    q1, s1, b1 = _dev_weights(torch, dev, ffn, dim, 21)
+    q2, s2, b2 = _dev_weights(torch, dev, dim, ffn, 22)
+    w1, w2 = sdq.Weight.from_device(q1, s1), sdq.Weight.from_device(q2, s2)
+    x, h = torch.randn((M, dim), device=dev), torch.randn((M, dim), device=dev)
+    hid = torch.empty((M, ffn), device=dev)
+    gate = torch.randn(dim, device=dev)
+
+    def fn():
+        sdq.qlinear(w1, h, hid, kind="gelu", bias=b1)
+        sdq.qlinear(w2, hid, x, kind="gated", bias=b2, gate=gate, resid=x)
+    ms = _timed(torch, fn, args.warmup, args.steps)
+    ops = 2.0 * 2 * M * dim * ffn
+    return {"metric": "FFN pair int8 (config 2), TOPS", "value": round(ops / ms / 1e9, 2),
+            "unit": "TOPS", "ms_per_pair": round(ms, 5), "dtype": "int8",
+            "config": {"workload": "FFN up+GELU, down+gated residual, M=768",
+                       "kernel_ms": _kernel_split(sdq, fn, 5)}}
+
+
+def bench_cross(torch, sdq, args):
+    """Config 4: text_embedding.0 [512,4096]x[3072,4096], the real cross k|v
+    [512,3072]x[6144,3072], video-token Q [27280,3072]x[3072,3072], and the
+    AdaLN time projection [1,3072]x[18432,3072] (HBM-bound: reported in GB/s)."""
+    dev = torch.device("cuda:0")
+    out = {"metric": "cross-attention / AdaLN projections (config 4)", "unit": "us", "dtype": "int8",
+           "ops": {}}
+    for name, (M, K, N) in {"text_embedding.0": (512, 4096, 3072), "cross_kv": (512, 3072, 6144),
+                            "video_q": (27280, 3072, 3072), "adaln_tp1": (1, 3072, 18432)}.items():
+        q, s, b = _dev_weights(torch, dev, N, K, 31)
+        w = sdq.Weight.from_device(q, s)
+        A = torch.randn((M, K), device=dev)
+        Y = torch.empty((M, N), device=dev)
+        fn = lambda: sdq.qlinear(w, A, Y, kind="none", bias=b)  # noqa: E731
+        ms = _timed(torch, fn, args.warmup, args.steps)
+        bytes_ = 4.0 * M * K + N * K + 8.0 * N + 4.0 * M * N
+        out["ops"][name] = {"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
+                            "TOPS": round(2.0 * M * N * K / ms / 1e9, 2),
+                            "GBps": round(bytes_ / ms / 1e6, 1)}
+        w.free()
+    out["value"] = out["ops"]["adaln_tp1"]["us"]
+    return out
+
+
+def bench_twin(torch, sdq, args):
+    """Config 5: the twin-backbone linear stack at 256x256/9 frames: video
+    M=768 and audio M=157 tokens, dim 3072, FFN 14336, text context 512, every
+    layer a fusion layer (k_fusion|v_fusion on the other branch's tokens);
+    28 layers (as stated) and 30 (the real model). Weights are device-resident
+    (10.2 / 10.95 GB int8): the pass streams them once, an HBM-bound stack.
+    The one-time GPU repack of all blocks is timed separately."""
+    dev = torch.device("cuda:0")
+    dim, ffn, Mv, Ma, Mc = 3072, 14336, 768, 157, 512
+    res = {"metric": "twin-backbone int8 linear stack (config 5)", "unit": "ms", "dtype": "int8",
+           "layers": {}}
+    blocks = []
+    wbytes = 0
+    t_repack = 0.0
+    for layers in (28, 30):
+        while len(blocks) < 2 * layers:
+            lin = _block_weights(torch, dev, dim, ffn, 1000 + len(blocks))
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            blocks.append(sdq.DitBlock(lin, True))
+            torch.cuda.synchronize()
+            t_repack += time.perf_counter() - t0
+            wbytes += sum(q.numel() for q, _, _ in lin.values())
+            del lin
+        iov = _block_io(torch, dev, Mv, Mc, Ma, dim, ffn)
+        ioa = _block_io(torch, dev, Ma, Mc, Mv, dim, ffn)
+
+        def fn():
+            for i in range(layers):
+                blocks[2 * i].forward(**iov)
+                blocks[2 * i + 1].forward(**ioa)
+        ms = _timed(torch, fn, 2, max(args.steps // 10, 3))
+        ops = sum(blocks[2 * i].ops(Mv, Mc, Ma) + blocks[2 * i + 1].ops(Ma, Mc, Mv)
+                  for i in range(layers))
+        lw = wbytes * (2 * layers) / len(blocks)  # bytes of the blocks this pass uses
+        res["layers"][str(layers)] = {"ms_per_pass": round(ms, 4), "TOPS": round(ops / ms / 1e9, 2),
+                                      "weight_GB": round(lw / 1e9, 3),
+                                      "weight_stream_GBps": round(lw / ms / 1e6, 1),
+                                      "repack_ms_total": round(t_repack * 1e3, 1)}
+    res["value"] = res["layers"]["28"]["ms_per_pass"]
+    return res
 
 
 def cpu_baseline(args, K, N):
@@ -137,6 +302,14 @@ def main():
 
     if args.profile_pass:
         profile_pass(torch, sdq, args)
+        return
+    if args.config != "ns":
+        sdq.init(0)
+        fn = {"block": bench_block, "ffn": bench_ffn, "cross": bench_cross,
+              "twin": bench_twin}[args.config]
+        line = fn(torch, sdq, args)
+        line.update({"n_gpus": 1, "data": "synthetic, resident in HBM"})
+        print(json.dumps(line), flush=True)
         return
     M, K, N = args.M, args.K, args.N
     dev = torch.device("cuda:0")

@@ -246,7 +246,8 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   const int64_t N = w->N;
   if (M > (int64_t(1) << 30)) return set_error(SDQ_ERR_INVALID, "M too large");
 
-  const int cfg = choose_gemm_cfg(M, N, g_dev[w->device].cu_count);
+  const int cfg = choose_gemm_cfg(M, N, w->KFp, epi ? epi->kind : SDQ_EPI_NONE,
+                                  g_dev[w->device].cu_count);
   const int64_t Mp = round_up(M, gemm_cfg_bm(cfg));
   const size_t at_bytes = (size_t)(Mp / kFragRows) * (size_t)w->KFp * kFragBytes;
   const size_t col_cap = (size_t)(w->Np + kColPad);

@@ -16,6 +16,7 @@
 // m = l & 31, n = 8(r >> 2) + 4(l >> 5) + (r & 3), i.e. four 16-byte
 // row-contiguous stores of Y[m, n..n+3] per 32x32 block.
 #include "sdq_internal.h"
+#include "sdq_device.h"
 
 #include <cstdlib>
 #include <type_traits>
@@ -24,29 +25,9 @@
 
 namespace sdq {
 
-// Per-column operands of the persistent kernel, read by LDS-DMA.
-struct ColOps {
-  const float* scale;  // [>= tiles_n*BN + 256] zero padded
-  const float* bias;   // same size, or nullptr
-  const float* gate;   // same size, or nullptr
-};
-
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-// s_waitcnt immediate that waits until at most n vector-memory operations
-// are outstanding (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
-// vmcnt[5:4] at [15:14]; the other counters are left at their maximum).
-constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
-
-__device__ __forceinline__ float gelu_tanh(float v) {
-  // nn.GELU(approximate='tanh'), src/model/ovi_dit.cpp:132-142.
-  const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-  return 0.5f * v * (1.f + tanhf(u));
-}
+using namespace dev;
 
 __device__ __forceinline__ void load4(const float* __restrict__ p, int64_t n0, int64_t N, bool vec,
                                       float v[4]) {
@@ -404,34 +385,6 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // make a wait longer. Per-tile weight scales, bias, gate and activation
 // scales arrive by LDS-DMA into a double buffer after the tile's first
 // stage.
-// Raw buffer descriptor as an SGPR quad (base, range, 32-bit format) and
-// the 16-byte-per-lane LDS-DMA load, written as inline asm so that the
-// compiler does not track it: it would otherwise assume every LDS read may
-// alias every LDS-DMA in flight and drain vmcnt before each read. The
-// kernel orders these loads itself (explicit vmcnt waits + barriers).
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ v4u raw_rsrc(const void* base, uint32_t range) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  v4u r;
-  r.x = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xffffu);
-  r.z = __builtin_amdgcn_readfirstlane(range);
-  r.w = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
-  return r;
-}
-// The compiler does not see hazards on inline-asm operands: a VALU write of
-// an SGPR (v_readfirstlane, or v_readlane reloading a spilled SGPR) needs 5
-// wait states before a vector-memory instruction reads that SGPR, and an
-// M0 write 1 before an LDS-DMA, so the asm starts with them.
-__device__ __forceinline__ void dma16(v4u rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
-}
-__device__ __forceinline__ uint32_t lds_addr32(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
-}
-
 template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI>
 __global__ void __launch_bounds__(WN* WM * 64, OCC)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
@@ -973,7 +926,7 @@ const char* gemm_cfg_name(int cfg) {
   }
 }
 
-int choose_gemm_cfg(int64_t M, int64_t N, int cu_count) {
+int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_count) {
   if (const char* f = std::getenv("SDQ_FORCE_CFG")) {
     const int c = std::atoi(f);
     if (c >= kCfg128x128 && c < kCfgCount && M > 128) return c;

@@ -95,7 +95,7 @@ enum GemmCfg : int {
 };
 int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
 const char* gemm_cfg_name(int cfg);
-int choose_gemm_cfg(int64_t M, int64_t N, int cu_count);
+int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_count);
 
 // Extra buffers of the persistent GEMM path: bias / gate copied into
 // zero-padded buffers (nullptr when absent) so they can be moved by LDS-DMA,

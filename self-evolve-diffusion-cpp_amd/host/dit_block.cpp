@@ -1,0 +1,149 @@
+// sd::gpu::DitBlock — see sd/dit_block.h.
+#include "sd/dit_block.h"
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace sd {
+namespace gpu {
+
+namespace {
+
+void need(bool ok, const std::string& msg) {
+  if (!ok) throw std::runtime_error("DitBlock: " + msg);
+}
+
+}  // namespace
+
+DitBlock::DitBlock(const LinearPart (&l)[kCount], bool fusion, bool on_device) : fusion_(fusion) {
+  dim_ = l[Q].in;
+  ffn_ = l[FC1].out;
+  for (int i : {Q, K, V, O, CQ, CK, CV, CO})
+    need(l[i].in == dim_ && l[i].out == dim_, "attention Linears must be [dim,dim]");
+  if (fusion) need(l[KF].in == dim_ && l[KF].out == dim_ && l[VF].in == dim_ && l[VF].out == dim_,
+                   "fusion Linears must be [dim,dim]");
+  need(l[FC1].in == dim_ && l[FC2].in == ffn_ && l[FC2].out == dim_, "ffn shapes");
+  qkv_ = QLinear(std::vector<LinearPart>{l[Q], l[K], l[V]}, on_device);
+  o_ = QLinear(std::vector<LinearPart>{l[O]}, on_device);
+  cq_ = QLinear(std::vector<LinearPart>{l[CQ]}, on_device);
+  ckv_ = QLinear(std::vector<LinearPart>{l[CK], l[CV]}, on_device);
+  if (fusion) kvf_ = QLinear(std::vector<LinearPart>{l[KF], l[VF]}, on_device);
+  co_ = QLinear(std::vector<LinearPart>{l[CO]}, on_device);
+  fc1_ = QLinear(std::vector<LinearPart>{l[FC1]}, on_device);
+  fc2_ = QLinear(std::vector<LinearPart>{l[FC2]}, on_device);
+}
+
+void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
+  need(io.M >= 0 && io.Mc >= 0 && io.Mt >= 0, "negative row count");
+  need(io.x && io.gate_sa && io.gate_ffn, "x and gates are required");
+  // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-189, 168-174)
+  qkv_.forward_device(io.h_sa, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.qkv, s);
+  o_.forward_device(io.att, io.M, SDQ_EPI_GATED, io.gate_sa, io.x, io.x, s);
+  // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
+  // the other branch, then x += o(xt)                (ovi_dit.cpp:206-241)
+  cq_.forward_device(io.xq, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.cq, s);
+  if (io.Mc > 0) ckv_.forward_device(io.ctx, io.Mc, SDQ_EPI_NONE, nullptr, nullptr, io.ckv, s);
+  if (fusion_ && io.Mt > 0)
+    kvf_.forward_device(io.tn, io.Mt, SDQ_EPI_NONE, nullptr, nullptr, io.kvt, s);
+  co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
+  // ffn: hid = gelu(fc1(h)); x += fc2(hid) * e[5]    (ovi_dit.cpp:196-204)
+  fc1_.forward_device(io.h_ffn, io.M, SDQ_EPI_GELU, nullptr, nullptr, io.hid, s);
+  fc2_.forward_device(io.hid, io.M, SDQ_EPI_GATED, io.gate_ffn, io.x, io.x, s);
+}
+
+double DitBlock::ops(int64_t M, int64_t Mc, int64_t Mt) const {
+  const double d = (double)dim_, f = (double)ffn_;
+  double o = 2.0 * M * d * (3 * d) + 2.0 * M * d * d * 3 + 2.0 * Mc * d * (2 * d) +
+             2.0 * M * d * f * 2;
+  if (fusion_) o += 2.0 * Mt * d * (2 * d);
+  return o;
+}
+
+DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                             const std::string& prefix, int layer, int64_t dim, int64_t ffn_dim,
+                             bool fusion) {
+  const std::string B = prefix + "blocks." + std::to_string(layer) + ".";
+  LinearPart l[DitBlock::kCount];
+  l[DitBlock::Q] = linear_part_from_pack(pack, B + "self_attn.q", dim, dim);
+  l[DitBlock::K] = linear_part_from_pack(pack, B + "self_attn.k", dim, dim);
+  l[DitBlock::V] = linear_part_from_pack(pack, B + "self_attn.v", dim, dim);
+  l[DitBlock::O] = linear_part_from_pack(pack, B + "self_attn.o", dim, dim);
+  l[DitBlock::CQ] = linear_part_from_pack(pack, B + "cross_attn.q", dim, dim);
+  l[DitBlock::CK] = linear_part_from_pack(pack, B + "cross_attn.k", dim, dim);
+  l[DitBlock::CV] = linear_part_from_pack(pack, B + "cross_attn.v", dim, dim);
+  l[DitBlock::CO] = linear_part_from_pack(pack, B + "cross_attn.o", dim, dim);
+  if (fusion) {
+    l[DitBlock::KF] = linear_part_from_pack(pack, B + "cross_attn.k_fusion", dim, dim);
+    l[DitBlock::VF] = linear_part_from_pack(pack, B + "cross_attn.v_fusion", dim, dim);
+  }
+  l[DitBlock::FC1] = linear_part_from_pack(pack, B + "ffn.0", dim, ffn_dim);
+  l[DitBlock::FC2] = linear_part_from_pack(pack, B + "ffn.2", ffn_dim, dim);
+  return DitBlock(l, fusion, false);
+}
+
+}  // namespace gpu
+}  // namespace sd
+
+// ---- C shim (tests, bench, non-C++ callers) ----
+struct sd_dit_block {
+  sd::gpu::DitBlock blk;
+};
+
+namespace {
+thread_local std::string t_dit_err;
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    return SDQ_OK;
+  } catch (const std::exception& e) {
+    t_dit_err = e.what();
+    return SDQ_ERR_INVALID;
+  }
+}
+}  // namespace
+
+extern "C" {
+
+const char* sd_dit_last_error(void) { return t_dit_err.c_str(); }
+
+int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_block** out) {
+  if (!lin || !out) {
+    t_dit_err = "sd_dit_block_create: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  *out = nullptr;
+  return guarded([&] {
+    sd::gpu::LinearPart l[sd::gpu::DitBlock::kCount];
+    for (int i = 0; i < sd::gpu::DitBlock::kCount; i++) {
+      if (!fusion && (i == sd::gpu::DitBlock::KF || i == sd::gpu::DitBlock::VF)) continue;
+      l[i].w = lin[i].w;
+      l[i].scale = lin[i].scale;
+      l[i].bias = lin[i].bias;
+      l[i].out = lin[i].out;
+      l[i].in = lin[i].in;
+    }
+    *out = new sd_dit_block{sd::gpu::DitBlock(l, fusion != 0, on_device != 0)};
+  });
+}
+
+int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void* stream) {
+  if (!b || !io) {
+    t_dit_err = "sd_dit_block_forward: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { b->blk.forward_linears(*io, stream); });
+}
+
+int sd_dit_block_free(sd_dit_block* b) {
+  delete b;
+  return SDQ_OK;
+}
+
+double sd_dit_block_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {
+  return b ? b->blk.ops(M, Mc, Mt) : 0.0;
+}
+
+}  // extern "C"

@@ -1,6 +1,7 @@
 // sd::gpu::QLinear — see sd/qlinear.h.
 #include "sd/qlinear.h"
 
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -23,20 +24,97 @@ QLinear::QLinear(const Tensor& w, const Tensor& scale, const Tensor& bias) {
     throw std::runtime_error("QLinear: bias must be F32 [out]");
   check(sdq_weight_upload(w.ptr<int8_t>(), scale.ptr<float>(), N_, K_, nullptr, &w_),
         "QLinear: weight upload");
-  if (bias.data) {
-    bias_host_.assign(bias.ptr<float>(), bias.ptr<float>() + N_);
-    void* p = nullptr;
-    int rc = sdq_device_alloc((size_t)N_ * 4, &p);
-    if (rc == SDQ_OK) rc = sdq_memcpy(p, bias_host_.data(), (size_t)N_ * 4, SDQ_H2D, nullptr);
-    if (rc == SDQ_OK) rc = sdq_stream_sync(nullptr);
-    if (rc != SDQ_OK) {
-      sdq_device_free(p);
-      sdq_weight_free(w_);
-      w_ = nullptr;
-      check(rc, "QLinear: bias upload");
+  if (bias.data) upload_bias(bias.ptr<float>(), false);
+}
+
+void QLinear::upload_bias(const float* b, bool on_device) {
+  bias_host_.assign((size_t)N_, 0.f);
+  void* p = nullptr;
+  int rc = sdq_device_alloc((size_t)N_ * 4, &p);
+  if (rc == SDQ_OK) {
+    if (on_device) {
+      rc = sdq_memcpy(bias_host_.data(), b, (size_t)N_ * 4, SDQ_D2H, nullptr);
+      if (rc == SDQ_OK) rc = sdq_memcpy(p, b, (size_t)N_ * 4, SDQ_D2D, nullptr);
+    } else {
+      bias_host_.assign(b, b + N_);
+      rc = sdq_memcpy(p, bias_host_.data(), (size_t)N_ * 4, SDQ_H2D, nullptr);
     }
-    bias_dev_ = static_cast<float*>(p);
   }
+  if (rc == SDQ_OK) rc = sdq_stream_sync(nullptr);
+  if (rc != SDQ_OK) {
+    sdq_device_free(p);
+    sdq_weight_free(w_);
+    w_ = nullptr;
+    check(rc, "QLinear: bias upload");
+  }
+  bias_dev_ = static_cast<float*>(p);
+}
+
+QLinear::QLinear(const std::vector<LinearPart>& parts, bool on_device) {
+  if (parts.empty()) throw std::runtime_error("QLinear: no parts");
+  K_ = parts[0].in;
+  N_ = 0;
+  bool any_bias = false, all_bias = true;
+  for (const LinearPart& p : parts) {
+    if (!p.w || !p.scale || p.out <= 0 || p.in != K_)
+      throw std::runtime_error("QLinear: parts must share in_features and have weights");
+    N_ += p.out;
+    any_bias = any_bias || p.bias;
+    all_bias = all_bias && p.bias;
+  }
+  if (any_bias && !all_bias) throw std::runtime_error("QLinear: bias on some parts only");
+  const size_t wbytes = (size_t)N_ * (size_t)K_;
+  if (!on_device) {
+    std::vector<int8_t> w(wbytes);
+    std::vector<float> sc((size_t)N_), b(any_bias ? (size_t)N_ : 0);
+    size_t r = 0;
+    for (const LinearPart& p : parts) {
+      std::memcpy(w.data() + r * K_, p.w, (size_t)p.out * K_);
+      std::memcpy(sc.data() + r, p.scale, (size_t)p.out * 4);
+      if (any_bias) std::memcpy(b.data() + r, p.bias, (size_t)p.out * 4);
+      r += (size_t)p.out;
+    }
+    check(sdq_weight_upload(w.data(), sc.data(), N_, K_, nullptr, &w_), "QLinear: weight upload");
+    if (any_bias) upload_bias(b.data(), false);
+    return;
+  }
+  // device parts: concatenate into temporaries, repack on the GPU
+  void *tw = nullptr, *ts = nullptr, *tb = nullptr;
+  int rc = sdq_device_alloc(wbytes, &tw);
+  if (rc == SDQ_OK) rc = sdq_device_alloc((size_t)N_ * 4, &ts);
+  if (rc == SDQ_OK && any_bias) rc = sdq_device_alloc((size_t)N_ * 4, &tb);
+  size_t r = 0;
+  for (const LinearPart& p : parts) {
+    if (rc != SDQ_OK) break;
+    rc = sdq_memcpy(static_cast<int8_t*>(tw) + r * K_, p.w, (size_t)p.out * K_, SDQ_D2D, nullptr);
+    if (rc == SDQ_OK)
+      rc = sdq_memcpy(static_cast<float*>(ts) + r, p.scale, (size_t)p.out * 4, SDQ_D2D, nullptr);
+    if (rc == SDQ_OK && any_bias)
+      rc = sdq_memcpy(static_cast<float*>(tb) + r, p.bias, (size_t)p.out * 4, SDQ_D2D, nullptr);
+    r += (size_t)p.out;
+  }
+  if (rc == SDQ_OK)
+    rc = sdq_weight_upload_device(static_cast<const int8_t*>(tw), static_cast<const float*>(ts),
+                                  N_, K_, nullptr, &w_);
+  if (rc == SDQ_OK) rc = sdq_stream_sync(nullptr);
+  const std::string err = rc == SDQ_OK ? "" : sdq_last_error();
+  sdq_device_free(tw);
+  sdq_device_free(ts);
+  if (rc != SDQ_OK) {
+    sdq_device_free(tb);
+    sdq_weight_free(w_);
+    w_ = nullptr;
+    throw std::runtime_error("QLinear: device upload: " + err);
+  }
+  if (any_bias) {
+    try {
+      upload_bias(static_cast<const float*>(tb), true);
+    } catch (...) {
+      sdq_device_free(tb);
+      throw;
+    }
+  }
+  sdq_device_free(tb);
 }
 
 QLinear::QLinear(QLinear&& o) noexcept { *this = std::move(o); }
@@ -115,8 +193,8 @@ void QLinear::forward_device(const float* x, int64_t M, int kind, const float* g
   check(sdq_qlinear(w_, x, M, K_, &e, Y, stream), "QLinear::forward_device");
 }
 
-QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
-                          const std::string& base, int64_t in, int64_t out) {
+LinearPart linear_part_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                                 const std::string& base, int64_t in, int64_t out) {
   auto get = [&](const std::string& n) -> const Tensor& {
     auto it = pack.find(n);
     if (it == pack.end() || !it->second.data)
@@ -134,7 +212,18 @@ QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
   const Tensor& b = get(base + ".bias");
   if (b.dtype != DType::F32 || b.shape.size() != 1 || b.shape[0] != out)
     throw std::runtime_error("ovi_dit: bad shape for " + base + ".bias");
-  return QLinear(w, sc, b);
+  LinearPart p;
+  p.w = w.ptr<int8_t>();
+  p.scale = sc.ptr<float>();
+  p.bias = b.ptr<float>();
+  p.out = out;
+  p.in = in;
+  return p;
+}
+
+QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                          const std::string& base, int64_t in, int64_t out) {
+  return QLinear(std::vector<LinearPart>{linear_part_from_pack(pack, base, in, out)});
 }
 
 }  // namespace gpu

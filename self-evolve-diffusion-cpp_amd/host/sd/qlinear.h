@@ -19,11 +19,25 @@
 namespace sd {
 namespace gpu {
 
+// One [out,in] int8 Linear's arrays (all host or all device memory).
+struct LinearPart {
+  const int8_t* w = nullptr;     // [out,in] row-major
+  const float* scale = nullptr;  // [out], may be unaligned (.sdcpp v1)
+  const float* bias = nullptr;   // [out] or nullptr
+  int64_t out = 0, in = 0;
+};
+
 class QLinear {
  public:
   QLinear() = default;
   // w: I8 [out,in] view; scale: F32 [out] view; bias: F32 [out] or empty.
   QLinear(const Tensor& w, const Tensor& scale, const Tensor& bias);
+  // Several Linears that read the same input, concatenated along out (one
+  // weight [sum out, in]): bit-identical to running them separately, since
+  // activations are quantized per row and each output column depends only
+  // on its own weight row and scale. Parts in host memory, or in device
+  // memory with on_device (then the concatenation and repack stay on the GPU).
+  explicit QLinear(const std::vector<LinearPart>& parts, bool on_device = false);
   QLinear(const QLinear&) = delete;
   QLinear& operator=(const QLinear&) = delete;
   QLinear(QLinear&& o) noexcept;
@@ -50,6 +64,7 @@ class QLinear {
 
  private:
   void run_host(const Tensor& x, int kind, const Tensor* gate, Tensor* res, Tensor* y) const;
+  void upload_bias(const float* b, bool on_device);
   sdq_weight* w_ = nullptr;
   float* bias_dev_ = nullptr;
   std::vector<float> bias_host_;
@@ -62,6 +77,9 @@ class QLinear {
 // std::runtime_error("ovi_dit: …") like the reference otherwise.
 QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                           const std::string& base, int64_t in, int64_t out);
+// The same checks, returning the views as a LinearPart (host memory).
+LinearPart linear_part_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                                 const std::string& base, int64_t in, int64_t out);
 
 // Throws std::runtime_error with sdq_last_error() when rc != SDQ_OK.
 void check(int rc, const char* what);

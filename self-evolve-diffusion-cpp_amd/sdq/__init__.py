@@ -242,3 +242,110 @@ def profile_end() -> dict:
 
 def sync():
     _check(_lib.sdq_sync())
+
+
+# ---- the DiT block linear stack (C++ host mirror, lib/libsd_host.so) ----
+HOST_LIB_PATH = os.path.join(LIB_DIR, "libsd_host.so")
+_host = None
+
+# order of sd_dit_block_create's Linear array (include: host/sd/dit_block.h)
+BLOCK_LINEARS = ("q", "k", "v", "o", "cq", "ck", "cv", "co", "kf", "vf", "fc1", "fc2")
+
+
+class Linear(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("out", ctypes.c_int64), ("in_", ctypes.c_int64)]
+
+
+class BlockIO(ctypes.Structure):
+    _fields_ = [("M", ctypes.c_int64), ("Mc", ctypes.c_int64), ("Mt", ctypes.c_int64)] + [
+        (n, ctypes.c_void_p) for n in ("h_sa", "att", "gate_sa", "xq", "ctx", "tn", "xt",
+                                       "h_ffn", "gate_ffn", "qkv", "cq", "ckv", "kvt", "hid", "x")]
+
+
+def load_host_library(path: str = HOST_LIB_PATH):
+    """Load libsd_host.so (raises if it has not been built)."""
+    global _host
+    if _host is not None:
+        return _host
+    load_library()  # libsdq first (libsd_host links it)
+    if not os.path.exists(path):
+        raise RuntimeError(f"libsd_host.so not built: {path} (run __graft_entry__.build())")
+    h = ctypes.CDLL(path)
+    h.sd_dit_last_error.restype = ctypes.c_char_p
+    h.sd_dit_last_error.argtypes = []
+    h.sd_dit_block_create.restype = ctypes.c_int
+    h.sd_dit_block_create.argtypes = [ctypes.POINTER(Linear), ctypes.c_int, ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_void_p)]
+    h.sd_dit_block_forward.restype = ctypes.c_int
+    h.sd_dit_block_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO), ctypes.c_void_p]
+    h.sd_dit_block_free.restype = ctypes.c_int
+    h.sd_dit_block_free.argtypes = [ctypes.c_void_p]
+    h.sd_dit_block_ops.restype = ctypes.c_double
+    h.sd_dit_block_ops.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                   ctypes.c_int64]
+    _host = h
+    return h
+
+
+def _hcheck(rc):
+    if rc != OK:
+        raise SdqError(rc, _host.sd_dit_last_error().decode(errors="replace"))
+
+
+class DitBlock:
+    """One DiT block's int8 Linears on the GPU (sd::gpu::DitBlock).
+
+    lin: {name: (q int8 [out,in], scale f32 [out], bias f32 [out])} for the
+    names in BLOCK_LINEARS (kf/vf only with fusion); numpy arrays (host) or
+    torch device tensors (device)."""
+
+    def __init__(self, lin: dict, fusion: bool):
+        h = load_host_library()
+        arr = (Linear * len(BLOCK_LINEARS))()
+        on_device = None
+        keep = []
+        for i, name in enumerate(BLOCK_LINEARS):
+            if name not in lin:
+                if name in ("kf", "vf") and not fusion:
+                    continue
+                raise ValueError(f"DitBlock: missing Linear {name}")
+            q, s, b = lin[name]
+            dev = not isinstance(q, np.ndarray)
+            if on_device is None:
+                on_device = dev
+            elif on_device != dev:
+                raise ValueError("DitBlock: mix of host and device arrays")
+            if not dev:
+                q = np.ascontiguousarray(q, np.int8)
+                s = np.ascontiguousarray(s, np.float32)
+                b = None if b is None else np.ascontiguousarray(b, np.float32)
+            keep += [q, s, b]
+            arr[i].w, arr[i].scale, arr[i].bias = _ptr(q), _ptr(s), _ptr(b)
+            arr[i].out, arr[i].in_ = q.shape
+        self.h = ctypes.c_void_p()
+        _hcheck(h.sd_dit_block_create(arr, 1 if fusion else 0, 1 if on_device else 0,
+                                      ctypes.byref(self.h)))
+        self.fusion = fusion
+
+    def forward(self, stream=None, **io):
+        """io: M, Mc, Mt and the device tensors named in BlockIO."""
+        b = BlockIO()
+        b.M, b.Mc, b.Mt = int(io.get("M", 0)), int(io.get("Mc", 0)), int(io.get("Mt", 0))
+        for name, _ in BlockIO._fields_[3:]:
+            setattr(b, name, _ptr(io.get(name)))
+        _hcheck(_host.sd_dit_block_forward(self.h, ctypes.byref(b), _stream(stream)))
+
+    def ops(self, M, Mc=0, Mt=0) -> float:
+        return _host.sd_dit_block_ops(self.h, M, Mc, Mt)
+
+    def free(self):
+        if self.h is not None and self.h.value:
+            _host.sd_dit_block_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:  # pragma: no cover - interpreter shutdown
+            pass
