@@ -37,12 +37,6 @@ thread_local std::string t_err;
 struct DevState {
   bool ready = false;
   int cu_count = 0;
-  // Tile phases per XCD in the persistent GEMM (SDQ_STAGGER). 1 (no stagger)
-  // is fastest: phase-shifted workgroups of one XCD re-fetch the weight
-  // panels they share into L2 (3.5 GB instead of 2.0 GB per north-star call).
-  int stagger = 1;
-  int stagger_spread = 0;  // SDQ_STAGGER_SPREAD: stages the phases span (0 = whole tile)
-  int stagger_xcd = 0;     // SDQ_STAGGER_XCD=1: phase per XCD
   hipDeviceProp_t prop{};
 };
 
@@ -58,8 +52,6 @@ struct Workspace {
   float* cols = nullptr;  // [2][col_cap]: zero-padded bias, gate copies
   size_t col_cap = 0;
   float* sink = nullptr;  // 1 KB target of masked epilogue stores
-  void* partials = nullptr;  // staggered-tile partial sums, one slot per workgroup
-  size_t partials_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -100,15 +92,6 @@ int ensure_device(int dev) {
     return set_error(SDQ_ERR_NODEV, std::string("sdq kernels are built for gfx950, device is ") +
                                         d.prop.gcnArchName);
   d.cu_count = d.prop.multiProcessorCount;
-  if (const char* st = std::getenv("SDQ_STAGGER")) {
-    const int v = std::atoi(st);
-    if (v >= 1 && v <= 64) d.stagger = v;
-  }
-  if (const char* st = std::getenv("SDQ_STAGGER_SPREAD")) {
-    const int v = std::atoi(st);
-    if (v >= 0 && v <= 4096) d.stagger_spread = v;
-  }
-  if (const char* st = std::getenv("SDQ_STAGGER_XCD")) d.stagger_xcd = std::atoi(st) ? 1 : 0;
   d.ready = true;
   return SDQ_OK;
 }
@@ -148,8 +131,6 @@ int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t c
     size_t have = 0;
     rc = grow(s, reinterpret_cast<void**>(&w.sink), &have, 4096);
   }
-  // one 256x256 int32 tile per resident workgroup of the persistent GEMM
-  if (!rc) rc = grow(s, &w.partials, &w.partials_bytes, (size_t)g_dev[dev].cu_count * 256 * 256 * 4);
   if (rc) return rc;
   *out = &w;
   return SDQ_OK;
@@ -270,10 +251,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (ea.bias) vec = vec && aligned16(ea.bias);
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
-  GemmAux aux{cc.bias_pad,    cc.gate_pad,          ws->sink,
-              ws->partials,   ws->partials_bytes,   g_dev[w->device].stagger,
-              g_dev[w->device].stagger_spread, g_dev[w->device].stagger_xcd,
-              g_dev[w->device].cu_count};
+  GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) return hip_error(e, "qgemm launch");
   if (t_prof) {

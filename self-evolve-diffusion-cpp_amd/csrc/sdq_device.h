@@ -46,14 +46,24 @@ __device__ __forceinline__ v4u raw_rsrc(const void* base, uint32_t range) {
   r.w = 0x00020000u;  // gfx9 raw buffer: 32-bit data format
   return r;
 }
-// The compiler does not see hazards on inline-asm operands: a VALU write of
-// an SGPR (v_readfirstlane, or v_readlane reloading a spilled SGPR) needs 5
-// wait states before a vector-memory instruction reads that SGPR, and an
-// M0 write 1 before an LDS-DMA, so the asm starts with them.
+// The compiler does not see hazards on inline-asm operands: an M0 write
+// needs 1 wait state before an LDS-DMA, and a VALU write of an SGPR
+// (v_readfirstlane, or v_readlane reloading a spilled SGPR) 5 before a
+// vector-memory instruction reads that SGPR. NOP is the asm's leading
+// s_nop count: 0 covers M0 and is 4-5% faster in the main loop; 4 covers
+// both, for kernels whose SGPR spill reloads can land next to a DMA. The
+// CPU test suite scans every compiled kernel for both hazards.
+template <int NOP>
 __device__ __forceinline__ void dma16(v4u rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
+  static_assert(NOP == 0 || NOP == 4, "s_nop count");
+  if constexpr (NOP == 0)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
+  else
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr));
 }
 __device__ __forceinline__ uint32_t lds_addr32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);

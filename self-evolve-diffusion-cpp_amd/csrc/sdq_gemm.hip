@@ -385,12 +385,11 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // make a wait longer. Per-tile weight scales, bias, gate and activation
 // scales arrive by LDS-DMA into a double buffer after the tile's first
 // stage.
-template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI>
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI, bool BIAS>
 __global__ void __launch_bounds__(WN* WM * 64, OCC)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
-              int tiles_m, EpiArgs epi, void* Y, int4* __restrict__ partials, int stagger,
-              int spread, int stagger_xcd) {
+              int tiles_m, EpiArgs epi, void* Y) {
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -404,6 +403,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
   static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
+  // GELU's epilogue spills SGPRs; their reloads can sit next to a DMA
+  constexpr int kDmaNop = EPI == SDQ_EPI_GELU ? 4 : 0;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
@@ -431,7 +432,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int bid = (int)blockIdx.x + i * G;
     const int xcd = bid & 7, jx = bid >> 3, q8 = T >> 3, r8 = T & 7;
     const int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + jx;
-    constexpr int GROUP_M = 8;
+    constexpr int GROUP_M = 4;
     const int per_group = GROUP_M * tiles_n;
     const int g = lin / per_group;
     const int first_m = g * GROUP_M;
@@ -440,28 +441,6 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     tm = first_m + rem % gsz;
     tn = rem / gsz;
   };
-
-  // ---- work segments. Tiles finishing in lockstep on all CUs of an XCD
-  // would push their stores through the XCD's memory path in one burst, so
-  // workgroups are staggered: workgroup b starts its first tile at stage s0
-  // (a per-CU phase within the XCD), saves that tile's partial int32
-  // accumulators to its own scratch slot, runs its other tiles whole, and
-  // finishes the first tile's stages [0, s0) last, adding the saved
-  // partial back (integer addition: exact). Segment j covers tile tseg(j),
-  // stages [kbeg(j), kend(j)).
-  // The phases spread over `spread` stages (whole tile when 0); with
-  // stagger_xcd the phase is the XCD's (all workgroups of one XCD in step,
-  // sharing their L2) instead of the workgroup's within its XCD.
-  int s0 = 0;
-  if (ntile > 1 && stagger > 1) {
-    const int phase = (stagger_xcd ? ((int)blockIdx.x & 7) : ((int)blockIdx.x >> 3)) % stagger;
-    const int span = (spread > 0 && spread < nks) ? spread : nks;
-    s0 = ((phase * span / stagger) / 2) * 2;  // even: stages run in pairs
-  }
-  const int nseg = s0 > 0 ? ntile + 1 : ntile;
-  auto tseg = [&](int j) { return (s0 > 0 && j == ntile) ? 0 : j; };
-  auto kbeg = [&](int j) { return j == 0 ? s0 : 0; };
-  auto kend = [&](int j) { return (s0 > 0 && j == ntile) ? s0 : nks; };
 
   // ---- issue cursor: the next stage to load (segment cj, stage cks), with
   // buffer descriptors over that tile's weight / activation panels (raw
@@ -473,8 +452,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int wso0 = ((w / KS) * (int)KFp + (w % KS)) * 1024;
   const int tso = (NW / KS) * (int)KFp * 1024;
   const uint32_t lds0 = lds_addr32(lds) + (uint32_t)w * 1024u;
-  int cj = 0, cks = s0, cend = kend(0), ctm = 0, ctn = 0, cgs = 0;
-  int wso = wso0 + s0 * KS * 1024;
+  int cj = 0, cks = 0, ctm = 0, ctn = 0, cgs = 0;
+  int wso = wso0;
   bool col_due = true;  // the segment's first stage was issued; its column loads follow
   v4u wr, ar;
   auto set_tile = [&](int i) {
@@ -482,20 +461,20 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     wr = raw_rsrc(wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
     ar = raw_rsrc(at + (int64_t)ctm * apanel, (uint32_t)apanel);
   };
-  set_tile(tseg(0));
+  set_tile(0);
   // Load t (0..LPW-1) of the cursor's stage: WLD weight, then ALD
   // activation fragments, 1 KB each.
   auto dma_stage = [&](int t) {
     const uint32_t buf = lds0 + (uint32_t)(((unsigned)cgs % STAGES) * STAGE);
     if (t < WLD)
-      dma16(wr, lane_off, (uint32_t)(wso + t * tso), buf + (uint32_t)(t * NW * 1024));
+      dma16<kDmaNop>(wr, lane_off, (uint32_t)(wso + t * tso), buf + (uint32_t)(t * NW * 1024));
     else
-      dma16(ar, lane_off, (uint32_t)(wso + (t - WLD) * tso),
+      dma16<kDmaNop>(ar, lane_off, (uint32_t)(wso + (t - WLD) * tso),
             buf + (uint32_t)((WFR + (t - WLD) * NW) * 1024));
   };
   auto dma_row = [&](const float* src, int64_t off, int count, const float* dst) {
     if (lane * 4 < count)
-      dma16(raw_rsrc(src + off, (uint32_t)count * 4u), lane_off, 0u, lds_addr32(dst));
+      dma16<kDmaNop>(raw_rsrc(src + off, (uint32_t)count * 4u), lane_off, 0u, lds_addr32(dst));
   };
   // After a stage's loads: the per-tile column operands (once per segment,
   // younger than the segment's first stage), then the cursor moves on.
@@ -512,17 +491,15 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     }
     cgs++;
     wso += KS * 1024;
-    if (++cks == cend) {
-      if (++cj < nseg) {
-        cks = kbeg(cj);
-        cend = kend(cj);
-        wso = wso0 + cks * KS * 1024;
-        set_tile(tseg(cj));
+    if (++cks == nks) {
+      if (++cj < ntile) {
+        cks = 0;
+        wso = wso0;
+        set_tile(cj);
         col_due = true;
       } else {
         wr = raw_rsrc(wt, 0u);
         ar = raw_rsrc(at, 0u);
-        cend = -1;
       }
     }
   };
@@ -544,6 +521,11 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int a = i / FM, b = i % FM;
     acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], acc[a][b], 0, 0, 0);
   };
+  // A tile's first k-fragment starts from zero (no separate clearing pass).
+  auto mfma0 = [&](const Half& h, int i) {
+    const int a = i / FM, b = i % FM;
+    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], v16i{}, 0, 0, 0);
+  };
   // One pipeline step (stage gs) in KS sub-steps: sub-step j runs the MFMAs
   // of k-fragment j from register set h0 / h1 (alternating), interleaved
   // with the LDS reads of k-fragment j + 1 into the other set; the last
@@ -555,7 +537,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // `Dma`, the refill is left to the caller (a tile's last step, whose
   // buffer serves the epilogue first).
   Half h0, h1;
-  auto sub = [&](auto dma_tag, auto j_tag, int gs, const Half& cur, Half& nxt) {
+  auto sub = [&](auto dma_tag, auto j_tag, auto first_tag, int gs, const Half& cur, Half& nxt) {
     constexpr bool Dma = decltype(dma_tag)::value;
     constexpr int j = decltype(j_tag)::value;
     if constexpr (j == KS - 1) {
@@ -566,7 +548,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const char* cb = lds + ((unsigned)(j == KS - 1 ? gs + 1 : gs) % STAGES) * STAGE;
 #pragma unroll
     for (int i = 0; i < FN * FM; i++) {
-      mfma(cur, i);
+      if constexpr (decltype(first_tag)::value && j == 0)
+        mfma0(cur, i);
+      else
+        mfma(cur, i);
       if constexpr (j == KS - 1) {
         if (Dma && i < LPW) dma_stage(i);
         if (i < FN + FM) read_frag(cb, 0, i, nxt);
@@ -576,17 +561,19 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto step = [&](auto dma_tag, int gs) {
-    sub(dma_tag, std::integral_constant<int, 0>{}, gs, h0, h1);
-    sub(dma_tag, std::integral_constant<int, 1>{}, gs, h1, h0);
+  // first_tag: the tile's first stage (its k-fragment 0 starts from zero)
+  auto step = [&](auto dma_tag, int gs, auto first_tag) {
+    const std::false_type later;
+    sub(dma_tag, std::integral_constant<int, 0>{}, first_tag, gs, h0, h1);
+    sub(dma_tag, std::integral_constant<int, 1>{}, later, gs, h1, h0);
     if constexpr (KS == 4) {
-      sub(dma_tag, std::integral_constant<int, 2>{}, gs, h0, h1);
-      sub(dma_tag, std::integral_constant<int, 3>{}, gs, h1, h0);
+      sub(dma_tag, std::integral_constant<int, 2>{}, later, gs, h0, h1);
+      sub(dma_tag, std::integral_constant<int, 3>{}, later, gs, h1, h0);
     }
     if (decltype(dma_tag)::value) advance();
   };
-  const std::true_type with_dma;
-  const std::false_type defer_dma;
+  const std::true_type with_dma, first_stage;
+  const std::false_type defer_dma, next_stage;
 
   // prologue: STAGES stages in flight, stage 0 landed
 #pragma unroll
@@ -608,10 +595,6 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // Output rows are written once, in whole 128-byte segments: streaming
   // (non-temporal) stores keep them from displacing the operand panels in L2.
   constexpr int kStreamStore = 2;
-  // this wave's scratch slot for the staggered tile's partial sums
-  __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      reinterpret_cast<char*>(partials) + ((int64_t)blockIdx.x * NW + w) * (FN * FM * 4) * 1024,
-      (short)0, FN * FM * 4 * 1024, kRsrcWord3);
   // Epilogue lane roles. MFMA layout: lane holds row lr of a 32x32 block,
   // 4-column chunks 2g + lh (g = 0..3). Row layout, after the transpose
   // through LDS: lane holds rows rr + 8i (i = 0..3), chunk rc, so eight
@@ -622,12 +605,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int wrow = wm * FM * 32, wcol = wn * FN * 32;  // this wave's block in the tile
   const int voff_lane = (wrow + rr) * ldy4 + (wcol + 4 * rc) * 4;
   int gs = 0;
-  for (int j = 0; j < nseg; j++) {
-#pragma unroll
-    for (int a = 0; a < FN; a++)
-#pragma unroll
-      for (int b = 0; b < FM; b++) acc[a][b] = v16i{};
-    const int nst = kend(j) - kbeg(j);  // >= 1
+  for (int j = 0; j < ntile; j++) {
+    const int nst = nks;  // >= STAGES
     // Transpose scratch of this wave: four 1 KB slots (stride kSlot), slot
     // t holding block rows 8t..8t+7 (128 bytes each, 16-byte chunks
     // XOR-swizzled by the row so both access patterns are bank-conflict
@@ -637,22 +616,20 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     // wave writes these slots, now and in the deferred refill.
     char* scr;
     if constexpr (kOwnScratch) {
-      for (int q = 0; q < nst; q++) step(with_dma, gs++);
+      step(with_dma, gs++, first_stage);
+      for (int q = 1; q < nst; q++) step(with_dma, gs++, next_stage);
       scr = escr + w * 4096;
     } else {
-      for (int q = 1; q < nst; q++) step(with_dma, gs++);
-      step(defer_dma, gs);
+      step(with_dma, gs++, first_stage);
+      for (int q = 2; q < nst; q++) step(with_dma, gs++, next_stage);
+      step(defer_dma, gs, next_stage);
       scr = lds + ((unsigned)gs % STAGES) * STAGE + w * 1024;
       gs++;
     }
     constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
-    // The staggered tile's first part parks its partial sums in this
-    // wave's slot; its last part adds them back before the epilogue.
-    const bool park = s0 > 0 && j == 0;
-    const bool unpark = s0 > 0 && j == nseg - 1;
-    // ---- epilogue of tile tseg(j)
+    // ---- epilogue of tile j
     int tm, tn;
-    coords(tseg(j), tm, tn);
+    coords(j, tm, tn);
     const int par = j & 1;
     const int64_t ybase = ((int64_t)tm * BM * N + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
@@ -661,8 +638,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         has_x ? const_cast<float*>(epi.resid) + (ybase >> 2) : static_cast<float*>(Y), (short)0,
         has_x ? kBigRange : 0, kRsrcWord3);
-    const int64_t mrow0 = (int64_t)tm * BM + wrow + rr;
-    const int64_t ncol0 = (int64_t)tn * BN + wcol + 4 * rc;
+    // 32-bit row / column checks: M <= 2^30, and N fits the 32-bit offsets
+    const int mrow0 = tm * BM + wrow + rr;
+    const int ncol0 = tn * BN + wcol + 4 * rc;
+    const int M32 = (int)M, N32 = (int)N;
     // Opaque copy of the lane's offset: keeps the compiler from hoisting the
     // per-row output offsets out of the tile loop (they would stay live
     // across the main loop and spill).
@@ -671,31 +650,13 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
     for (int a = 0; a < FN; a++) {
       const int cl = wcol + a * 32 + 4 * rc;  // tile column of this lane's chunk
-      const bool n_ok = ncol0 + a * 32 < N;
+      const bool n_ok = ncol0 + a * 32 < N32;
       const float4 s4 = *reinterpret_cast<const float4*>(&colb[par][0][cl]);
       const float4 b4 = *reinterpret_cast<const float4*>(&colb[par][1][cl]);
       const float4 g4 = *reinterpret_cast<const float4*>(&colb[par][2][cl]);
 #pragma unroll
       for (int b = 0; b < FM; b++) {
-        v16i c = acc[a][b];
-        if (park) {
-#pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const v4i c4 = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-            __builtin_amdgcn_raw_buffer_store_b128(c4, pr, (int)lane_off + ((a * FM + b) * 4 + g) * 1024,
-                                                   0, 0);
-          }
-          continue;
-        }
-        if (unpark) {
-#pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const v4i p4 = __builtin_amdgcn_raw_buffer_load_b128(
-                pr, (int)lane_off + ((a * FM + b) * 4 + g) * 1024, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; r++) c[4 * g + r] += p4[r];
-          }
-        }
+        const v16i& c = acc[a][b];
         // transpose the block: MFMA layout -> scratch -> row layout
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -710,7 +671,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int rl = b * 32 + 8 * i;  // block row offset of this store
-          const bool ok = n_ok && (mrow0 + rl < M);
+          const bool ok = n_ok && (mrow0 + rl < M32);
           // All offsets in the VGPR, soffset 0: the compiler then inserts
           // the wait states a wide store's data VGPRs need before reuse.
           const int voff = ok ? vlane + rl * ldy4 + a * 128 : kOutOfRange;
@@ -726,9 +687,9 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
             for (int r = 0; r < 4; r++) {
               const float sc = as_m * sv[r];
               const float af = (float)t4[i][r];
-              v[r] = epi.kzero ? 0.f : af * sc;
+              v[r] = af * sc;  // K > 0 here (the launcher requires it)
             }
-            if (epi.bias) {
+            if constexpr (BIAS) {
 #pragma unroll
               for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
             }
@@ -859,27 +820,32 @@ hipError_t run_tiled(const int8_t* wt, const float* bs, const int8_t* at, const 
 template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC>
 hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, const float* as,
                        int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
-                       const GemmAux& aux, int max_groups, hipStream_t s) {
+                       int max_groups, hipStream_t s) {
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m;
   if (T <= 0) return hipSuccess;
-  if (KFp % KS != 0 || (KFp / KS) % 2 != 0 || KFp / KS < STAGES) return hipErrorInvalidValue;
+  // K > 0 and at least STAGES stages: the epilogue has no K == 0 case
+  if (KFp % KS != 0 || KFp / KS < STAGES || epi.kzero) return hipErrorInvalidValue;
   int G = (int)(T < max_groups ? T : max_groups);
   if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
-  if ((size_t)G * BN * BM * 4 > aux.partials_bytes) return hipErrorInvalidValue;
-#define SDQ_LAUNCH_PERSIST(K)                                                                    \
-  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K>), dim3((unsigned)G),     \
+#define SDQ_LAUNCH_PERSIST(K, B)                                                                 \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K, B>), dim3((unsigned)G),  \
                      dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
-                     epi, Y, reinterpret_cast<int4*>(aux.partials), aux.stagger,            \
-                     aux.stagger_spread, aux.stagger_xcd)
+                     epi, Y)
+#define SDQ_LAUNCH_PERSIST_B(K)    \
+  if (epi.bias)                    \
+    SDQ_LAUNCH_PERSIST(K, true);   \
+  else                             \
+    SDQ_LAUNCH_PERSIST(K, false)
   switch (epi.kind) {
-    case SDQ_EPI_NONE: SDQ_LAUNCH_PERSIST(SDQ_EPI_NONE); break;
-    case SDQ_EPI_GELU: SDQ_LAUNCH_PERSIST(SDQ_EPI_GELU); break;
-    case SDQ_EPI_GATED: SDQ_LAUNCH_PERSIST(SDQ_EPI_GATED); break;
-    case SDQ_EPI_RESID: SDQ_LAUNCH_PERSIST(SDQ_EPI_RESID); break;
-    case SDQ_EPI_ACC: SDQ_LAUNCH_PERSIST(SDQ_EPI_ACC); break;
+    case SDQ_EPI_NONE: SDQ_LAUNCH_PERSIST_B(SDQ_EPI_NONE); break;
+    case SDQ_EPI_GELU: SDQ_LAUNCH_PERSIST_B(SDQ_EPI_GELU); break;
+    case SDQ_EPI_GATED: SDQ_LAUNCH_PERSIST_B(SDQ_EPI_GATED); break;
+    case SDQ_EPI_RESID: SDQ_LAUNCH_PERSIST_B(SDQ_EPI_RESID); break;
+    case SDQ_EPI_ACC: SDQ_LAUNCH_PERSIST(SDQ_EPI_ACC, false); break;
     default: return hipErrorInvalidValue;
   }
+#undef SDQ_LAUNCH_PERSIST_B
 #undef SDQ_LAUNCH_PERSIST
   return hipGetLastError();
 }
@@ -905,9 +871,6 @@ int gemm_cfg_bm(int cfg) {
     case kCfgSkinny4: return 128;
     case kCfg128x128: return 128;
     case kCfg256x256: return 256;
-    case kCfg256x256k4: return 256;
-    case kCfg256x128: return 256;  // activation rows padded to 256 either way
-    case kCfg128x256: return 256;
     default: return 256;
   }
 }
@@ -919,9 +882,6 @@ const char* gemm_cfg_name(int cfg) {
     case kCfgSkinny4: return "skinny128";
     case kCfg128x128: return "tile128x128";
     case kCfg256x256: return "tile256x256";
-    case kCfg256x256k4: return "tile256x256k4";
-    case kCfg256x128: return "tile256x128x2";
-    case kCfg128x256: return "tile128x256x2";
     default: return "?";
   }
 }
@@ -944,7 +904,7 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
   const ColOps cols{bs, aux.bias_pad, aux.gate_pad};
   // The persistent kernel addresses a tile's panels and output rows with
   // 32-bit buffer offsets.
-  const bool persist = vec && aux.sink && aux.partials && KFp * 1024 * 8 <= 0x7FFFFFFF &&
+  const bool persist = vec && aux.sink && !epi.kzero && KFp * 1024 * 8 <= 0x7FFFFFFF &&
                        N * 4 * 256 <= 0x7FFFFFF0;
   switch (cfg) {
     case kCfgSkinny1: return run_skinny<1>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
@@ -952,28 +912,13 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
     case kCfgSkinny4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg128x128:
       if (persist)
-        return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+        return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi, Y,
                                                     2 * aux.cu_count, s);
       return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
       if (persist)
-        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
+        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi, Y,
                                                     aux.cu_count, s);
-      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
-    case kCfg256x256k4:
-      if (persist)
-        return run_persist<256, 256, 2, 4, 4, 2, 1>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
-                                                    aux.cu_count, s);
-      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
-    case kCfg256x128:
-      if (persist)
-        return run_persist<256, 128, 2, 2, 2, 3, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
-                                                    2 * aux.cu_count, s);
-      return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
-    case kCfg128x256:
-      if (persist)
-        return run_persist<128, 256, 2, 2, 2, 3, 2>(wt, cols, at, as, M, N, KFp, epi, Y, aux,
-                                                    2 * aux.cu_count, s);
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;
   }

@@ -88,9 +88,6 @@ enum GemmCfg : int {
   kCfgSkinny4,      // M <= 128
   kCfg128x128,      // BN=128, BM=128
   kCfg256x256,      // BN=256, BM=256
-  kCfg256x128,      // BN=256, BM=128, two workgroups per CU
-  kCfg128x256,      // BN=128, BM=256, two workgroups per CU
-  kCfg256x256k4,    // BN=256, BM=256, four k-fragments per stage, two stages
   kCfgCount
 };
 int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
@@ -105,11 +102,6 @@ struct GemmAux {
   const float* bias_pad;
   const float* gate_pad;
   float* sink;
-  void* partials;         // per-workgroup scratch for staggered partial sums
-  size_t partials_bytes;  // >= grid * BN * BM * 4
-  int stagger;            // tile phases per XCD (1 = none)
-  int stagger_spread;     // stages the phases spread over (0 = a whole tile)
-  int stagger_xcd;        // 1: one phase per XCD instead of per workgroup
   int cu_count;
 };
 
