@@ -29,12 +29,6 @@ constexpr int kQuantCache = 6;  // 16 waves x 6 frags x 32 = K <= 3072 in one pa
 constexpr int kQuantRows = 8;
 constexpr int kQuantUnitWaves = 8;
 constexpr int kQuantUnitCache = 3;
-// Long rows (K > 3072): 4-row units, 16 waves, 4 groups (of 8 fragments)
-// cached per lane = K <= 16384 read once (the FFN down-projection's
-// K = 14336 rows otherwise read 80% of every row twice).
-constexpr int kQuantLongRows = 4;
-constexpr int kQuantLongWaves = 16;
-constexpr int kQuantLongCache = 4;
 
 __device__ __forceinline__ int quant_one(float v, float inv) {
   const float y = v * inv;
@@ -163,10 +157,9 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
   }
 }
 
-// Fragment-layout quantizer over R-row units (R = 4, 8 or 16: an eighth, a
-// quarter or half of a fragment row), for a finer grid than one 32-row
-// fragment row per workgroup (fewer idle CUs in the last wave of
-// workgroups). Lane l owns
+// Fragment-layout quantizer over R-row units (R = 8 or 16: a quarter or half
+// of a fragment row), for a finer grid than one 32-row fragment row per
+// workgroup (fewer idle CUs in the last wave of workgroups). Lane l owns
 // row unit*R + (l % R), half h = (l / R) & 1 of fragment g*F + l / (2R),
 // F = 32 / R fragments per group: the fragment slot (row & 31) + 32h, 16
 // bytes, so each fragment is written as two contiguous runs of 16R bytes.
@@ -174,7 +167,7 @@ template <int R, int NW, int CACHE>
 __global__ void __launch_bounds__(NW * 64)
 act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
                        int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
-  static_assert(R == 4 || R == 8 || R == 16, "unit height");
+  static_assert(R == 8 || R == 16, "unit height");
   constexpr int F = 32 / R;  // fragments per lane group
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -190,7 +183,7 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
   const int sub = l / (2 * R);         // fragment within the group
   const int half = (l / R) & 1;
   const int kg = half * 16;            // k offset inside the fragment
-  const int64_t ng = KFp / F;          // fragment groups (KFp is a multiple of 8 >= F)
+  const int64_t ng = KFp / F;          // fragment groups (KFp is a multiple of 8)
   const int slot = (int)((row & 31) + half * 32) * 16;
 
   float cache[CACHE][16];
@@ -251,18 +244,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
                                   int8_t* at, float* as, const ColCopy& cc, hipStream_t s) {
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
-  constexpr int64_t kShortGroups = (int64_t)kQuantUnitWaves * kQuantUnitCache;  // of 32/8 frags
-  if (KFp / (32 / kQuantRows) <= kShortGroups) {
-    const int64_t units = Mp / kQuantRows;
-    hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache>),
-                       dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp,
-                       vec, at, as, cc);
-  } else {
-    const int64_t units = Mp / kQuantLongRows;
-    hipLaunchKernelGGL(
-        (act_quant_units_kernel<kQuantLongRows, kQuantLongWaves, kQuantLongCache>),
-        dim3((unsigned)units), dim3(kQuantLongWaves * 64), 0, s, A, M, K, KFp, vec, at, as, cc);
-  }
+  const int64_t units = Mp / kQuantRows;
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache>),
+                     dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
+                     at, as, cc);
   return hipGetLastError();
 }
 

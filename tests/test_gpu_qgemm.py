@@ -106,6 +106,9 @@ SHAPES = [
     (300, 257, 129),     # ragged everything
     (512, 3072, 3072),   # cross-attn K/V on ctx[512]
     (768, 14336, 3072),  # cfg2 FFN down
+    (70, 4200, 300),     # long rows, last 32-fragment group of the quantizer partial
+    (33, 16384, 64),     # the longest row the single-pass quantizer keeps in registers
+    (40, 20000, 96),     # longer rows: the quantizer's re-read loop
 ]
 
 
