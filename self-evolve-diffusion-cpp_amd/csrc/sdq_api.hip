@@ -52,6 +52,10 @@ struct Workspace {
   float* cols = nullptr;  // [2][col_cap]: zero-padded bias, gate copies
   size_t col_cap = 0;
   float* sink = nullptr;  // 1 KB target of masked epilogue stores
+  int* part = nullptr;    // split-K int32 partial sums
+  size_t part_bytes = 0;
+  float* pmax = nullptr;  // split quantizer's per-(row, k-chunk) maxima
+  size_t pmax_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -117,7 +121,7 @@ int grow(hipStream_t s, void** p, size_t* have, size_t need) {
 }
 
 int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t col_cap,
-              Workspace** out) {
+              size_t part_bytes, size_t pmax_bytes, Workspace** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace& w = g_ws[{dev, s}];
   int rc = grow(s, reinterpret_cast<void**>(&w.at), &w.at_bytes, at_bytes);
@@ -131,6 +135,8 @@ int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t c
     size_t have = 0;
     rc = grow(s, reinterpret_cast<void**>(&w.sink), &have, 4096);
   }
+  if (!rc && part_bytes) rc = grow(s, reinterpret_cast<void**>(&w.part), &w.part_bytes, part_bytes);
+  if (!rc && pmax_bytes) rc = grow(s, reinterpret_cast<void**>(&w.pmax), &w.pmax_bytes, pmax_bytes);
   if (rc) return rc;
   *out = &w;
   return SDQ_OK;
@@ -233,7 +239,13 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   const size_t at_bytes = (size_t)(Mp / kFragRows) * (size_t)w->KFp * kFragBytes;
   const size_t col_cap = (size_t)(w->Np + kColPad);
   Workspace* ws = nullptr;
-  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap, &ws))) return rc;
+  const int splitk = choose_splitk(cfg, M, N, w->KFp, g_dev[w->device].cu_count);
+  const size_t part_bytes = splitk > 1 ? (size_t)splitk * (size_t)M * (size_t)N * 4 : 0;
+  const int cu_count = g_dev[w->device].cu_count;
+  const size_t pmax_bytes = (size_t)act_quant_pmax_floats(Mp, w->KFp, cu_count) * sizeof(float);
+  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap, part_bytes,
+                      pmax_bytes, &ws)))
+    return rc;
   const EpiArgs ea = make_epi(epi, K);
   ColCopy cc{};
   cc.bias = ea.bias;
@@ -244,21 +256,24 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   cc.CP = (int64_t)col_cap;
 
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, s);
+  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
+                                        pmax_bytes ? ws->pmax : nullptr, cu_count, s);
   if (e != hipSuccess) return hip_error(e, "act_quant launch");
   hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
   int vec = (N % 4 == 0) && aligned16(Y);
   if (ea.bias) vec = vec && aligned16(ea.bias);
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
-  GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count};
+  GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count, splitk,
+              splitk > 1 ? ws->part : nullptr};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) return hip_error(e, "qgemm launch");
   if (t_prof) {
     hipEvent_t p2 = prof_mark(s);
     if (p0 && p1 && p2) {
       t_recs.push_back({"act_quant", p0, p1});
-      t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg), p1, p2});
+      t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg) + (splitk > 1 ? "_splitk" : ""),
+                        p1, p2});
     } else {
       for (hipEvent_t ev : {p0, p1, p2})
         if (ev) (void)hipEventDestroy(ev);

@@ -385,11 +385,16 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // make a wait longer. Per-tile weight scales, bias, gate and activation
 // scales arrive by LDS-DMA into a double buffer after the tile's first
 // stage.
-template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI, bool BIAS>
+// SPLITK: the work items are (tile, k-range) pairs, `splits` contiguous
+// k-ranges per tile, each writing raw int32 sums to its own [M,N] slice of
+// Y (EPI_ACC); splitk_reduce adds the slices and applies the epilogue.
+template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI, bool BIAS,
+          bool SPLITK>
 __global__ void __launch_bounds__(WN* WM * 64, OCC)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
-              int tiles_m, EpiArgs epi, void* Y) {
+              int tiles_m, EpiArgs epi, void* Y, int splits) {
+  static_assert(!SPLITK || EPI == SDQ_EPI_ACC, "split-K partials are raw accumulators");
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -421,17 +426,25 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const uint32_t lane_off = (uint32_t)lane * 16u;
 
   const int T = tiles_n * tiles_m;
+  const int S = SPLITK ? splits : 1;
+  const int TS = T * S;  // work items
   const int G = gridDim.x;
-  const int ntile = (T - (int)blockIdx.x + G - 1) / G;
-  const int nks = (int)(KFp / KS);
+  const int ntile = (TS - (int)blockIdx.x + G - 1) / G;
+  const int klen = (int)(KFp / S);  // k-fragments per work item
+  const int nks = klen / KS;
 
-  // Tile i of this workgroup -> (tm, tn): XCD-aware grouped order applied
-  // to the virtual block id blockIdx.x + i*G (G is a multiple of 8, so it
-  // stays on this XCD).
-  auto coords = [&](int i, int& tm, int& tn) {
+  // Work item i of this workgroup -> (tm, tn, k-range ks): XCD-aware
+  // grouped order applied to the virtual block id blockIdx.x + i*G (G is a
+  // multiple of 8, so it stays on this XCD).
+  auto coords = [&](int i, int& tm, int& tn, int& ks) {
     const int bid = (int)blockIdx.x + i * G;
-    const int xcd = bid & 7, jx = bid >> 3, q8 = T >> 3, r8 = T & 7;
-    const int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + jx;
+    const int xcd = bid & 7, jx = bid >> 3, q8 = TS >> 3, r8 = TS & 7;
+    int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + jx;
+    ks = 0;
+    if constexpr (SPLITK) {
+      ks = lin / T;
+      lin -= ks * T;
+    }
     constexpr int GROUP_M = 4;
     const int per_group = GROUP_M * tiles_n;
     const int g = lin / per_group;
@@ -452,14 +465,15 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int wso0 = ((w / KS) * (int)KFp + (w % KS)) * 1024;
   const int tso = (NW / KS) * (int)KFp * 1024;
   const uint32_t lds0 = lds_addr32(lds) + (uint32_t)w * 1024u;
-  int cj = 0, cks = 0, ctm = 0, ctn = 0, cgs = 0;
+  int cj = 0, cks = 0, ctm = 0, ctn = 0, cgs = 0, csp = 0;
   int wso = wso0;
   bool col_due = true;  // the segment's first stage was issued; its column loads follow
   v4u wr, ar;
   auto set_tile = [&](int i) {
-    coords(i, ctm, ctn);
+    coords(i, ctm, ctn, csp);
     wr = raw_rsrc(wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
     ar = raw_rsrc(at + (int64_t)ctm * apanel, (uint32_t)apanel);
+    wso = wso0 + csp * klen * 1024;  // the work item's first k-fragment
   };
   set_tile(0);
   // Load t (0..LPW-1) of the cursor's stage: WLD weight, then ALD
@@ -494,7 +508,6 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     if (++cks == nks) {
       if (++cj < ntile) {
         cks = 0;
-        wso = wso0;
         set_tile(cj);
         col_due = true;
       } else {
@@ -628,10 +641,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     }
     constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
     // ---- epilogue of tile j
-    int tm, tn;
-    coords(j, tm, tn);
+    int tm, tn, ksp;
+    coords(j, tm, tn, ksp);
     const int par = j & 1;
-    const int64_t ybase = ((int64_t)tm * BM * N + (int64_t)tn * BN) * 4;
+    const int64_t ybase = (((int64_t)ksp * M + (int64_t)tm * BM) * N + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<char*>(Y) + ybase, (short)0, kBigRange, kRsrcWord3);
     const bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
@@ -733,10 +746,15 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Skinny kernel (M <= 32*FMS): one workgroup per 32 weight rows; its SPLIT
-// waves stride over K, each streaming 1 KB weight fragments straight from
-// HBM into VGPRs, then the partial int32 accumulators are summed through LDS
-// in a fixed order (exact, so the order does not matter anyway).
+// Skinny kernel (M <= 32*FMS, FMS <= 8): one workgroup per 32 weight rows;
+// its SPLIT waves stride over K, each streaming 1 KB weight fragments
+// straight from HBM into VGPRs (and the small activation panel from L2),
+// two k-fragments per group with the next group's loads in flight while
+// the current one multiplies; then the partial int32 accumulators are
+// summed through LDS in a fixed order (exact, so the order does not matter
+// anyway). Small M is latency-bound on the tiled kernels (a 128x128 tile
+// walks all of K alone); here every CU that holds a workgroup streams a
+// quarter of K per wave.
 template <int FMS, int SPLIT>
 __global__ void __launch_bounds__(SPLIT * 64)
 qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
@@ -752,32 +770,39 @@ qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 #pragma unroll
   for (int j = 0; j < FMS; j++) acc[j] = v16i{};
 
-  constexpr int U = 4;
-  int64_t kb = w;
-  for (; kb + (int64_t)(U - 1) * SPLIT < KFp; kb += (int64_t)U * SPLIT) {
+  constexpr int U = 2;  // k-fragments per group; KFp is a multiple of 8 = U * SPLIT
+  static_assert(U * SPLIT == 8, "groups tile KFp exactly");
+  const int64_t ngrp = KFp / (U * SPLIT);
+  struct Grp {
     v4i a[U], b[U][FMS];
+  };
+  auto load = [&](int64_t g, Grp& x) {
 #pragma unroll
-    for (int u = 0; u < U; u++)
-      a[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (kb + u * SPLIT) * 1024));
-#pragma unroll
-    for (int u = 0; u < U; u++)
-#pragma unroll
-      for (int j = 0; j < FMS; j++)
-        b[u][j] = *reinterpret_cast<const v4i*>(ap + (j * KFp + kb + u * SPLIT) * 1024);
-#pragma unroll
-    for (int u = 0; u < U; u++)
+    for (int u = 0; u < U; u++) {
+      const int64_t kb = w + (g * U + u) * SPLIT;
+      x.a[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + kb * 1024));
 #pragma unroll
       for (int j = 0; j < FMS; j++)
-        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u], b[u][j], acc[j], 0, 0, 0);
-  }
-  for (; kb < KFp; kb += SPLIT) {
-    const v4i a = *reinterpret_cast<const v4i*>(wp + kb * 1024);
-#pragma unroll
-    for (int j = 0; j < FMS; j++) {
-      const v4i b = *reinterpret_cast<const v4i*>(ap + (j * KFp + kb) * 1024);
-      acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[j], 0, 0, 0);
+        x.b[u][j] = *reinterpret_cast<const v4i*>(ap + (j * KFp + kb) * 1024);
     }
+  };
+  auto mma = [&](const Grp& x) {
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+      for (int j = 0; j < FMS; j++)
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x.a[u], x.b[u][j], acc[j], 0, 0, 0);
+  };
+  Grp c0, c1;
+  load(0, c0);  // ngrp >= 1 (KFp >= 8)
+  int64_t g = 0;
+  for (; g + 1 < ngrp; g += 2) {
+    load(g + 1, c1);
+    mma(c0);
+    if (g + 2 < ngrp) load(g + 2, c0);
+    mma(c1);
   }
+  if (g < ngrp) mma(c0);
 
   __shared__ int red[SPLIT][16][64];
   const int64_t n_lane = rb * 32 + (lane >> 5) * 4;
@@ -820,18 +845,27 @@ hipError_t run_tiled(const int8_t* wt, const float* bs, const int8_t* at, const 
 template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC>
 hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, const float* as,
                        int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
-                       int max_groups, hipStream_t s) {
+                       int max_groups, hipStream_t s, int splits = 1) {
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
-  const int64_t T = (int64_t)tiles_n * tiles_m;
+  const int64_t T = (int64_t)tiles_n * tiles_m * splits;
   if (T <= 0) return hipSuccess;
-  // K > 0 and at least STAGES stages: the epilogue has no K == 0 case
-  if (KFp % KS != 0 || KFp / KS < STAGES || epi.kzero) return hipErrorInvalidValue;
+  // K > 0 and at least STAGES stages per work item: the epilogue has no
+  // K == 0 case
+  if (splits < 1 || KFp % (KS * splits) != 0 || KFp / splits / KS < STAGES || epi.kzero)
+    return hipErrorInvalidValue;
   int G = (int)(T < max_groups ? T : max_groups);
   if (G >= 8) G &= ~7;  // keeps virtual block ids on their XCD
-#define SDQ_LAUNCH_PERSIST(K, B)                                                                 \
-  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K, B>), dim3((unsigned)G),  \
-                     dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp, tiles_n, tiles_m,   \
-                     epi, Y)
+  if (splits > 1) {
+    if (epi.kind != SDQ_EPI_ACC) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, SDQ_EPI_ACC, false, true>),
+                       dim3((unsigned)G), dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp,
+                       tiles_n, tiles_m, epi, Y, splits);
+    return hipGetLastError();
+  }
+#define SDQ_LAUNCH_PERSIST(K, B)                                                                  \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K, B, false>),              \
+                     dim3((unsigned)G), dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp,  \
+                     tiles_n, tiles_m, epi, Y, 1)
 #define SDQ_LAUNCH_PERSIST_B(K)    \
   if (epi.bias)                    \
     SDQ_LAUNCH_PERSIST(K, true);   \
@@ -850,6 +884,83 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   return hipGetLastError();
 }
 
+// Split-K reduction: Y[m, n..n+3] = epilogue(sum_s part[s][m][n..n+3]),
+// the same fp32 steps as the GEMM epilogues (the int32 sum is exact).
+template <int EPI, bool BIAS>
+__global__ void __launch_bounds__(256)
+splitk_reduce(const int* __restrict__ part, int S, int64_t M, int64_t N,
+              const float* __restrict__ as, const float* __restrict__ bs, EpiArgs epi, void* Y) {
+  const int64_t n4 = N / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * n4) return;
+  const int64_t m = idx / n4, n = (idx - m * n4) * 4;
+  v4i acc = *reinterpret_cast<const v4i*>(part + m * N + n);
+  for (int s = 1; s < S; s++) acc += *reinterpret_cast<const v4i*>(part + (s * M + m) * N + n);
+  if constexpr (EPI == SDQ_EPI_ACC) {
+    *reinterpret_cast<v4i*>(static_cast<int*>(Y) + m * N + n) = acc;
+    return;
+  } else {
+    const float as_m = as[m];
+    const v4f s4 = *reinterpret_cast<const v4f*>(bs + n);
+    v4f v;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float sc = as_m * s4[r];
+      const float af = (float)acc[r];
+      v[r] = af * sc;
+    }
+    if constexpr (BIAS) {
+      const v4f b4 = *reinterpret_cast<const v4f*>(epi.bias + n);
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = v[r] + b4[r];
+    }
+    if constexpr (EPI == SDQ_EPI_GELU) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
+    } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
+      const v4f x = *reinterpret_cast<const v4f*>(epi.resid + m * N + n);
+      if constexpr (EPI == SDQ_EPI_RESID) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
+      } else {
+        const v4f g4 = *reinterpret_cast<const v4f*>(epi.gate + n);
+        if (epi.gate_fma) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) v[r] = __builtin_fmaf(v[r], g4[r], x[r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float p = v[r] * g4[r];
+            v[r] = x[r] + p;
+          }
+        }
+      }
+    }
+    *reinterpret_cast<v4f*>(static_cast<float*>(Y) + m * N + n) = v;
+  }
+}
+
+hipError_t run_splitk_reduce(const int* part, int S, int64_t M, int64_t N, const float* as,
+                             const float* bs, const EpiArgs& epi, void* Y, hipStream_t s) {
+  const int64_t items = M * (N / 4);
+  if (items <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)ceil_div(items, 256);
+#define SDQ_LAUNCH_REDUCE(K, B)                                                              \
+  hipLaunchKernelGGL((splitk_reduce<K, B>), dim3(blocks), dim3(256), 0, s, part, S, M, N, as, \
+                     bs, epi, Y)
+  const bool b = epi.bias != nullptr;
+  switch (epi.kind) {
+    case SDQ_EPI_NONE: if (b) SDQ_LAUNCH_REDUCE(SDQ_EPI_NONE, true); else SDQ_LAUNCH_REDUCE(SDQ_EPI_NONE, false); break;
+    case SDQ_EPI_GELU: if (b) SDQ_LAUNCH_REDUCE(SDQ_EPI_GELU, true); else SDQ_LAUNCH_REDUCE(SDQ_EPI_GELU, false); break;
+    case SDQ_EPI_GATED: if (b) SDQ_LAUNCH_REDUCE(SDQ_EPI_GATED, true); else SDQ_LAUNCH_REDUCE(SDQ_EPI_GATED, false); break;
+    case SDQ_EPI_RESID: if (b) SDQ_LAUNCH_REDUCE(SDQ_EPI_RESID, true); else SDQ_LAUNCH_REDUCE(SDQ_EPI_RESID, false); break;
+    case SDQ_EPI_ACC: SDQ_LAUNCH_REDUCE(SDQ_EPI_ACC, false); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef SDQ_LAUNCH_REDUCE
+  return hipGetLastError();
+}
+
 template <int FMS>
 hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const float* as,
                       int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y, int vec,
@@ -857,18 +968,33 @@ hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const
   constexpr int SPLIT = 4;
   const int64_t blocks = ceil_div(N, 32);
   if (blocks <= 0) return hipSuccess;
+  if (KFp % 8 != 0 || KFp < 8) return hipErrorInvalidValue;
   hipLaunchKernelGGL((qgemm_skinny<FMS, SPLIT>), dim3((unsigned)blocks), dim3(SPLIT * 64), 0, s,
                      wt, bs, at, as, M, N, KFp, epi, Y, vec);
   return hipGetLastError();
+}
+
+hipError_t run_skinny_m(const int8_t* wt, const float* bs, const int8_t* at, const float* as,
+                        int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y, int vec,
+                        hipStream_t s) {
+  switch (ceil_div(M, 32)) {
+    case 1: return run_skinny<1>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 2: return run_skinny<2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 3: return run_skinny<3>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 5: return run_skinny<5>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 6: return run_skinny<6>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 7: return run_skinny<7>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case 8: return run_skinny<8>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
 int gemm_cfg_bm(int cfg) {
   switch (cfg) {
-    case kCfgSkinny1: return 32;
-    case kCfgSkinny2: return 64;
-    case kCfgSkinny4: return 128;
+    case kCfgSkinny: return 32;
     case kCfg128x128: return 128;
     case kCfg256x256: return 256;
     default: return 256;
@@ -877,9 +1003,7 @@ int gemm_cfg_bm(int cfg) {
 
 const char* gemm_cfg_name(int cfg) {
   switch (cfg) {
-    case kCfgSkinny1: return "skinny32";
-    case kCfgSkinny2: return "skinny64";
-    case kCfgSkinny4: return "skinny128";
+    case kCfgSkinny: return "skinny";
     case kCfg128x128: return "tile128x128";
     case kCfg256x256: return "tile256x256";
     default: return "?";
@@ -890,12 +1014,33 @@ int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_coun
   if (const char* f = std::getenv("SDQ_FORCE_CFG")) {
     const int c = std::atoi(f);
     if (c >= kCfg128x128 && c < kCfgCount && M > 128) return c;
+    if (c == kCfgSkinny && M <= kSkinnyMaxM) return c;
   }
-  if (M <= 32) return kCfgSkinny1;
-  if (M <= 64) return kCfgSkinny2;
+  if (M <= 64) return kCfgSkinny;
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
   if (t256 >= 2 * (int64_t)(cu_count > 0 ? cu_count : 256)) return kCfg256x256;
   return kCfg128x128;
+}
+
+int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count) {
+  // Long K on a grid that leaves CUs idle: split K so the 128x128 kernel's
+  // (tile, k-range) items number at most one per CU (measured: more items
+  // than CUs is slower, the two workgroups of a CU then share its LDS and
+  // load bandwidth and the slices grow); each item keeps >= 16 k-fragments.
+  // SDQ_FORCE_SPLITK=S overrides the factor (1 = never split); a factor
+  // that does not divide the k-fragments into >= 16 per item is lowered.
+  if (cfg != kCfg128x128 || N % 4 != 0) return 1;
+  int S = 0;
+  if (const char* f = std::getenv("SDQ_FORCE_SPLITK")) S = std::atoi(f) < 1 ? 1 : std::atoi(f);
+  if (S == 0) {
+    if (KFp < 192) return 1;
+    const int64_t T = ceil_div(M, 128) * ceil_div(N, 128);
+    const int64_t per = (cu_count > 0 ? cu_count : 256) / T;
+    S = per < 1 ? 1 : (per > 8 ? 8 : (int)per);
+  }
+  if (S > 8) S = 8;
+  while (S > 1 && (KFp % (2 * S) != 0 || KFp / S < 16)) S--;
+  return S;
 }
 
 hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,
@@ -907,10 +1052,19 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
   const bool persist = vec && aux.sink && !epi.kzero && KFp * 1024 * 8 <= 0x7FFFFFFF &&
                        N * 4 * 256 <= 0x7FFFFFF0;
   switch (cfg) {
-    case kCfgSkinny1: return run_skinny<1>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
-    case kCfgSkinny2: return run_skinny<2>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
-    case kCfgSkinny4: return run_skinny<4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
+    case kCfgSkinny:
+      if (M > kSkinnyMaxM) return hipErrorInvalidValue;
+      return run_skinny_m(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg128x128:
+      if (persist && aux.splitk > 1 && aux.part) {
+        EpiArgs acc_epi = epi;
+        acc_epi.kind = SDQ_EPI_ACC;
+        hipError_t e = run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, acc_epi,
+                                                            aux.part, 2 * aux.cu_count, s,
+                                                            aux.splitk);
+        if (e != hipSuccess) return e;
+        return run_splitk_reduce(aux.part, aux.splitk, M, N, as, bs, epi, Y, s);
+      }
       if (persist)
         return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi, Y,
                                                     2 * aux.cu_count, s);

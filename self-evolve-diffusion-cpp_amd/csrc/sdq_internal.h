@@ -67,8 +67,13 @@ struct ColCopy {
   float* gate_pad;
   int64_t N, CP;
 };
+// Few rows (Mp / 8 units below a grid's worth) run the split form: one
+// kernel writes per-(row, k-chunk) maxima to pmax, a second reduces them and
+// quantizes; act_quant_pmax_floats gives pmax's size (0: single kernel).
+int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count);
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
-                                  int8_t* at, float* as, const ColCopy& cc, hipStream_t s);
+                                  int8_t* at, float* as, const ColCopy& cc, float* pmax,
+                                  int cu_count, hipStream_t s);
 // Same quantizer, row-major int8 output [M,K] (parity API).
 hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
                                      hipStream_t s);
@@ -83,16 +88,17 @@ hipError_t launch_unpack_weight(const int8_t* frags, int64_t N, int64_t K, int64
 
 // GEMM tile configurations.
 enum GemmCfg : int {
-  kCfgSkinny1 = 0,  // M <= 32: one 32-row activation block, split-K waves
-  kCfgSkinny2,      // M <= 64
-  kCfgSkinny4,      // M <= 128
+  kCfgSkinny = 0,   // M <= kSkinnyMaxM: 32-row activation blocks, split-K waves
   kCfg128x128,      // BN=128, BM=128
   kCfg256x256,      // BN=256, BM=256
   kCfgCount
 };
+constexpr int64_t kSkinnyMaxM = 256;
 int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
 const char* gemm_cfg_name(int cfg);
 int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_count);
+// Split-K factor for the 128x128 kernel at this shape (1 = no split).
+int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count);
 
 // Extra buffers of the persistent GEMM path: bias / gate copied into
 // zero-padded buffers (nullptr when absent) so they can be moved by LDS-DMA,
@@ -103,6 +109,8 @@ struct GemmAux {
   const float* gate_pad;
   float* sink;
   int cu_count;
+  int splitk;  // choose_splitk's factor (1 = none)
+  int* part;   // splitk x M x N int32 partial sums (splitk > 1)
 };
 
 hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,

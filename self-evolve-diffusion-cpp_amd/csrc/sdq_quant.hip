@@ -13,7 +13,11 @@
 // reduction (a single HBM read when the row fits), and re-reads only the
 // part of the row beyond that. The fragment-layout kernel works on 8-row
 // units (a quarter of a fragment row per workgroup) for a fine grid; the
-// row-major kernel (parity API) on 32-row blocks.
+// row-major kernel (parity API) on 32-row blocks. Few long rows take a
+// split form instead (per-chunk maxima, then reduce + quantize), so that
+// the whole GPU walks them.
+#include <cstdlib>
+
 #include "sdq_internal.h"
 
 #pragma clang fp contract(off)
@@ -196,6 +200,8 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
       mx = amax16(cache[c], mx);
     }
   }
+  // (loading several groups per iteration here measured slower at large
+  // M: the extra VGPRs cost occupancy, 5 -> 3 waves per SIMD)
   for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
     float t[16];
     load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
@@ -237,14 +243,150 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
   }
 }
 
+// Split form of the fragment-layout quantizer for few rows, where one
+// workgroup per 8-row unit walks too much of K serially (latency-bound: a
+// handful of workgroups each waiting on dependent row loads). Work item =
+// (unit, chunk of GPW fragment groups), one wave each, same lane roles as
+// act_quant_units_kernel (R = 8). Pass 1 writes the item's per-row maxima;
+// pass 2 reduces a row's maxima (max is exact and order-free; NaN never
+// enters, as in amax16) and quantizes its chunk, re-reading it (from L2:
+// same grid, so item i runs on the same XCD in both passes).
+template <int GPW>
+__global__ void __launch_bounds__(256)
+act_quant_pmax_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
+                      int C, int64_t items, float* __restrict__ pmax) {
+  constexpr int R = 8, F = 32 / R;
+  const int l = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const int64_t unit = item / C;
+  const int c = (int)(item - unit * C);
+  const int64_t row = unit * R + (l % R);
+  const bool row_ok = row < M;
+  const float* rowp = A + (row_ok ? row : 0) * K;
+  const int sub = l / (2 * R), kg = ((l / R) & 1) * 16;
+  const int64_t ng = KFp / F;
+  float v[GPW][16];
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < GPW; i++) {
+    const int64_t g = (int64_t)c * GPW + i;
+    if (g < ng) {
+      load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, v[i]);
+      mx = amax16(v[i], mx);
+    }
+  }
+#pragma unroll
+  for (int d = R; d < 64; d *= 2) {
+    const float o = __shfl_xor(mx, d);
+    mx = (mx < o) ? o : mx;
+  }
+  // rows of pmax have Cp = C rounded up to 4 floats, the tail zeroed
+  if (l < R) {
+    const int Cp = (C + 3) & ~3;
+    float* pr = pmax + (unit * R + l) * Cp;
+    pr[c] = mx;
+    if (c == C - 1)
+      for (int j = C; j < Cp; j++) pr[j] = 0.f;
+  }
+}
+
+template <int GPW>
+__global__ void __launch_bounds__(256)
+act_quant_emit_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
+                      int C, int64_t items, const float* __restrict__ pmax,
+                      int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
+  constexpr int R = 8, F = 32 / R;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (cc.bias_pad) cc.bias_pad[i] = i < cc.N ? cc.bias[i] : 0.f;
+    if (cc.gate_pad) cc.gate_pad[i] = i < cc.N ? cc.gate[i] : 0.f;
+  }
+  const int l = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const int64_t unit = item / C;
+  const int c = (int)(item - unit * C);
+  const int64_t row = unit * R + (l % R);
+  const bool row_ok = row < M;
+  const float* rowp = A + (row_ok ? row : 0) * K;
+  const int sub = l / (2 * R), half = (l / R) & 1, kg = half * 16;
+  const int64_t ng = KFp / F;
+  float v[GPW][16];
+#pragma unroll
+  for (int i = 0; i < GPW; i++) {
+    const int64_t g = (int64_t)c * GPW + i;
+    if (g < ng) load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, v[i]);
+  }
+  const int Cp = (C + 3) & ~3;
+  const float4* pm = reinterpret_cast<const float4*>(pmax + (unit * R + l % R) * Cp);
+  float mx = 0.f;
+  for (int j = 0; j < Cp / 4; j++) {
+    const float4 r = pm[j];
+    mx = (mx < r.x) ? r.x : mx;
+    mx = (mx < r.y) ? r.y : mx;
+    mx = (mx < r.z) ? r.z : mx;
+    mx = (mx < r.w) ? r.w : mx;
+  }
+  float sc = mx / 127.f;
+  if (sc == 0.f) sc = 1.f;
+  const float inv = 1.f / sc;
+  if (c == 0 && l < R && row_ok) as[row] = sc;
+  int8_t* base = out + (unit / F) * KFp * 1024 + (int)((row & 31) + half * 32) * 16;
+#pragma unroll
+  for (int i = 0; i < GPW; i++) {
+    const int64_t g = (int64_t)c * GPW + i;
+    if (g < ng) *reinterpret_cast<uint4*>(base + (g * F + sub) * 1024) = pack16(v[i], inv);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Fragment groups per split item: 4 from 64 units up (measured at K=14336:
+// M=512 16.3 vs 19.0 us, M=768 22.1 vs 25.2), else 2 (M=157 12.7 vs 14.4).
+int split_gpw(int64_t Mp) { return Mp / kQuantRows >= 64 ? 4 : 2; }
+int64_t split_chunks(int64_t Mp, int64_t KFp) {
+  return ceil_div(KFp / (32 / kQuantRows), split_gpw(Mp));
+}
 
 }  // namespace
 
+int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count) {
+  // The split form pays a second launch and a re-read from L2; it wins
+  // where a row does not fit the single kernel's register cache and the
+  // 8-row units are too few to fill every CU twice (measured at K=14336:
+  // M=157 12.7 vs 30.5 us, M=768 22.1 vs 31.3; at K=3072 the single
+  // kernel wins, 7.4 vs 9.1 at M=157). SDQ_QUANT_SINGLE forces the single
+  // kernel, for comparisons.
+  if (std::getenv("SDQ_QUANT_SINGLE")) return 0;
+  const int64_t units = Mp / kQuantRows;
+  if (units >= 2 * (int64_t)(cu_count > 0 ? cu_count : 256)) return 0;
+  if (KFp <= (int64_t)kQuantUnitCache * kQuantUnitWaves * (32 / kQuantRows) || std::getenv("TMP_B1")) return 0;
+  return Mp * ((split_chunks(Mp, KFp) + 3) & ~3);
+}
+
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
-                                  int8_t* at, float* as, const ColCopy& cc, hipStream_t s) {
+                                  int8_t* at, float* as, const ColCopy& cc, float* pmax,
+                                  int cu_count, hipStream_t s) {
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
   const int64_t units = Mp / kQuantRows;
+  if (pmax && act_quant_pmax_floats(Mp, KFp, cu_count) > 0) {
+    const int C = (int)split_chunks(Mp, KFp);
+    const int64_t items = units * C;
+    const unsigned blocks = (unsigned)ceil_div(items, 4);
+    if (split_gpw(Mp) == 4) {
+      hipLaunchKernelGGL((act_quant_pmax_kernel<4>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, pmax);
+      hipLaunchKernelGGL((act_quant_emit_kernel<4>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, pmax, at, as, cc);
+    } else {
+      hipLaunchKernelGGL((act_quant_pmax_kernel<2>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, pmax);
+      hipLaunchKernelGGL((act_quant_emit_kernel<2>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, pmax, at, as, cc);
+    }
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache>),
                      dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
                      at, as, cc);

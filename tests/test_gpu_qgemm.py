@@ -344,3 +344,39 @@ def test_repeated_calls_and_streams(sdq_dev, oracle):
         outs.append(Y.cpu().numpy())
     for o in outs:
         assert_bitexact(o, want, "repeat")
+
+
+# ----------------------------------------------------------------- split-K
+# Few output tiles over a long K: the 128x128 kernel splits K across
+# workgroups (int32 partial slices, exact) and a reduction applies the
+# epilogue. M is not a multiple of 128, so the last row tile of every slice
+# is masked.
+SPLITK_SHAPES = [(157, 14336, 3072),  # FFN down at the audio branch's token count
+                 (200, 6144, 1000),   # ragged N, eight splits
+                 (90, 8192, 512)]     # fewest tiles
+
+
+@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+def test_splitk_epilogues_bitexact(sdq_dev, oracle, M, K, N):
+    import sdq
+
+    print(f"[splitk] M={M} K={K} N={N}", flush=True)
+    A, q, s, bias = _inputs(M, K, N, seed=11 * M + K + N)
+    gate = oracle.randn(N, 91)
+    x = oracle.randn(M * N, 92).reshape(M, N)
+    w = sdq.Weight.from_host(q, s)
+    aq, _ = oracle.act_quant(A)
+    assert_bitexact(_run(sdq_dev, w, A, kind="acc"), oracle.qgemm_acc(aq, q), "int32 acc")
+    assert_bitexact(_run(sdq_dev, w, A), oracle.qgemm(A, q, s), "qgemm")
+    assert_bitexact(_run(sdq_dev, w, A, bias=bias), oracle.linear(A, q, s, bias=bias), "mlin")
+    for fma in (True, False):
+        got = _run(sdq_dev, w, A, kind="gated", bias=bias, gate=gate, resid=x, gate_fma=fma)
+        want = oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x,
+                             use_fma=fma)
+        assert_bitexact(got, want, f"gated fma={fma}")
+    got = _run(sdq_dev, w, A, kind="resid", bias=bias, resid=x)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias, epilogue="resid", resid=x), "resid")
+    got = _run(sdq_dev, w, A, kind="gelu", bias=bias)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gelu")
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-6 * (1.0 + np.abs(want))), float(err.max())
