@@ -116,6 +116,18 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale);
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
                 void* Y, void* stream);
 
+/* The FFN of a DiT block after its norm (src/model/ovi_dit.cpp:218-221,
+ * ffn_fwd):  hid = gelu_tanh(mlin(h, fc1));  x = fma(mlin(hid, fc2), gate, x)
+ * (gate_fma = 0: x + fl(y*gate)). fc1 is [F,D], fc2 [D,F]; h and x are
+ * [M,D], hid [M,F] (written), all device pointers; x is updated in place.
+ * Same results as sdq_qlinear(fc1, GELU) then sdq_qlinear(fc2, GATED), bit
+ * for bit; faster: fc1's epilogue passes hid's row maxima to fc2's
+ * activation quantizer, which then reads hid once.
+ * Replaces: mlin + gelu_tanh_inplace + mlin + gated_add_inplace (218-221). */
+int sdq_ffn(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
+            const float* h, int64_t M, const float* gate, int gate_fma, float* hid, float* x,
+            void* stream);
+
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
 

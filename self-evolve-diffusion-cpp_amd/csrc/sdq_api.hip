@@ -8,6 +8,7 @@
 // its qgemm has no error path at all, src/core/qgemm.cpp:73-142).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -56,6 +57,8 @@ struct Workspace {
   size_t part_bytes = 0;
   float* pmax = nullptr;  // split quantizer's per-(row, k-chunk) maxima
   size_t pmax_bytes = 0;
+  float* rmax = nullptr;  // row maxima of a GELU output (sdq_ffn's hidden state)
+  size_t rmax_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -142,6 +145,16 @@ int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t c
   return SDQ_OK;
 }
 
+// The (device, stream) workspace's row-maxima buffer, at least `bytes`.
+int rmax_buffer(int dev, hipStream_t s, size_t bytes, float** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, s}];
+  int rc = grow(s, reinterpret_cast<void**>(&w.rmax), &w.rmax_bytes, bytes);
+  if (rc) return rc;
+  *out = w.rmax;
+  return SDQ_OK;
+}
+
 int check_weight(const sdq_weight* w, int64_t K) {
   if (!w) return set_error(SDQ_ERR_INVALID, "null weight handle");
   if (K != w->K)
@@ -219,9 +232,19 @@ int hip_error(hipError_t e, const char* what) {
   return e == hipErrorOutOfMemory ? SDQ_ERR_NOMEM : SDQ_ERR_HIP;
 }
 
-// Core device-pointer path shared by the entry points.
+// Row maxima handed from a GELU GEMM's epilogue to the next quantizer:
+// p[row * stride + c], c < chunks (chunks = 0: not written).
+struct RowMax {
+  float* p = nullptr;
+  int stride = 0;
+  int chunks = 0;
+};
+
+// Core device-pointer path shared by the entry points. `pre` (nullable):
+// A's row maxima are known; `rmax_out` (nullable, GELU): write Y's.
 int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
-                   const sdq_epilogue* epi, void* Y, hipStream_t s) {
+                   const sdq_epilogue* epi, void* Y, hipStream_t s, const RowMax* pre = nullptr,
+                   RowMax* rmax_out = nullptr) {
   int rc = check_weight(w, K);
   if (rc) return rc;
   if ((rc = validate_epi(epi))) return rc;
@@ -246,7 +269,13 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap, part_bytes,
                       pmax_bytes, &ws)))
     return rc;
-  const EpiArgs ea = make_epi(epi, K);
+  EpiArgs ea = make_epi(epi, K);
+  if (rmax_out) {
+    ea.rmax = rmax_out->p;
+    ea.rmax_stride = rmax_out->stride;
+    rmax_out->chunks = 0;
+  }
+  const bool premax = pre && pre->chunks > 0;
   ColCopy cc{};
   cc.bias = ea.bias;
   cc.gate = ea.gate;
@@ -256,8 +285,11 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   cc.CP = (int64_t)col_cap;
 
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
-                                        pmax_bytes ? ws->pmax : nullptr, cu_count, s);
+  hipError_t e =
+      premax ? launch_act_quant_frags_premax(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, pre->p,
+                                             pre->chunks, pre->stride, cu_count, s)
+             : launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
+                                      pmax_bytes ? ws->pmax : nullptr, cu_count, s);
   if (e != hipSuccess) return hip_error(e, "act_quant launch");
   hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
   int vec = (N % 4 == 0) && aligned16(Y);
@@ -265,13 +297,13 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
   GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count, splitk,
-              splitk > 1 ? ws->part : nullptr};
+              splitk > 1 ? ws->part : nullptr, rmax_out ? &rmax_out->chunks : nullptr};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) return hip_error(e, "qgemm launch");
   if (t_prof) {
     hipEvent_t p2 = prof_mark(s);
     if (p0 && p1 && p2) {
-      t_recs.push_back({"act_quant", p0, p1});
+      t_recs.push_back({premax ? "act_quant_premax" : "act_quant", p0, p1});
       t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg) + (splitk > 1 ? "_splitk" : ""),
                         p1, p2});
     } else {
@@ -423,6 +455,36 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale) {
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
                 void* Y, void* stream) {
   return qlinear_device(w, A, M, K, epi, Y, static_cast<hipStream_t>(stream));
+}
+
+int sdq_ffn(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
+            const float* h, int64_t M, const float* gate, int gate_fma, float* hid, float* x,
+            void* stream) {
+  if (!fc1 || !fc2) return set_error(SDQ_ERR_INVALID, "null weight handle");
+  if (fc2->K != fc1->N || fc2->N != fc1->K)
+    return set_error(SDQ_ERR_INVALID,
+                     "ffn: fc1 is [" + std::to_string(fc1->N) + "," + std::to_string(fc1->K) +
+                         "], fc2 is [" + std::to_string(fc2->N) + "," + std::to_string(fc2->K) +
+                         "]; need fc1 [F,D] and fc2 [D,F]");
+  if (fc1->device != fc2->device)
+    return set_error(SDQ_ERR_INVALID, "ffn: fc1 and fc2 are on different devices");
+  if (!gate || !hid || !x) return set_error(SDQ_ERR_INVALID, "ffn: null gate, hid or x");
+  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
+  if (M == 0) return SDQ_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = ensure_device(fc1->device);
+  if (rc) return rc;
+  // fc1's GELU epilogue writes hid's row maxima (either persistent tile
+  // config: two wave columns per tile) for fc2's quantizer.
+  RowMax rm;
+  rm.stride = (int)round_up(std::max(gemm_rmax_chunks(kCfg128x128, fc1->N),
+                                     gemm_rmax_chunks(kCfg256x256, fc1->N)),
+                            4);
+  if ((rc = rmax_buffer(fc1->device, s, (size_t)M * rm.stride * sizeof(float), &rm.p))) return rc;
+  sdq_epilogue e1{SDQ_EPI_GELU, 1, b1, nullptr, nullptr};
+  if ((rc = qlinear_device(fc1, h, M, fc1->K, &e1, hid, s, nullptr, &rm))) return rc;
+  sdq_epilogue e2{SDQ_EPI_GATED, gate_fma, b2, gate, x};
+  return qlinear_device(fc2, hid, M, fc2->K, &e2, x, s, &rm, nullptr);
 }
 
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream) {

@@ -660,6 +660,11 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     // across the main loop and spill).
     int vlane = voff_lane;
     asm volatile("" : "+v"(vlane));
+    // GELU: running max |Y| of the lane's rows over its columns (for the
+    // next GEMM's activation quantizer); NaN never wins, as in the
+    // quantizer's own max.
+    constexpr bool kRowMax = EPI == SDQ_EPI_GELU;
+    float rm[kRowMax ? FM : 1][4] = {};
 #pragma unroll
     for (int a = 0; a < FN; a++) {
       const int cl = wcol + a * 32 + 4 * rc;  // tile column of this lane's chunk
@@ -708,7 +713,11 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
             }
             if constexpr (EPI == SDQ_EPI_GELU) {
 #pragma unroll
-              for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
+              for (int r = 0; r < 4; r++) {
+                v[r] = gelu_tanh(v[r]);
+                const float av = ok ? fabsf(v[r]) : 0.f;
+                rm[b][i] = rm[b][i] < av ? av : rm[b][i];
+              }
             } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
               const v4f x = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, 0, 0);
               if constexpr (EPI == SDQ_EPI_RESID) {
@@ -731,6 +740,26 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
         }
         // keep the scheduler from hoisting every block's operands at once
         __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if constexpr (kRowMax) {
+      // Lanes rr*8 .. rr*8+7 hold the same rows: reduce over them, then
+      // one lane per row writes the wave's column chunk tn*WN + wn.
+      if (epi.rmax) {
+#pragma unroll
+        for (int b = 0; b < FM; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float m = rm[b][i];
+#pragma unroll
+            for (int d = 1; d < 8; d *= 2) {
+              const float o = __shfl_xor(m, d);
+              m = m < o ? o : m;
+            }
+            const int row = mrow0 + b * 32 + 8 * i;
+            if (rc == 0 && row < M32)
+              epi.rmax[(int64_t)row * epi.rmax_stride + tn * WN + wn] = m;
+          }
       }
     }
     if constexpr (!kOwnScratch) {
@@ -1022,6 +1051,13 @@ int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_coun
   return kCfg128x128;
 }
 
+int gemm_rmax_chunks(int cfg, int64_t N) {
+  // both persistent configs have two wave columns per tile
+  if (cfg == kCfg128x128) return (int)ceil_div(N, 128) * 2;
+  if (cfg == kCfg256x256) return (int)ceil_div(N, 256) * 2;
+  return 0;
+}
+
 int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count) {
   // Long K on a grid that leaves CUs idle: split K so the 128x128 kernel's
   // (tile, k-range) items number at most one per CU (measured: more items
@@ -1051,6 +1087,15 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
   // 32-bit buffer offsets.
   const bool persist = vec && aux.sink && !epi.kzero && KFp * 1024 * 8 <= 0x7FFFFFFF &&
                        N * 4 * 256 <= 0x7FFFFFF0;
+  // Row maxima of a GELU output: written by the persistent kernels only
+  // (not under split-K), one column chunk per wave column of each tile.
+  if (aux.rmax_chunks) *aux.rmax_chunks = 0;
+  const bool rmax = epi.rmax && epi.kind == SDQ_EPI_GELU && persist && aux.splitk <= 1 &&
+                    (cfg == kCfg128x128 || cfg == kCfg256x256) &&
+                    gemm_rmax_chunks(cfg, N) <= epi.rmax_stride;
+  EpiArgs epi_r = epi;
+  if (!rmax) epi_r.rmax = nullptr;
+  else if (aux.rmax_chunks) *aux.rmax_chunks = gemm_rmax_chunks(cfg, N);
   switch (cfg) {
     case kCfgSkinny:
       if (M > kSkinnyMaxM) return hipErrorInvalidValue;
@@ -1066,12 +1111,12 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
         return run_splitk_reduce(aux.part, aux.splitk, M, N, as, bs, epi, Y, s);
       }
       if (persist)
-        return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi, Y,
+        return run_persist<128, 128, 2, 2, 2, 4, 2>(wt, cols, at, as, M, N, KFp, epi_r, Y,
                                                     2 * aux.cu_count, s);
       return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
       if (persist)
-        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi, Y,
+        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y,
                                                     aux.cu_count, s);
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;

@@ -53,6 +53,11 @@ struct EpiArgs {
   const float* bias;
   const float* gate;
   const float* resid;
+  // GELU only (optional): rmax[row * rmax_stride + c] = max |Y[row, n]| over
+  // the n of column chunk c (gemm_rmax_chunks chunks), for the next GEMM's
+  // activation quantizer. Launchers that cannot write it report 0 chunks.
+  float* rmax;
+  int rmax_stride;
 };
 
 // ---- launchers (return hipError_t of the launch) -------------------------
@@ -74,6 +79,13 @@ int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count);
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
                                   int8_t* at, float* as, const ColCopy& cc, float* pmax,
                                   int cu_count, hipStream_t s);
+// Same output, with the row maxima already known: max_c rmax[row*rstride + c]
+// over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
+// read once.
+hipError_t launch_act_quant_frags_premax(const float* A, int64_t M, int64_t K, int64_t Mp,
+                                         int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
+                                         const float* rmax, int rchunks, int rstride,
+                                         int cu_count, hipStream_t s);
 // Same quantizer, row-major int8 output [M,K] (parity API).
 hipError_t launch_act_quant_rowmajor(const float* A, int64_t M, int64_t K, int8_t* aq, float* as,
                                      hipStream_t s);
@@ -111,7 +123,10 @@ struct GemmAux {
   int cu_count;
   int splitk;  // choose_splitk's factor (1 = none)
   int* part;   // splitk x M x N int32 partial sums (splitk > 1)
+  int* rmax_chunks;  // out (nullable): column chunks written to epi.rmax, 0 = none
 };
+// Column chunks of the row maxima a GELU launch of this config writes.
+int gemm_rmax_chunks(int cfg, int64_t N);
 
 hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t* at,
                         const float* as, int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi,

@@ -85,6 +85,33 @@ __device__ __forceinline__ uint4 pack16(const float v[16], float inv) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Max over c < pc of a row's given maxima pm[c] (pm 16-byte aligned), read
+// by the eight lanes l = row + 8j that share the row (lane l takes every
+// eighth float4 from l / 8), then combined across them; `ok` (the row
+// exists) is the same on all eight. Every lane must call it. NaN never
+// enters the maxima, and max is exact and order-free.
+__device__ __forceinline__ float premax_row(const float* __restrict__ pm, int pc, bool ok,
+                                            int l) {
+  float mx = 0.f;
+  if (ok) {
+    const float4* p4 = reinterpret_cast<const float4*>(pm);
+    for (int j = l >> 3; j < pc / 4; j += 8) {
+      const float4 r = p4[j];
+      mx = (mx < r.x) ? r.x : mx;
+      mx = (mx < r.y) ? r.y : mx;
+      mx = (mx < r.z) ? r.z : mx;
+      mx = (mx < r.w) ? r.w : mx;
+    }
+    for (int j = (pc & ~3) + (l >> 3); j < pc; j += 8) mx = (mx < pm[j]) ? pm[j] : mx;
+  }
+#pragma unroll
+  for (int d = 8; d < 64; d *= 2) {
+    const float o = __shfl_xor(mx, d);
+    mx = (mx < o) ? o : mx;
+  }
+  return mx;
+}
+
 // Row-major output variant (the parity API): one workgroup per 32 rows.
 template <int NW, int CACHE, bool FRAG_OUT>
 __global__ void __launch_bounds__(NW * 64)
@@ -167,10 +194,13 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
 // row unit*R + (l % R), half h = (l / R) & 1 of fragment g*F + l / (2R),
 // F = 32 / R fragments per group: the fragment slot (row & 31) + 32h, 16
 // bytes, so each fragment is written as two contiguous runs of 16R bytes.
-template <int R, int NW, int CACHE>
+// PRE: the row maxima come from pre[row * pstride + c], c < pc (written by
+// the producing GEMM), so the row is read once, with no max pass.
+template <int R, int NW, int CACHE, bool PRE>
 __global__ void __launch_bounds__(NW * 64)
 act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
-                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
+                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc,
+                       const float* __restrict__ pre, int pc, int pstride) {
   static_assert(R == 8 || R == 16, "unit height");
   constexpr int F = 32 / R;  // fragments per lane group
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
@@ -197,30 +227,35 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
     const int64_t g = w + (int64_t)c * NW;
     if (g < ng) {
       load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, cache[c]);
-      mx = amax16(cache[c], mx);
+      if constexpr (!PRE) mx = amax16(cache[c], mx);
     }
   }
-  // (loading several groups per iteration here measured slower at large
-  // M: the extra VGPRs cost occupancy, 5 -> 3 waves per SIMD)
-  for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
-    float t[16];
-    load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
-    mx = amax16(t, mx);
-  }
-  // the lanes l + R*j (j = 0 .. 64/R - 1) hold the same row
+  if constexpr (PRE) {
+    static_assert(!PRE || R == 8, "given maxima are read by the 8 lanes of a row");
+    mx = premax_row(pre + (row_ok ? row : 0) * pstride, pc, row_ok, l);
+  } else {
+    // (loading several groups per iteration here measured slower at large
+    // M: the extra VGPRs cost occupancy, 5 -> 3 waves per SIMD)
+    for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
+      float t[16];
+      load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
+      mx = amax16(t, mx);
+    }
+    // the lanes l + R*j (j = 0 .. 64/R - 1) hold the same row
 #pragma unroll
-  for (int d = R; d < 64; d *= 2) {
-    const float o = __shfl_xor(mx, d);
-    mx = (mx < o) ? o : mx;
-  }
-  __shared__ float red[NW][R];
-  if (l < R) red[w][l] = mx;
-  __syncthreads();
-  mx = 0.f;
+    for (int d = R; d < 64; d *= 2) {
+      const float o = __shfl_xor(mx, d);
+      mx = (mx < o) ? o : mx;
+    }
+    __shared__ float red[NW][R];
+    if (l < R) red[w][l] = mx;
+    __syncthreads();
+    mx = 0.f;
 #pragma unroll
-  for (int i = 0; i < NW; i++) {
-    const float r = red[i][l % R];
-    mx = (mx < r) ? r : mx;
+    for (int i = 0; i < NW; i++) {
+      const float r = red[i][l % R];
+      mx = (mx < r) ? r : mx;
+    }
   }
   float sc = mx / 127.f;
   if (sc == 0.f) sc = 1.f;
@@ -281,20 +316,14 @@ act_quant_pmax_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t
     const float o = __shfl_xor(mx, d);
     mx = (mx < o) ? o : mx;
   }
-  // rows of pmax have Cp = C rounded up to 4 floats, the tail zeroed
-  if (l < R) {
-    const int Cp = (C + 3) & ~3;
-    float* pr = pmax + (unit * R + l) * Cp;
-    pr[c] = mx;
-    if (c == C - 1)
-      for (int j = C; j < Cp; j++) pr[j] = 0.f;
-  }
+  // rows of pmax have C rounded up to 4 floats (16-byte aligned rows)
+  if (l < R) pmax[(unit * R + l) * ((C + 3) & ~3) + c] = mx;
 }
 
 template <int GPW>
 __global__ void __launch_bounds__(256)
 act_quant_emit_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
-                      int C, int64_t items, const float* __restrict__ pmax,
+                      int C, int64_t items, const float* __restrict__ pmax, int pc, int pstride,
                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc) {
   constexpr int R = 8, F = 32 / R;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
@@ -318,16 +347,7 @@ act_quant_emit_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t
     const int64_t g = (int64_t)c * GPW + i;
     if (g < ng) load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, v[i]);
   }
-  const int Cp = (C + 3) & ~3;
-  const float4* pm = reinterpret_cast<const float4*>(pmax + (unit * R + l % R) * Cp);
-  float mx = 0.f;
-  for (int j = 0; j < Cp / 4; j++) {
-    const float4 r = pm[j];
-    mx = (mx < r.x) ? r.x : mx;
-    mx = (mx < r.y) ? r.y : mx;
-    mx = (mx < r.z) ? r.z : mx;
-    mx = (mx < r.w) ? r.w : mx;
-  }
+  const float mx = premax_row(pmax + (row_ok ? row : 0) * pstride, pc, row_ok, l);
   float sc = mx / 127.f;
   if (sc == 0.f) sc = 1.f;
   const float inv = 1.f / sc;
@@ -371,25 +391,53 @@ hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t 
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
   const int64_t units = Mp / kQuantRows;
   if (pmax && act_quant_pmax_floats(Mp, KFp, cu_count) > 0) {
-    const int C = (int)split_chunks(Mp, KFp);
+    const int C = (int)split_chunks(Mp, KFp), Cp = (C + 3) & ~3;
     const int64_t items = units * C;
     const unsigned blocks = (unsigned)ceil_div(items, 4);
     if (split_gpw(Mp) == 4) {
       hipLaunchKernelGGL((act_quant_pmax_kernel<4>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
                          vec, C, items, pmax);
       hipLaunchKernelGGL((act_quant_emit_kernel<4>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
-                         vec, C, items, pmax, at, as, cc);
+                         vec, C, items, pmax, C, Cp, at, as, cc);
     } else {
       hipLaunchKernelGGL((act_quant_pmax_kernel<2>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
                          vec, C, items, pmax);
       hipLaunchKernelGGL((act_quant_emit_kernel<2>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
-                         vec, C, items, pmax, at, as, cc);
+                         vec, C, items, pmax, C, Cp, at, as, cc);
     }
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache>),
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false>),
                      dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
-                     at, as, cc);
+                     at, as, cc, nullptr, 0, 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_frags_premax(const float* A, int64_t M, int64_t K, int64_t Mp,
+                                         int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
+                                         const float* rmax, int rchunks, int rstride,
+                                         int cu_count, hipStream_t s) {
+  if (!rmax || rchunks < 1 || rstride < rchunks || (rstride & 3) || !aligned16(rmax))
+    return hipErrorInvalidValue;
+  const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
+  const int64_t units = Mp / kQuantRows;
+  // Few long rows: the split form's second kernel alone, over the whole GPU.
+  if (units < 2 * (int64_t)(cu_count > 0 ? cu_count : 256) &&
+      KFp > (int64_t)kQuantUnitCache * kQuantUnitWaves * (32 / kQuantRows)) {
+    const int C = (int)split_chunks(Mp, KFp);
+    const int64_t items = units * C;
+    const unsigned blocks = (unsigned)ceil_div(items, 4);
+    if (split_gpw(Mp) == 4)
+      hipLaunchKernelGGL((act_quant_emit_kernel<4>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, rmax, rchunks, rstride, at, as, cc);
+    else
+      hipLaunchKernelGGL((act_quant_emit_kernel<2>), dim3(blocks), dim3(256), 0, s, A, M, K, KFp,
+                         vec, C, items, rmax, rchunks, rstride, at, as, cc);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, true>),
+                     dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
+                     at, as, cc, rmax, rchunks, rstride);
   return hipGetLastError();
 }
 

@@ -37,19 +37,21 @@ DitBlock::DitBlock(const LinearPart (&l)[kCount], bool fusion, bool on_device) :
 void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   need(io.M >= 0 && io.Mc >= 0 && io.Mt >= 0, "negative row count");
   need(io.x && io.gate_sa && io.gate_ffn, "x and gates are required");
-  // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-189, 168-174)
+  // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-188, 205-212)
   qkv_.forward_device(io.h_sa, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.qkv, s);
   o_.forward_device(io.att, io.M, SDQ_EPI_GATED, io.gate_sa, io.x, io.x, s);
   // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
-  // the other branch, then x += o(xt)                (ovi_dit.cpp:206-241)
+  // the other branch, then x += o(xt)                (ovi_dit.cpp:229-254)
   cq_.forward_device(io.xq, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.cq, s);
   if (io.Mc > 0) ckv_.forward_device(io.ctx, io.Mc, SDQ_EPI_NONE, nullptr, nullptr, io.ckv, s);
   if (fusion_ && io.Mt > 0)
     kvf_.forward_device(io.tn, io.Mt, SDQ_EPI_NONE, nullptr, nullptr, io.kvt, s);
   co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
-  // ffn: hid = gelu(fc1(h)); x += fc2(hid) * e[5]    (ovi_dit.cpp:196-204)
-  fc1_.forward_device(io.h_ffn, io.M, SDQ_EPI_GELU, nullptr, nullptr, io.hid, s);
-  fc2_.forward_device(io.hid, io.M, SDQ_EPI_GATED, io.gate_ffn, io.x, io.x, s);
+  // ffn: hid = gelu(fc1(h)); x += fc2(hid) * e[5]    (ovi_dit.cpp:214-222); one
+  // call, so fc1's epilogue hands hid's row maxima to fc2's quantizer
+  check(sdq_ffn(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.h_ffn,
+                io.M, io.gate_ffn, 1, io.hid, io.x, s),
+        "DitBlock ffn");
 }
 
 double DitBlock::ops(int64_t M, int64_t Mc, int64_t Mt) const {

@@ -63,6 +63,7 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_ffn": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _vp, _vp]),
     "sdq_qlinear_host": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp]),
     "sdq_act_quant": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "sdq_device_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
@@ -206,6 +207,15 @@ def qgemm(w: Weight, A, out, stream=None):
     M, K = A.shape
     _check(_lib.sdq_qgemm(w.h, _ptr(A), M, K, _ptr(out), _stream(stream)))
     return out
+
+
+def ffn(fc1: Weight, b1, fc2: Weight, b2, h, gate, hid, x, gate_fma=True, stream=None):
+    """hid = gelu_tanh(mlin(h, fc1)); x = fma(mlin(hid, fc2), gate, x), in place
+    (ovi_dit.cpp:218-221), device tensors, stream-ordered."""
+    M = h.shape[0]
+    _check(_lib.sdq_ffn(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(h), M, _ptr(gate),
+                        1 if gate_fma else 0, _ptr(hid), _ptr(x), _stream(stream)))
+    return x
 
 
 def qlinear_host(w: Weight, A: np.ndarray, kind="none", bias=None, gate=None, resid=None,
