@@ -258,6 +258,29 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
 
   const int cfg = choose_gemm_cfg(M, N, w->KFp, epi ? epi->kind : SDQ_EPI_NONE,
                                   g_dev[w->device].cu_count);
+  if (cfg == kCfgSkinny && qin_fits(M, K, w->KFp) && !std::getenv("SDQ_NO_QIN")) {
+    // a few rows: the GEMM quantizes them itself (SDQ_NO_QIN: the two-launch
+    // path, for comparisons)
+    const EpiArgs ea = make_epi(epi, K);
+    int vec = (N % 4 == 0) && aligned16(Y);
+    if (ea.bias) vec = vec && aligned16(ea.bias);
+    if (ea.gate) vec = vec && aligned16(ea.gate);
+    if (ea.resid) vec = vec && aligned16(ea.resid);
+    if (rmax_out) rmax_out->chunks = 0;
+    hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+    hipError_t e = launch_qgemm_qin(w->frags, w->scale, A, M, K, N, w->KFp, ea, Y, vec, s);
+    if (e != hipSuccess) return hip_error(e, "qgemm launch");
+    if (t_prof) {
+      hipEvent_t p1 = prof_mark(s);
+      if (p0 && p1) {
+        t_recs.push_back({"qgemm_skinny_qin", p0, p1});
+      } else {
+        for (hipEvent_t ev : {p0, p1})
+          if (ev) (void)hipEventDestroy(ev);
+      }
+    }
+    return SDQ_OK;
+  }
   const int64_t Mp = round_up(M, gemm_cfg_bm(cfg));
   const size_t at_bytes = (size_t)(Mp / kFragRows) * (size_t)w->KFp * kFragBytes;
   const size_t col_cap = (size_t)(w->Np + kColPad);

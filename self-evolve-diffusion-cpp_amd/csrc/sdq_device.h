@@ -25,6 +25,18 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // vmcnt[5:4] at [15:14]; the other counters are left at their maximum).
 constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
 
+// One activation value -> int8 (src/core/qgemm.cpp:62-69, 94): y = v*inv,
+// round half to even; NaN and |t| >= 2^31 give -127 (x86 cvtss2si returns
+// INT_MIN, which the clamp maps to -127); else clamp to [-127, 127].
+__device__ __forceinline__ int quant_one(float v, float inv) {
+  const float y = v * inv;
+  const float t = __builtin_rintf(y);  // v_rndne_f32: ties to even
+  // NaN and |t| >= 2^31 fail this test, like cvtss2si returning INT_MIN.
+  if (!(t >= -2147483648.0f && t < 2147483648.0f)) return -127;
+  const float c = t < -127.f ? -127.f : (t > 127.f ? 127.f : t);
+  return (int)c;
+}
+
 __device__ __forceinline__ float gelu_tanh(float v) {
   // nn.GELU(approximate='tanh'), src/model/ovi_dit.cpp:132-142.
   const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);

@@ -784,7 +784,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 // anyway). Small M is latency-bound on the tiled kernels (a 128x128 tile
 // walks all of K alone); here every CU that holds a workgroup streams a
 // quarter of K per wave.
-template <int FMS, int SPLIT>
+template <int FMS, int SPLIT, int D>
 __global__ void __launch_bounds__(SPLIT * 64)
 qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
              const int8_t* __restrict__ at, const float* __restrict__ as, int64_t M, int64_t N,
@@ -822,16 +822,20 @@ qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
       for (int j = 0; j < FMS; j++)
         acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x.a[u], x.b[u][j], acc[j], 0, 0, 0);
   };
-  Grp c0, c1;
-  load(0, c0);  // ngrp >= 1 (KFp >= 8)
-  int64_t g = 0;
-  for (; g + 1 < ngrp; g += 2) {
-    load(g + 1, c1);
-    mma(c0);
-    if (g + 2 < ngrp) load(g + 2, c0);
-    mma(c1);
+  // D groups in flight: group g + D loads while groups g+1 .. g+D-1 multiply
+  Grp c[D];
+#pragma unroll
+  for (int d = 0; d < D; d++)
+    if (d < ngrp) load(d, c[d]);
+  for (int64_t g = 0; g < ngrp; g += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      if (g + d < ngrp) {
+        mma(c[d]);
+        if (g + d + D < ngrp) load(g + d + D, c[d]);
+      }
+    }
   }
-  if (g < ngrp) mma(c0);
 
   __shared__ int red[SPLIT][16][64];
   const int64_t n_lane = rb * 32 + (lane >> 5) * 4;
@@ -854,6 +858,133 @@ qgemm_skinny(const int8_t* __restrict__ wt, const float* __restrict__ bs,
       store_block(s, m, n_lane, M, N, as_m, bs, epi, Y, vec);
     }
     __syncthreads();
+  }
+}
+
+// Tiny M (M <= kQinMaxM rows): the skinny kernel (one row fragment) with the
+// activation quantizer folded in. Every workgroup quantizes the few rows of
+// A itself, with the quantizer's exact steps (max |a| with NaN never
+// winning, sc = mx/127 or 1, inv = 1/sc, quant_one), into LDS (M rows of
+// KFp*32 bytes, zero-padded values beyond K): M*K*4 bytes read from L2 per
+// workgroup (12 KB at M = 1, K = 3072), so the call is one launch with no
+// quantized-activation round trip.
+template <int SPLIT, int D>
+__global__ void __launch_bounds__(SPLIT * 64)
+qgemm_skinny_qin(const int8_t* __restrict__ wt, const float* __restrict__ bs,
+                 const float* __restrict__ A, int64_t M, int64_t K, int64_t N, int64_t KFp,
+                 EpiArgs epi, void* Y, int vec, int avec) {
+  extern __shared__ __attribute__((aligned(16))) int8_t aqs[];  // [M][KFp * 32]
+  __shared__ float rmx[SPLIT][kQinMaxM];
+  __shared__ float rsc[kQinMaxM], rinv[kQinMaxM];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  constexpr int NT = SPLIT * 64;
+  const int64_t KB = KFp * 32;  // bytes per quantized row
+  const int Mi = (int)M;
+  for (int r = 0; r < Mi; r++) {
+    const float* row = A + r * K;
+    float mx = 0.f;
+    if (avec) {
+      for (int64_t k4 = tid; k4 < K / 4; k4 += NT) {
+        const float4 v = reinterpret_cast<const float4*>(row)[k4];
+        const float a[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
+#pragma unroll
+        for (int e = 0; e < 4; e++) mx = (mx < a[e]) ? a[e] : mx;
+      }
+    } else {
+      for (int64_t k = tid; k < K; k += NT) {
+        const float a = fabsf(row[k]);
+        mx = (mx < a) ? a : mx;
+      }
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+      const float o = __shfl_xor(mx, d);
+      mx = (mx < o) ? o : mx;
+    }
+    if (lane == 0) rmx[w][r] = mx;
+  }
+  __syncthreads();
+  if (tid < Mi) {
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < SPLIT; i++) mx = (mx < rmx[i][tid]) ? rmx[i][tid] : mx;
+    float sc = mx / 127.f;
+    if (sc == 0.f) sc = 1.f;
+    rsc[tid] = sc;
+    rinv[tid] = 1.f / sc;
+  }
+  __syncthreads();
+  for (int r = 0; r < Mi; r++) {
+    const float* row = A + r * K;
+    const float inv = rinv[r];
+    for (int64_t k4 = tid; k4 < KB / 4; k4 += NT) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int64_t k = 4 * k4 + e;
+        const float v = k < K ? row[k] : 0.f;
+        x |= (uint32_t)(uint8_t)(int8_t)quant_one(v, inv) << (8 * e);
+      }
+      *reinterpret_cast<uint32_t*>(aqs + r * KB + 4 * k4) = x;
+    }
+  }
+  __syncthreads();
+
+  const int64_t rb = blockIdx.x;
+  const int8_t* wp = wt + rb * KFp * 1024 + lane * 16;
+  const int arow = lane & 31;
+  const int8_t* ap = aqs + (arow < Mi ? arow : 0) * KB + 16 * (lane >> 5);
+  v16i acc = v16i{};
+  constexpr int U = 2;
+  static_assert(U * SPLIT == 8, "groups tile KFp exactly");
+  const int64_t ngrp = KFp / (U * SPLIT);
+  struct Grp {
+    v4i a[U], b[U];
+  };
+  auto load = [&](int64_t g, Grp& x) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t kb = w + (g * U + u) * SPLIT;
+      x.a[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + kb * 1024));
+      x.b[u] = arow < Mi ? *reinterpret_cast<const v4i*>(ap + kb * 32) : v4i{};
+    }
+  };
+  auto mma = [&](const Grp& x) {
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(x.a[u], x.b[u], acc, 0, 0, 0);
+  };
+  // D groups in flight: group g + D loads while groups g+1 .. g+D-1 multiply
+  Grp c[D];
+#pragma unroll
+  for (int d = 0; d < D; d++)
+    if (d < ngrp) load(d, c[d]);
+  for (int64_t g = 0; g < ngrp; g += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      if (g + d < ngrp) {
+        mma(c[d]);
+        if (g + d + D < ngrp) load(g + d + D, c[d]);
+      }
+    }
+  }
+
+  __shared__ int red[SPLIT][16][64];
+#pragma unroll
+  for (int r = 0; r < 16; r++) red[w][r][lane] = acc[r];
+  __syncthreads();
+  if (w == 0) {
+    v16i sacc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      int t = red[0][r][lane];
+#pragma unroll
+      for (int ww = 1; ww < SPLIT; ww++) t += red[ww][r][lane];
+      sacc[r] = t;
+    }
+    const int64_t m = lane & 31;
+    const float as_m = (m < M) ? rsc[m] : 0.f;
+    store_block(sacc, m, rb * 32 + (lane >> 5) * 4, M, N, as_m, bs, epi, Y, vec);
   }
 }
 
@@ -990,6 +1121,10 @@ hipError_t run_splitk_reduce(const int* part, int S, int64_t M, int64_t N, const
   return hipGetLastError();
 }
 
+// Groups in flight per wave in the skinny kernels (4 vs 2: equal within
+// noise at M=1..64, 1-7% better at M=5..20 with long K).
+constexpr int kSkinnyDepth = 4;
+
 template <int FMS>
 hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const float* as,
                       int64_t M, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y, int vec,
@@ -998,8 +1133,9 @@ hipError_t run_skinny(const int8_t* wt, const float* bs, const int8_t* at, const
   const int64_t blocks = ceil_div(N, 32);
   if (blocks <= 0) return hipSuccess;
   if (KFp % 8 != 0 || KFp < 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((qgemm_skinny<FMS, SPLIT>), dim3((unsigned)blocks), dim3(SPLIT * 64), 0, s,
-                     wt, bs, at, as, M, N, KFp, epi, Y, vec);
+  constexpr int D = FMS <= 2 ? kSkinnyDepth : 2;  // register budget of the wider groups
+  hipLaunchKernelGGL((qgemm_skinny<FMS, SPLIT, D>), dim3((unsigned)blocks), dim3(SPLIT * 64), 0,
+                     s, wt, bs, at, as, M, N, KFp, epi, Y, vec);
   return hipGetLastError();
 }
 
@@ -1020,6 +1156,25 @@ hipError_t run_skinny_m(const int8_t* wt, const float* bs, const int8_t* at, con
 }
 
 }  // namespace
+
+bool qin_fits(int64_t M, int64_t K, int64_t KFp) {
+  // Every workgroup reads and quantizes M*K values first: worth it up to
+  // M*K = 8192 (measured, N=18432: M=1 21.8 -> 12.6 us, M=2 22.3 -> 15.5,
+  // M=4 22.6 -> 20.8 at K=3072; at M=4, K=14336 it loses, 30.6 -> 51).
+  return M >= 1 && M <= kQinMaxM && K > 0 && M * K <= 8192 && M * KFp * 32 <= kQinMaxLds;
+}
+
+hipError_t launch_qgemm_qin(const int8_t* wt, const float* bs, const float* A, int64_t M,
+                            int64_t K, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
+                            int vec, hipStream_t s) {
+  if (!qin_fits(M, K, KFp) || KFp % 8 != 0 || epi.kzero) return hipErrorInvalidValue;
+  const int64_t blocks = ceil_div(N, 32);
+  if (blocks <= 0) return hipSuccess;
+  const int avec = ((reinterpret_cast<uintptr_t>(A) & 15) == 0 && K % 4 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((qgemm_skinny_qin<4, kSkinnyDepth>), dim3((unsigned)blocks), dim3(4 * 64),
+                     (unsigned)(M * KFp * 32), s, wt, bs, A, M, K, N, KFp, epi, Y, vec, avec);
+  return hipGetLastError();
+}
 
 int gemm_cfg_bm(int cfg) {
   switch (cfg) {

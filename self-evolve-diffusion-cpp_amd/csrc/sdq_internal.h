@@ -109,6 +109,14 @@ constexpr int64_t kSkinnyMaxM = 256;
 int gemm_cfg_bm(int cfg);  // activation rows per tile (row padding of `at`)
 const char* gemm_cfg_name(int cfg);
 int choose_gemm_cfg(int64_t M, int64_t N, int64_t KFp, int epi_kind, int cu_count);
+// Tiny M: the skinny GEMM quantizes A itself (one launch). qin_fits says
+// whether M rows of K fit (M <= kQinMaxM, M*KFp*32 bytes of LDS <= kQinMaxLds).
+constexpr int kQinMaxM = 4;
+constexpr int64_t kQinMaxLds = 64 * 1024;
+bool qin_fits(int64_t M, int64_t K, int64_t KFp);
+hipError_t launch_qgemm_qin(const int8_t* wt, const float* bs, const float* A, int64_t M,
+                            int64_t K, int64_t N, int64_t KFp, const EpiArgs& epi, void* Y,
+                            int vec, hipStream_t s);
 // Split-K factor for the 128x128 kernel at this shape (1 = no split).
 int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count);
 

@@ -19,11 +19,14 @@
 #include <cstdlib>
 
 #include "sdq_internal.h"
+#include "sdq_device.h"
 
 #pragma clang fp contract(off)
 
 namespace sdq {
 namespace {
+
+using dev::quant_one;
 
 constexpr int kQuantWaves = 16;
 constexpr int kQuantCache = 6;  // 16 waves x 6 frags x 32 = K <= 3072 in one pass
@@ -34,14 +37,6 @@ constexpr int kQuantRows = 8;
 constexpr int kQuantUnitWaves = 8;
 constexpr int kQuantUnitCache = 3;
 
-__device__ __forceinline__ int quant_one(float v, float inv) {
-  const float y = v * inv;
-  const float t = __builtin_rintf(y);  // v_rndne_f32: ties to even
-  // NaN and |t| >= 2^31 fail this test, like cvtss2si returning INT_MIN.
-  if (!(t >= -2147483648.0f && t < 2147483648.0f)) return -127;
-  const float c = t < -127.f ? -127.f : (t > 127.f ? 127.f : t);
-  return (int)c;
-}
 
 __device__ __forceinline__ void load16(const float* __restrict__ rowp, int64_t k0, int64_t K,
                                        bool row_ok, bool vec, float v[16]) {

@@ -380,3 +380,54 @@ def test_splitk_epilogues_bitexact(sdq_dev, oracle, M, K, N):
     want = oracle.linear(A, q, s, bias=bias, epilogue="gelu")
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     assert np.all(err <= 1e-6 * (1.0 + np.abs(want))), float(err.max())
+
+
+# ------------------------------------------------- tiny M, quantized in-kernel
+# M <= 4 rows: the skinny GEMM quantizes A itself (every workgroup, into LDS).
+@pytest.mark.parametrize("M,K,N", [(1, 3072, 18432), (2, 3072, 3072), (3, 31, 13), (4, 14336, 3072),
+                                   (4, 257, 516), (1, 1, 64)])
+def test_tiny_m_in_kernel_quant_bitexact(sdq_dev, oracle, M, K, N):
+    import sdq
+
+    print(f"[qin] M={M} K={K} N={N}", flush=True)
+    A, q, s, bias = _inputs(M, K, N, seed=7 * M + K + N)
+    A[0, 0] = np.float32(-A[0].__abs__().max() * 2)  # the row max is a negative value
+    w = sdq.Weight.from_host(q, s)
+    gate = oracle.randn(N, 77)
+    x = oracle.randn(M * N, 78).reshape(M, N)
+    assert_bitexact(_run(sdq_dev, w, A), oracle.qgemm(A, q, s), "qgemm")
+    assert_bitexact(_run(sdq_dev, w, A, bias=bias), oracle.linear(A, q, s, bias=bias), "mlin")
+    got = _run(sdq_dev, w, A, kind="gated", bias=bias, gate=gate, resid=x)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x),
+                    "gated")
+    got = _run(sdq_dev, w, A, kind="resid", bias=bias, resid=x)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias, epilogue="resid", resid=x), "resid")
+    aq, _ = oracle.act_quant(A)
+    assert_bitexact(_run(sdq_dev, w, A, kind="acc"), oracle.qgemm_acc(aq, q), "acc")
+
+
+def test_tiny_m_special_rows_and_unaligned(sdq_dev, oracle):
+    """The reference's special rows (zero, NaN, +-Inf, denormal, huge, ties)
+    in groups of 1..4 rows, through the in-kernel quantizer; then A and Y at
+    4-byte aligned addresses (scalar loads)."""
+    import torch
+
+    import sdq
+
+    r = np.load(os.path.join(GOLDEN, "ref_qgemm.npz"))
+    A_all, bq, bs, want = r["special_a"], r["special_bq"], r["special_bs"], r["special_out"]
+    w = sdq.Weight.from_host(bq, bs)
+    for M in (1, 2, 3, 4):
+        for i0 in range(0, A_all.shape[0] - M + 1, M):
+            got = _run(sdq_dev, w, A_all[i0:i0 + M])
+            assert_bitexact(got, want[i0:i0 + M], f"special rows {i0}..{i0 + M - 1}")
+    M, K, N = 3, 1028, 516
+    A, q, s, bias = _inputs(M, K, N, seed=33)
+    w = sdq.Weight.from_host(q, s)
+    Abuf = torch.zeros(M * K + 1, device=sdq_dev)
+    Abuf[1:] = torch.from_numpy(A.ravel()).to(sdq_dev)
+    Ybuf = torch.zeros(M * N + 1, device=sdq_dev)
+    sdq.qlinear(w, Abuf[1:].view(M, K), Ybuf[1:].view(M, N), bias=torch.from_numpy(bias).to(sdq_dev))
+    torch.cuda.synchronize()
+    assert_bitexact(Ybuf[1:].view(M, N).cpu().numpy(), oracle.linear(A, q, s, bias=bias),
+                    "unaligned tiny M")
