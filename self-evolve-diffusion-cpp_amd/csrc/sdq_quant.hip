@@ -366,18 +366,24 @@ int64_t split_chunks(int64_t Mp, int64_t KFp) {
 
 }  // namespace
 
+// The split form pays a second launch and a re-read from L2; it wins for
+// long rows (several times the single kernel's register cache) in few 8-row
+// units. Measured (single vs split, us): K=14336: M=157 30.5 / 12.7, M=768
+// 31.3 / 22.1, M=2048 36.1 / 44.6; K=8192: M=157 18.0 / 9.6, M=768 17.2 /
+// 15.0, M=2048 24.3 / 28.0; K=6144: M=157 14.3 / 9.9, M=512 13.2 / 12.2,
+// M=768 13.8 / 15.2; K=4096: M=512 10.6 / 12.9; K=3072: M=157 7.4 / 9.1.
+// (cu_count scales the unit limits from the 256-CU part.)
+bool split_wins(int64_t units, int64_t KFp, int cu_count) {
+  const int64_t c = cu_count > 0 ? cu_count : 256;
+  if (KFp >= 256) return units * 2 < c;  // K >= 8192: M < 1024
+  if (KFp >= 192) return units * 4 <= c;  // K >= 6144: M <= 512
+  return false;
+}
+
 int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count) {
-  // The split form pays a second launch and a re-read from L2; it wins
-  // where a row does not fit the single kernel's register cache and the
-  // 8-row units are too few to fill every CU twice (measured at K=14336:
-  // M=157 12.7 vs 30.5 us, M=768 22.1 vs 31.3; at K=3072 the single
-  // kernel wins, 7.4 vs 9.1 at M=157). SDQ_QUANT_SINGLE forces the single
-  // kernel, for comparisons.
+  // SDQ_QUANT_SINGLE forces the single kernel, for comparisons.
   if (std::getenv("SDQ_QUANT_SINGLE")) return 0;
-  const int64_t units = Mp / kQuantRows;
-  if (units >= 2 * (int64_t)(cu_count > 0 ? cu_count : 256)) return 0;
-  if (KFp <= (int64_t)kQuantUnitCache * kQuantUnitWaves * (32 / kQuantRows) || std::getenv("TMP_B1")) return 0;
-  return Mp * ((split_chunks(Mp, KFp) + 3) & ~3);
+  return split_wins(Mp / kQuantRows, KFp, cu_count) ? Mp * ((split_chunks(Mp, KFp) + 3) & ~3) : 0;
 }
 
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
@@ -417,8 +423,7 @@ hipError_t launch_act_quant_frags_premax(const float* A, int64_t M, int64_t K, i
   const int vec = (aligned16(A) && (K % 4) == 0) ? 1 : 0;
   const int64_t units = Mp / kQuantRows;
   // Few long rows: the split form's second kernel alone, over the whole GPU.
-  if (units < 2 * (int64_t)(cu_count > 0 ? cu_count : 256) &&
-      KFp > (int64_t)kQuantUnitCache * kQuantUnitWaves * (32 / kQuantRows)) {
+  if (split_wins(units, KFp, cu_count)) {
     const int C = (int)split_chunks(Mp, KFp);
     const int64_t items = units * C;
     const unsigned blocks = (unsigned)ceil_div(items, 4);
