@@ -385,6 +385,18 @@ def main():
             traffic = tj[key]["qgemm_hbm_bytes_per_launch"]
     except (OSError, ValueError, KeyError):
         traffic = None
+    # MFMA busy fraction of the GEMM's active cycles and its active cycles per
+    # XCD (rocprofv3 PMC, profiles/mfma_util.json): with this run's GEMM time
+    # they give the effective shader clock.
+    mfma = {}
+    if (M, K, N) == (M_NS, K_NS, N_NS):
+        try:
+            with open(os.path.join(ROOT, "profiles", "mfma_util.json")) as f:
+                mj = json.load(f)
+            mfma = {"mfma_busy_frac_pmc": mj["mfma_busy_frac"],
+                    "sclk_ghz_effective": round(mj["gui_active_cycles_per_xcd"] / (gemm_ms * 1e6), 3)}
+        except (OSError, ValueError, KeyError):
+            mfma = {}
 
     line = {
         "metric": "int8 qGEMM TOPS + % of MI355X MFMA peak at M=27280,K=3072,N=14336",
@@ -405,7 +417,7 @@ def main():
                    "gemm_kernel": gemm_name, "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
                    "act_quant_ms": round(q_ms / max(q_launch, 1), 5),
                    "gemm_ms": round(gemm_ms, 5), "weight_repack_ms": round(repack_ms, 3),
-                   "device": info},
+                   **mfma, "device": info},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
                      "traffic": traffic},
