@@ -128,6 +128,27 @@ int sdq_ffn(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const
             const float* h, int64_t M, const float* gate, int gate_fma, float* hid, float* x,
             void* stream);
 
+/* The DiT's norm + modulation folded into the activation quantizer:
+ *   Y = epilogue(qgemm(mod_rows(layernorm(x, eps), shift, scale), W))
+ * for the Linears that read a normalized, modulated copy of the residual
+ * stream: q|k|v after norm1 (src/model/ovi_dit.cpp:208-210) and ffn fc1
+ * after norm2 (216-218). layernorm is blk::layernorm without affine
+ * (src/model/blocks.cpp:18-43), mod_rows is x*(1+scale)+shift
+ * (ovi_dit.cpp:161-172); both bit-exact with the reference build (serial
+ * float sums in k order; mod_rows as one fused multiply-add). shift, scale:
+ * [K] device vectors; the normalized rows are never written to memory. */
+int sdq_qlinear_lnmod(const sdq_weight* w, const float* x, int64_t M, int64_t K,
+                      const float* shift, const float* scale, float eps,
+                      const sdq_epilogue* epi, void* Y, void* stream);
+
+/* ffn_fwd whole (src/model/ovi_dit.cpp:214-222): h = mod_rows(layernorm(x),
+ * shift, scale); hid = gelu_tanh(mlin(h, fc1)); x = fma(mlin(hid, fc2),
+ * gate, x). x [M,D] is the norm's input and the residual, updated in place;
+ * hid [M,F] is written. Same bits as sdq_ffn on the reference's h. */
+int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
+                  float* x, int64_t M, const float* shift, const float* scale, float eps,
+                  const float* gate, int gate_fma, float* hid, void* stream);
+
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
 

@@ -44,6 +44,8 @@ def _load():
     lib.orc_gated_add.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_int]
     lib.orc_add.argtypes = [_f32p, _f32p, _i64]
     lib.orc_gelu_tanh.argtypes = [_f32p, _i64]
+    lib.orc_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
+    lib.orc_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
     lib.orc_quantize_rowwise.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
     lib.orc_quant_rows.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
     lib.orc_randu.argtypes = [_f32p, _i64, ctypes.c_uint64]
@@ -184,6 +186,25 @@ def gelu_tanh(x):
     return x
 
 
+def layernorm(x, eps=1e-6):
+    """blocks.cpp:18-43 with no affine (the DiT's norm1/norm2)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, N = x.shape
+    y = np.empty_like(x)
+    lib().orc_layernorm(x, M, N, eps, y)
+    return y
+
+
+def mod_rows(x, shift, scale):
+    """ovi_dit.cpp:161-172: x*(1+scale)+shift (fused multiply-add)."""
+    x = np.ascontiguousarray(x, np.float32)
+    L, C = x.shape
+    y = np.empty_like(x)
+    lib().orc_mod_rows(x, np.ascontiguousarray(shift, np.float32),
+                       np.ascontiguousarray(scale, np.float32), L, C, y)
+    return y
+
+
 def quantize_rowwise(W):
     W = np.ascontiguousarray(W, np.float32)
     N, K = W.shape
@@ -258,6 +279,10 @@ class Ref:
             ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
             ctypes.POINTER(ctypes.c_int), ctypes.c_char_p, ctypes.c_int]
         L.sdref_sdcpp_lookup.restype = ctypes.c_int
+        L.sdref_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
+        L.sdref_layernorm.restype = ctypes.c_int
+        L.sdref_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
+        L.sdref_mod_rows.restype = ctypes.c_int
         self.L = L
         self.set_nthreads(nthreads or nthreads_default())
 
@@ -287,6 +312,23 @@ class Ref:
         s = np.empty((N,), np.float32)
         self.L.sdref_quantize_rowwise(W, N, K, q, s)
         return q, s
+
+    def layernorm(self, x, eps=1e-6):
+        x = np.ascontiguousarray(x, np.float32)
+        M, N = x.shape
+        y = np.empty_like(x)
+        if self.L.sdref_layernorm(x, M, N, eps, y) != 0:
+            raise RuntimeError("reference layernorm threw")
+        return y
+
+    def mod_rows(self, x, shift, scale):
+        x = np.ascontiguousarray(x, np.float32)
+        L, C = x.shape
+        y = np.empty_like(x)
+        if self.L.sdref_mod_rows(x, np.ascontiguousarray(shift, np.float32),
+                                 np.ascontiguousarray(scale, np.float32), L, C, y) != 0:
+            raise RuntimeError("reference mod_rows threw")
+        return y
 
     def randu(self, n, seed):
         x = np.empty((n,), np.float32)

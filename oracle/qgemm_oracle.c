@@ -26,6 +26,11 @@
  *                          y*g+x rounded once (exact for fp32 inputs).
  *   orc_add              - numpy float32 add.
  *   orc_gelu_tanh        - float64 closed form within tolerance only.
+ *   orc_layernorm        - compiled reference blk::layernorm (oracle/_ref)
+ *                          bit-exact, incl. zero, constant, tiny and huge rows;
+ *                          float64 closed form within tolerance.
+ *   orc_mod_rows         - compiled reference mod_rows (oracle/_ref) bit-exact;
+ *                          float64 x*(1+h)+s rounded once.
  *   orc_quantize_rowwise - compiled reference sd::quantize_rowwise bit-exact,
  *                          reference golden replica (lround) bit-exact.
  *   orc_quant_rows       - closed form of the packer's numpy expression
@@ -212,6 +217,44 @@ void orc_gated_add(float* x, const float* y, const float* g, int64_t M, int64_t 
 /* src/model/ovi_dit.cpp:144-149 add_inplace: x += y. */
 void orc_add(float* x, const float* y, int64_t n) {
   for (int64_t i = 0; i < n; i++) x[i] = x[i] + y[i];
+}
+
+/* src/model/blocks.cpp:18-43 blk::layernorm with w = b = nullptr (the DiT's
+ * norm1 / norm2 before the self-attention and the FFN, ovi_dit.cpp:208, 216),
+ * as the reference build compiles it (pinned against oracle/_ref): the mean
+ * and the variance are serial float sums in k order; the variance adds the
+ * rounded d*d (not contracted); inv = 1/sqrtf(var/N + eps); the output is
+ * (x - mu)*inv*1 + 0 (the +0 turns -0 into +0). */
+void orc_layernorm(const float* x, int64_t M, int64_t N, float eps, float* y) {
+  for (int64_t i = 0; i < M; i++) {
+    const float* r = x + i * N;
+    float mu = 0.f;
+    for (int64_t k = 0; k < N; k++) mu = mu + r[k];
+    mu = mu / (float)N;
+    float var = 0.f;
+    for (int64_t k = 0; k < N; k++) {
+      const float d = r[k] - mu;
+      const float dd = d * d;
+      var = var + dd;
+    }
+    const float inv = 1.f / sqrtf(var / (float)N + eps);
+    for (int64_t k = 0; k < N; k++) {
+      const float t = (r[k] - mu) * inv;
+      y[i * N + k] = t * 1.f + 0.f;
+    }
+  }
+}
+
+/* src/model/ovi_dit.cpp:161-172 mod_rows: y = x*(1+scale)+shift with scale,
+ * shift [C] broadcast over rows; the reference build contracts it to
+ * fmaf(x, 1+scale, shift) (pinned against oracle/_ref). */
+void orc_mod_rows(const float* x, const float* shift, const float* scale, int64_t L, int64_t C,
+                  float* y) {
+  for (int64_t l = 0; l < L; l++)
+    for (int64_t c = 0; c < C; c++) {
+      const float a = 1.f + scale[c];
+      y[l * C + c] = fmaf(x[l * C + c], a, shift[c]);
+    }
 }
 
 /* src/model/ovi_dit.cpp:132-142 gelu_tanh_inplace (nn.GELU(approximate='tanh')).

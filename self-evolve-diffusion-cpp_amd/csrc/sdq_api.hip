@@ -59,6 +59,8 @@ struct Workspace {
   size_t pmax_bytes = 0;
   float* rmax = nullptr;  // row maxima of a GELU output (sdq_ffn's hidden state)
   size_t rmax_bytes = 0;
+  float2* st = nullptr;  // layernorm row statistics (mean, 1/std)
+  size_t st_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -240,11 +242,20 @@ struct RowMax {
   int chunks = 0;
 };
 
+// Norm + modulation folded into the activation quantizer: the GEMM's rows
+// are mod_rows(layernorm(A, eps), shift, scale).
+struct LnMod {
+  const float* shift;
+  const float* scale;
+  float eps;
+};
+
 // Core device-pointer path shared by the entry points. `pre` (nullable):
-// A's row maxima are known; `rmax_out` (nullable, GELU): write Y's.
+// A's row maxima are known; `rmax_out` (nullable, GELU): write Y's; `lnmod`
+// (nullable): quantize mod_rows(layernorm(A)) instead of A.
 int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                    const sdq_epilogue* epi, void* Y, hipStream_t s, const RowMax* pre = nullptr,
-                   RowMax* rmax_out = nullptr) {
+                   RowMax* rmax_out = nullptr, const LnMod* lnmod = nullptr) {
   int rc = check_weight(w, K);
   if (rc) return rc;
   if ((rc = validate_epi(epi))) return rc;
@@ -258,7 +269,9 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
 
   const int cfg = choose_gemm_cfg(M, N, w->KFp, epi ? epi->kind : SDQ_EPI_NONE,
                                   g_dev[w->device].cu_count);
-  if (cfg == kCfgSkinny && qin_fits(M, K, w->KFp) && !std::getenv("SDQ_NO_QIN")) {
+  if (lnmod && (!lnmod->shift || !lnmod->scale || K == 0))
+    return set_error(SDQ_ERR_INVALID, "layernorm+modulation needs shift, scale and K > 0");
+  if (!lnmod && cfg == kCfgSkinny && qin_fits(M, K, w->KFp) && !std::getenv("SDQ_NO_QIN")) {
     // a few rows: the GEMM quantizes them itself (SDQ_NO_QIN: the two-launch
     // path, for comparisons)
     const EpiArgs ea = make_epi(epi, K);
@@ -298,7 +311,13 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
     ea.rmax_stride = rmax_out->stride;
     rmax_out->chunks = 0;
   }
-  const bool premax = pre && pre->chunks > 0;
+  const bool premax = !lnmod && pre && pre->chunks > 0;
+  if (lnmod) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((rc = grow(s, reinterpret_cast<void**>(&ws->st), &ws->st_bytes,
+                   (size_t)M * sizeof(float2))))
+      return rc;
+  }
   ColCopy cc{};
   cc.bias = ea.bias;
   cc.gate = ea.gate;
@@ -309,10 +328,12 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
 
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   hipError_t e =
-      premax ? launch_act_quant_frags_premax(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, pre->p,
-                                             pre->chunks, pre->stride, cu_count, s)
-             : launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
-                                      pmax_bytes ? ws->pmax : nullptr, cu_count, s);
+      lnmod ? launch_act_quant_frags_lnmod(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, lnmod->shift,
+                                           lnmod->scale, lnmod->eps, ws->st, s)
+      : premax ? launch_act_quant_frags_premax(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, pre->p,
+                                               pre->chunks, pre->stride, cu_count, s)
+               : launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
+                                        pmax_bytes ? ws->pmax : nullptr, cu_count, s);
   if (e != hipSuccess) return hip_error(e, "act_quant launch");
   hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
   int vec = (N % 4 == 0) && aligned16(Y);
@@ -326,7 +347,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (t_prof) {
     hipEvent_t p2 = prof_mark(s);
     if (p0 && p1 && p2) {
-      t_recs.push_back({premax ? "act_quant_premax" : "act_quant", p0, p1});
+      t_recs.push_back({lnmod ? "ln_mod_quant" : premax ? "act_quant_premax" : "act_quant", p0, p1});
       t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg) + (splitk > 1 ? "_splitk" : ""),
                         p1, p2});
     } else {
@@ -335,6 +356,37 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
     }
   }
   return SDQ_OK;
+}
+
+// sdq_ffn / sdq_ffn_lnmod: fc1 (GELU, row maxima out) then fc2 (gated, row
+// maxima in); lnmod folds the FFN's norm + modulation into fc1's quantizer.
+int ffn_device(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
+               const float* h, int64_t M, const float* gate, int gate_fma, float* hid, float* x,
+               hipStream_t s, const LnMod* lnmod) {
+  if (!fc1 || !fc2) return set_error(SDQ_ERR_INVALID, "null weight handle");
+  if (fc2->K != fc1->N || fc2->N != fc1->K)
+    return set_error(SDQ_ERR_INVALID,
+                     "ffn: fc1 is [" + std::to_string(fc1->N) + "," + std::to_string(fc1->K) +
+                         "], fc2 is [" + std::to_string(fc2->N) + "," + std::to_string(fc2->K) +
+                         "]; need fc1 [F,D] and fc2 [D,F]");
+  if (fc1->device != fc2->device)
+    return set_error(SDQ_ERR_INVALID, "ffn: fc1 and fc2 are on different devices");
+  if (!gate || !hid || !x) return set_error(SDQ_ERR_INVALID, "ffn: null gate, hid or x");
+  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
+  if (M == 0) return SDQ_OK;
+  int rc = ensure_device(fc1->device);
+  if (rc) return rc;
+  // fc1's GELU epilogue writes hid's row maxima (either persistent tile
+  // config: two wave columns per tile) for fc2's quantizer.
+  RowMax rm;
+  rm.stride = (int)round_up(std::max(gemm_rmax_chunks(kCfg128x128, fc1->N),
+                                     gemm_rmax_chunks(kCfg256x256, fc1->N)),
+                            4);
+  if ((rc = rmax_buffer(fc1->device, s, (size_t)M * rm.stride * sizeof(float), &rm.p))) return rc;
+  sdq_epilogue e1{SDQ_EPI_GELU, 1, b1, nullptr, nullptr};
+  if ((rc = qlinear_device(fc1, h, M, fc1->K, &e1, hid, s, nullptr, &rm, lnmod))) return rc;
+  sdq_epilogue e2{SDQ_EPI_GATED, gate_fma, b2, gate, x};
+  return qlinear_device(fc2, hid, M, fc2->K, &e2, x, s, &rm, nullptr);
 }
 
 }  // namespace sdq
@@ -483,31 +535,26 @@ int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const
 int sdq_ffn(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
             const float* h, int64_t M, const float* gate, int gate_fma, float* hid, float* x,
             void* stream) {
-  if (!fc1 || !fc2) return set_error(SDQ_ERR_INVALID, "null weight handle");
-  if (fc2->K != fc1->N || fc2->N != fc1->K)
-    return set_error(SDQ_ERR_INVALID,
-                     "ffn: fc1 is [" + std::to_string(fc1->N) + "," + std::to_string(fc1->K) +
-                         "], fc2 is [" + std::to_string(fc2->N) + "," + std::to_string(fc2->K) +
-                         "]; need fc1 [F,D] and fc2 [D,F]");
-  if (fc1->device != fc2->device)
-    return set_error(SDQ_ERR_INVALID, "ffn: fc1 and fc2 are on different devices");
-  if (!gate || !hid || !x) return set_error(SDQ_ERR_INVALID, "ffn: null gate, hid or x");
-  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
-  if (M == 0) return SDQ_OK;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = ensure_device(fc1->device);
-  if (rc) return rc;
-  // fc1's GELU epilogue writes hid's row maxima (either persistent tile
-  // config: two wave columns per tile) for fc2's quantizer.
-  RowMax rm;
-  rm.stride = (int)round_up(std::max(gemm_rmax_chunks(kCfg128x128, fc1->N),
-                                     gemm_rmax_chunks(kCfg256x256, fc1->N)),
-                            4);
-  if ((rc = rmax_buffer(fc1->device, s, (size_t)M * rm.stride * sizeof(float), &rm.p))) return rc;
-  sdq_epilogue e1{SDQ_EPI_GELU, 1, b1, nullptr, nullptr};
-  if ((rc = qlinear_device(fc1, h, M, fc1->K, &e1, hid, s, nullptr, &rm))) return rc;
-  sdq_epilogue e2{SDQ_EPI_GATED, gate_fma, b2, gate, x};
-  return qlinear_device(fc2, hid, M, fc2->K, &e2, x, s, &rm, nullptr);
+  return ffn_device(fc1, b1, fc2, b2, h, M, gate, gate_fma, hid, x,
+                    static_cast<hipStream_t>(stream), nullptr);
+}
+
+int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,
+                  float* x, int64_t M, const float* shift, const float* scale, float eps,
+                  const float* gate, int gate_fma, float* hid, void* stream) {
+  if (!shift || !scale) return set_error(SDQ_ERR_INVALID, "ffn: null shift or scale");
+  const LnMod lm{shift, scale, eps};
+  return ffn_device(fc1, b1, fc2, b2, x, M, gate, gate_fma, hid, x,
+                    static_cast<hipStream_t>(stream), &lm);
+}
+
+int sdq_qlinear_lnmod(const sdq_weight* w, const float* x, int64_t M, int64_t K,
+                      const float* shift, const float* scale, float eps,
+                      const sdq_epilogue* epi, void* Y, void* stream) {
+  if (!shift || !scale) return set_error(SDQ_ERR_INVALID, "null shift or scale");
+  const LnMod lm{shift, scale, eps};
+  return qlinear_device(w, x, M, K, epi, Y, static_cast<hipStream_t>(stream), nullptr, nullptr,
+                        &lm);
 }
 
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream) {

@@ -79,6 +79,19 @@ int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count);
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
                                   int8_t* at, float* as, const ColCopy& cc, float* pmax,
                                   int cu_count, hipStream_t s);
+// mod_rows(layernorm(A)) as the quantized rows (the DiT's norm + modulation
+// before q|k|v and the FFN, blocks.cpp:18-43 + ovi_dit.cpp:161-172): per-row
+// (mean, 1/std) into st[M] (bit-exact serial sums), then the quantizer on the
+// transformed values. shift / scale: [K] device vectors.
+struct LnModArgs {
+  const float2* st;
+  const float* shift;
+  const float* scale;
+};
+hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, int64_t Mp,
+                                        int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
+                                        const float* shift, const float* scale, float eps,
+                                        float2* st, hipStream_t s);
 // Same output, with the row maxima already known: max_c rmax[row*rstride + c]
 // over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
 // read once.

@@ -107,6 +107,155 @@ __device__ __forceinline__ float premax_row(const float* __restrict__ pm, int pc
   return mx;
 }
 
+// mod_rows(layernorm(.)) of 16 consecutive values of one row (columns
+// k0 .. k0+15; those >= K are padding and stay 0), the reference build's
+// steps: t = fl(v - mu) * inv, rounded; o = t + 0 (-0 -> +0); then
+// fmaf(o, 1 + scale[k], shift[k]).
+__device__ __forceinline__ void lnmod16(float v[16], int64_t k0, int64_t K, float2 st,
+                                        const LnModArgs& lm, bool vec) {
+  float sh[16], sc[16];
+  if (vec && k0 + 16 <= K) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float4 a = reinterpret_cast<const float4*>(lm.shift + k0)[i];
+      const float4 b = reinterpret_cast<const float4*>(lm.scale + k0)[i];
+      sh[4 * i] = a.x; sh[4 * i + 1] = a.y; sh[4 * i + 2] = a.z; sh[4 * i + 3] = a.w;
+      sc[4 * i] = b.x; sc[4 * i + 1] = b.y; sc[4 * i + 2] = b.z; sc[4 * i + 3] = b.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      sh[e] = k0 + e < K ? lm.shift[k0 + e] : 0.f;
+      sc[e] = k0 + e < K ? lm.scale[k0 + e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const float d = v[e] - st.x;
+    const float t = d * st.y;
+    const float o = t + 0.f;
+    const float a = 1.f + sc[e];
+    const float y = __builtin_fmaf(o, a, sh[e]);
+    v[e] = k0 + e < K ? y : 0.f;
+  }
+}
+
+// Row statistics of blocks.cpp:18-43 (no affine), bit-exact with the
+// reference build: the mean and the variance are serial float sums in k
+// order (d*d rounded, then added), inv = 1/sqrtf(var/K + eps). One wave per
+// 8 rows: the 64 lanes load 8-row x 32-column tiles coalesced (lane l: row
+// l & 7, 16 bytes at column 4*(l >> 3)), kLnDepth tiles in flight in
+// registers; each tile is transposed through LDS and lanes 0-7 add their
+// row's 32 values in order. Two passes (mean, then variance). A row's 2K
+// dependent adds bound the latency for few rows; HBM bandwidth (2 reads of
+// x) for many.
+// tiles in flight per wave: 32 for few rows (latency), 16 for many (more
+// waves per SIMD; bandwidth-bound there)
+constexpr int kLnDepthFew = 32, kLnDepthMany = 16;
+
+// 4 values of row r at columns c .. c+3, 0 past K; every lane issues its
+// load(s) (the address is clamped into the row), so the tile loop has no
+// branches and its loads stay in flight across iterations. VEC: K % 4 == 0
+// and 16-byte aligned rows (one 16-byte load).
+template <bool VEC>
+__device__ __forceinline__ float4 load4(const float* __restrict__ r, int64_t c, int64_t K) {
+  float4 v;
+  if constexpr (VEC) {
+    v = *reinterpret_cast<const float4*>(r + (c + 4 <= K ? c : K - 4));
+  } else {
+    v.x = r[c < K ? c : K - 1];
+    v.y = r[c + 1 < K ? c + 1 : K - 1];
+    v.z = r[c + 2 < K ? c + 2 : K - 1];
+    v.w = r[c + 3 < K ? c + 3 : K - 1];
+  }
+  v.x = c < K ? v.x : 0.f;
+  v.y = c + 1 < K ? v.y : 0.f;
+  v.z = c + 2 < K ? v.z : 0.f;
+  v.w = c + 3 < K ? v.w : 0.f;
+  return v;
+}
+
+// Serial sum of one 32-column tile of this lane's row (lanes 0-7) from the
+// transposed tile in LDS: PASS 0 adds the values, PASS 1 the rounded
+// (v - mu)^2; n = columns of the tile inside the row (32 but for the last).
+template <int PASS>
+__device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int l, float acc,
+                                             float mu, int n) {
+  auto add = [&](float v) {
+    if constexpr (PASS == 0) {
+      acc = acc + v;
+    } else {
+      const float d = v - mu;
+      const float dd = d * d;
+      acc = acc + dd;
+    }
+  };
+  if (n == 32) {
+    // all eight reads first (one LDS latency per tile), then the 32 adds
+    float4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = tb[q * 8 + l];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      add(v[q].x);
+      add(v[q].y);
+      add(v[q].z);
+      add(v[q].w);
+    }
+  } else {
+    for (int c = 0; c < n; c++) {
+      const float4 v = tb[(c >> 2) * 8 + l];
+      const int e = c & 3;
+      add(e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w)));
+    }
+  }
+  return acc;
+}
+
+template <bool VEC, int PASS, int D>
+__device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K, int l,
+                                         float4 (&tb)[2][64], float mu) {
+  const int j = l >> 3;
+  const int64_t nt = (K + 31) / 32;
+  float acc = 0.f;
+  float4 buf[D];
+#pragma unroll
+  for (int u = 0; u < D; u++) buf[u] = load4<VEC>(r, (int64_t)u * 32 + 4 * j, K);
+  for (int64_t t0 = 0; t0 < nt; t0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int64_t t = t0 + u;
+      tb[t & 1][l] = buf[u];
+      buf[u] = load4<VEC>(r, (t + D) * 32 + 4 * j, K);
+      __syncthreads();
+      if (l < 8 && t < nt) {
+        const int n = (int)((K - t * 32) < 32 ? (K - t * 32) : 32);
+        acc = ln_tile_sum<PASS>(tb[t & 1], l, acc, mu, n);
+      }
+    }
+  }
+  return acc;
+}
+
+template <bool VEC, int D>
+__global__ void __launch_bounds__(64)
+ln_stats_kernel(const float* __restrict__ x, int64_t M, int64_t K, float eps,
+                float2* __restrict__ st) {
+  __shared__ float4 tb[2][64];
+  const int l = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (l & 7);
+  const bool ok = row < M;
+  const float* r = x + (ok ? row : 0) * K;
+  float mu = ln_pass<VEC, 0, D>(r, K, l, tb, 0.f);
+  mu = mu / (float)K;
+  const float var = ln_pass<VEC, 1, D>(r, K, l, tb, mu);
+  if (l < 8 && ok) {
+    const float den = var / (float)K + eps;
+    st[row] = float2{mu, 1.f / sqrtf(den)};
+  }
+}
+
 // Row-major output variant (the parity API): one workgroup per 32 rows.
 template <int NW, int CACHE, bool FRAG_OUT>
 __global__ void __launch_bounds__(NW * 64)
@@ -191,12 +340,17 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
 // bytes, so each fragment is written as two contiguous runs of 16R bytes.
 // PRE: the row maxima come from pre[row * pstride + c], c < pc (written by
 // the producing GEMM), so the row is read once, with no max pass.
-template <int R, int NW, int CACHE, bool PRE>
+// XF: the quantized rows are mod_rows(layernorm(A)) (ovi_dit.cpp:161-172,
+// blocks.cpp:18-43): value v of row r, column k becomes
+//   fmaf(fl(fl(v - mu_r) * inv_r) + 0, 1 + scale[k], shift[k])
+// with (mu_r, inv_r) from ln_stats_kernel; padding columns stay 0.
+template <int R, int NW, int CACHE, bool PRE, bool XF>
 __global__ void __launch_bounds__(NW * 64)
 act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
                        int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc,
-                       const float* __restrict__ pre, int pc, int pstride) {
+                       const float* __restrict__ pre, int pc, int pstride, LnModArgs lm) {
   static_assert(R == 8 || R == 16, "unit height");
+  static_assert(!(PRE && XF), "given maxima are for the plain rows");
   constexpr int F = 32 / R;  // fragments per lane group
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -214,6 +368,14 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
   const int kg = half * 16;            // k offset inside the fragment
   const int64_t ng = KFp / F;          // fragment groups (KFp is a multiple of 8)
   const int slot = (int)((row & 31) + half * 32) * 16;
+  float2 st = {0.f, 0.f};
+  if constexpr (XF) st = row_ok ? lm.st[row] : float2{0.f, 0.f};
+  // the lane's 16 values of group g (transformed under XF)
+  auto fetch = [&](int64_t g, float v[16]) {
+    const int64_t k0 = (g * F + sub) * 32 + kg;
+    load16(rowp, k0, K, row_ok, vec != 0, v);
+    if constexpr (XF) lnmod16(v, k0, K, st, lm, vec != 0);
+  };
 
   float cache[CACHE][16];
   float mx = 0.f;
@@ -221,7 +383,7 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
   for (int c = 0; c < CACHE; c++) {
     const int64_t g = w + (int64_t)c * NW;
     if (g < ng) {
-      load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, cache[c]);
+      fetch(g, cache[c]);
       if constexpr (!PRE) mx = amax16(cache[c], mx);
     }
   }
@@ -233,7 +395,7 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
     // M: the extra VGPRs cost occupancy, 5 -> 3 waves per SIMD)
     for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
       float t[16];
-      load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
+      fetch(g, t);
       mx = amax16(t, mx);
     }
     // the lanes l + R*j (j = 0 .. 64/R - 1) hold the same row
@@ -268,7 +430,7 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
   }
   for (int64_t g = w + (int64_t)CACHE * NW; g < ng; g += NW) {
     float t[16];
-    load16(rowp, (g * F + sub) * 32 + kg, K, row_ok, vec != 0, t);
+    fetch(g, t);
     emit(g, t);
   }
 }
@@ -408,9 +570,35 @@ hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t 
     }
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false>),
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false, false>),
                      dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
-                     at, as, cc, nullptr, 0, 0);
+                     at, as, cc, nullptr, 0, 0, LnModArgs{});
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, int64_t Mp,
+                                        int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
+                                        const float* shift, const float* scale, float eps,
+                                        float2* st, hipStream_t s) {
+  if (!shift || !scale || !st || K <= 0) return hipErrorInvalidValue;
+  const int vec = (aligned16(A) && aligned16(shift) && aligned16(scale) && (K % 4) == 0) ? 1 : 0;
+  const bool vx = aligned16(A) && (K % 4) == 0, few = M <= 4096;
+  const dim3 g((unsigned)ceil_div(M, 8)), b(64);
+  if (vx && few)
+    hipLaunchKernelGGL((ln_stats_kernel<true, kLnDepthFew>), g, b, 0, s, A, M, K, eps, st);
+  else if (vx)
+    hipLaunchKernelGGL((ln_stats_kernel<true, kLnDepthMany>), g, b, 0, s, A, M, K, eps, st);
+  else if (few)
+    hipLaunchKernelGGL((ln_stats_kernel<false, kLnDepthFew>), g, b, 0, s, A, M, K, eps, st);
+  else
+    hipLaunchKernelGGL((ln_stats_kernel<false, kLnDepthMany>), g, b, 0, s, A, M, K, eps, st);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t units = Mp / kQuantRows;
+  LnModArgs lm{st, shift, scale};
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false, true>),
+                     dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
+                     at, as, cc, nullptr, 0, 0, lm);
   return hipGetLastError();
 }
 
@@ -435,9 +623,9 @@ hipError_t launch_act_quant_frags_premax(const float* A, int64_t M, int64_t K, i
                          vec, C, items, rmax, rchunks, rstride, at, as, cc);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, true>),
+  hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, true, false>),
                      dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
-                     at, as, cc, rmax, rchunks, rstride);
+                     at, as, cc, rmax, rchunks, rstride, LnModArgs{});
   return hipGetLastError();
 }
 

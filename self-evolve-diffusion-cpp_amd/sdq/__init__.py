@@ -64,6 +64,10 @@ SIGNATURES = {
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "sdq_ffn": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _vp, _vp]),
+    "sdq_qlinear_lnmod": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, ctypes.c_float,
+                                         ctypes.POINTER(Epilogue), _vp, _vp]),
+    "sdq_ffn_lnmod": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _vp,
+                                     ctypes.c_int, _vp, _vp]),
     "sdq_qlinear_host": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp]),
     "sdq_act_quant": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "sdq_device_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
@@ -215,6 +219,26 @@ def ffn(fc1: Weight, b1, fc2: Weight, b2, h, gate, hid, x, gate_fma=True, stream
     M = h.shape[0]
     _check(_lib.sdq_ffn(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(h), M, _ptr(gate),
                         1 if gate_fma else 0, _ptr(hid), _ptr(x), _stream(stream)))
+    return x
+
+
+def qlinear_lnmod(w: Weight, x, out, shift, scale, eps=1e-6, kind="none", bias=None, gate=None,
+                  resid=None, gate_fma=True, stream=None):
+    """out = epilogue(qgemm(mod_rows(layernorm(x), shift, scale), W) + bias)."""
+    M, K = x.shape
+    e = make_epilogue(kind, bias, gate, resid, gate_fma)
+    _check(_lib.sdq_qlinear_lnmod(w.h, _ptr(x), M, K, _ptr(shift), _ptr(scale), eps,
+                                  ctypes.byref(e), _ptr(out), _stream(stream)))
+    return out
+
+
+def ffn_lnmod(fc1: Weight, b1, fc2: Weight, b2, x, shift, scale, gate, hid, eps=1e-6,
+              gate_fma=True, stream=None):
+    """ffn_fwd (ovi_dit.cpp:214-222) with x the norm input and the residual."""
+    M = x.shape[0]
+    _check(_lib.sdq_ffn_lnmod(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(x), M, _ptr(shift),
+                              _ptr(scale), eps, _ptr(gate), 1 if gate_fma else 0, _ptr(hid),
+                              _stream(stream)))
     return x
 
 

@@ -267,3 +267,73 @@ def test_oracle_planted_mistakes_are_caught(oracle):
     trunc = np.clip(np.trunc(A * (np.float32(1) / asc)[:, None]), -127, 127).astype(np.int64)
     assert np.any(trunc != aq)
     assert not np.array_equal(aq @ q.T.astype(np.int64), (aq @ q.T.astype(np.int64))[:, ::-1])
+
+
+# ------------------------------------------------ DiT glue: layernorm, mod_rows
+def _ln_rows(seed, M=24, N=3072):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((M, N)) * rng.uniform(0.01, 100, (M, 1))).astype(np.float32)
+    x[1] = 0.0                      # var = 0: inv = 1/sqrt(eps)
+    x[2] = np.float32(3.25)         # constant row
+    x[3] *= np.float32(1e-30)       # tiny values
+    x[4] *= np.float32(1e15)        # huge values (d*d near the float range)
+    x[5, ::7] = -x[5, ::7]
+    return x
+
+
+def _ln_serial_numpy(x, eps, fma_var=False):
+    """blocks.cpp:18-43 restated in numpy: serial float32 sums over k,
+    vectorized over rows (each step rounds like the C loop)."""
+    M, N = x.shape
+    mu = np.zeros(M, np.float32)
+    for k in range(N):
+        mu = mu + x[:, k]
+    mu = mu / np.float32(N)
+    var = np.zeros(M, np.float32)
+    for k in range(N):
+        d = x[:, k] - mu
+        if fma_var:  # a contracted d*d + var (one rounding), for the planted-mistake check
+            var = (d.astype(np.float64) * d + var).astype(np.float32)
+        else:
+            var = var + d * d
+    inv = np.float32(1) / np.sqrt(var / np.float32(N) + np.float32(eps))
+    t = (x - mu[:, None]) * inv[:, None]
+    return t * np.float32(1) + np.float32(0)
+
+
+def test_layernorm_matches_reference_build(oracle, ref):
+    x = _ln_rows(41)
+    want = ref.layernorm(x, 1e-6)
+    assert_bitexact(oracle.layernorm(x, 1e-6), want, "layernorm vs reference build")
+    assert_bitexact(_ln_serial_numpy(x, 1e-6), want, "numpy serial restatement")
+    assert not np.signbit(want[1]).any()  # (x-mu)*inv*1 + 0 turns -0 into +0
+
+
+def test_layernorm_closed_form_and_planted_mistakes(oracle):
+    x = _ln_rows(42)
+    y = oracle.layernorm(x, 1e-6)
+    assert_bitexact(y, _ln_serial_numpy(x, 1e-6), "numpy serial restatement")
+    xd = x.astype(np.float64)
+    mu = xd.mean(1, keepdims=True)
+    yd = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(1, keepdims=True) + 1e-6)
+    ok = np.isfinite(yd).all(1) & (np.abs(x).max(1) < 1e10)
+    assert np.allclose(y[ok], yd[ok], rtol=2e-4, atol=2e-4)
+    # planted: a contracted variance sum, or float64 sums, differ from the oracle
+    assert np.any(bits(_ln_serial_numpy(x, 1e-6, fma_var=True)) != bits(y))
+    assert np.any(bits(yd.astype(np.float32)[ok]) != bits(y[ok]))
+
+
+def test_mod_rows_matches_reference_build_and_closed_form(oracle, ref):
+    rng = np.random.default_rng(43)
+    x = _ln_rows(44, M=16, N=1024)
+    shift = rng.standard_normal(1024).astype(np.float32)
+    scale = (rng.standard_normal(1024) * 0.3).astype(np.float32)
+    want = ref.mod_rows(x, shift, scale)
+    got = oracle.mod_rows(x, shift, scale)
+    assert_bitexact(got, want, "mod_rows vs reference build")
+    a = (np.float32(1) + scale).astype(np.float64)
+    once = (x.astype(np.float64) * a + shift).astype(np.float32)  # x*a exact in float64
+    fin = np.isfinite(once)
+    assert (bits(got[fin]) == bits(once[fin])).mean() > 0.9999
+    two = (x * (np.float32(1) + scale) + shift).astype(np.float32)  # planted: two roundings
+    assert np.any(bits(two) != bits(got))
