@@ -153,10 +153,19 @@ def bench_block(torch, sdq, args):
     ms = _timed(torch, fn, max(args.warmup // 5, 2), max(args.steps // 10, 3))
     ops = blk.ops(M, Mc, Mt)
     split = _kernel_split(sdq, fn, 2)
+    # the same block with norm1/norm2 + modulation folded into q|k|v's and
+    # fc1's quantizers (x is normalized in place of the given h_sa / h_ffn)
+    mods = {k: torch.randn(dim, device=dev) * 0.3
+            for k in ("shift_sa", "scale_sa", "shift_ffn", "scale_ffn")}
+    fn_ln = lambda: blk.forward(**io, **mods, eps=1e-6)  # noqa: E731
+    ms_ln = _timed(torch, fn_ln, max(args.warmup // 5, 2), max(args.steps // 10, 3))
+    split_ln = _kernel_split(sdq, fn_ln, 2)
     return {"metric": "DiT block int8 linear stack (config 3), TOPS", "value": round(ops / ms / 1e9, 2),
             "unit": "TOPS", "ms_per_block": round(ms, 4), "ops": ops, "dtype": "int8",
             "config": {"workload": "DiT block linears M=27280 dim=3072 ffn=14336 ctx=512 "
-                                   "fusion=157", "kernel_ms_per_block": split}}
+                                   "fusion=157", "kernel_ms_per_block": split,
+                       "ms_per_block_norms_folded": round(ms_ln, 4),
+                       "kernel_ms_per_block_norms_folded": split_ln}}
 
 
 def bench_ffn(torch, sdq, args):

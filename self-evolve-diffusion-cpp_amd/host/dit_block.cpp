@@ -38,7 +38,15 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   need(io.M >= 0 && io.Mc >= 0 && io.Mt >= 0, "negative row count");
   need(io.x && io.gate_sa && io.gate_ffn, "x and gates are required");
   // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-188, 205-212)
-  qkv_.forward_device(io.h_sa, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.qkv, s);
+  const bool ln_sa = io.shift_sa && io.scale_sa, ln_ffn = io.shift_ffn && io.scale_ffn;
+  if (ln_sa) {
+    sdq_epilogue e{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
+    check(sdq_qlinear_lnmod(qkv_.handle(), io.x, io.M, dim_, io.shift_sa, io.scale_sa, io.eps, &e,
+                            io.qkv, s),
+          "DitBlock q|k|v");
+  } else {
+    qkv_.forward_device(io.h_sa, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.qkv, s);
+  }
   o_.forward_device(io.att, io.M, SDQ_EPI_GATED, io.gate_sa, io.x, io.x, s);
   // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
   // the other branch, then x += o(xt)                (ovi_dit.cpp:229-254)
@@ -49,9 +57,14 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
   // ffn: hid = gelu(fc1(h)); x += fc2(hid) * e[5]    (ovi_dit.cpp:214-222); one
   // call, so fc1's epilogue hands hid's row maxima to fc2's quantizer
-  check(sdq_ffn(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.h_ffn,
-                io.M, io.gate_ffn, 1, io.hid, io.x, s),
-        "DitBlock ffn");
+  if (ln_ffn)
+    check(sdq_ffn_lnmod(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.x,
+                        io.M, io.shift_ffn, io.scale_ffn, io.eps, io.gate_ffn, 1, io.hid, s),
+          "DitBlock ffn");
+  else
+    check(sdq_ffn(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.h_ffn,
+                  io.M, io.gate_ffn, 1, io.hid, io.x, s),
+          "DitBlock ffn");
 }
 
 double DitBlock::ops(int64_t M, int64_t Mc, int64_t Mt) const {

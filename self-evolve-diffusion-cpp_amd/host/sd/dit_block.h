@@ -4,18 +4,21 @@
 // checks the block's Linears; the block forward (ovi_dit.cpp:176-259) runs
 // them through mlin:
 //   self_attn  q, k, v on the modulated norm1 output; o on the attention
-//              output, then x += o * e[2]             (block_self_fwd, 168-174)
+//              output, then x += o * e[2]   (self_attn_fwd 176-188, block_self_fwd 205-212)
 //   cross_attn q on the tokens; k, v on the text context; in fusion layers
 //              k_fusion, v_fusion on the normed other-branch tokens; o on the
-//              summed attention outputs, then x += o  (fusion_cross_ffn, 206-241)
+//              summed attention outputs, then x += o  (fusion_cross_ffn, 229-256)
 //   ffn        fc1 (ffn.0) + GELU-tanh, fc2 (ffn.2), then x += fc2 * e[5]
-//                                                     (ffn_fwd, 196-204)
+//                                                     (ffn_fwd, 214-222)
 // Linears that read the same input run as one GEMM, concatenated along out
 // (q|k|v, cross k|v, k_fusion|v_fusion): bit-identical to separate mlin calls
 // (activation quantization is per input row; each output column depends only
 // on its own weight row and scale). Everything between the Linears (norms,
 // modulation, RoPE, attention) is outside this path: those tensors are
-// inputs here, device-resident.
+// inputs here, device-resident; except that the norm + modulation in front
+// of q|k|v and of fc1 can be folded into their activation quantizers
+// (shift_sa/scale_sa, shift_ffn/scale_ffn below: then h_sa / h_ffn are not
+// read and x itself is normalized, bit-exact with the reference build).
 #pragma once
 #include <cstdint>
 #include <string>
@@ -48,6 +51,15 @@ typedef struct sd_dit_block_io {
   float* kvt;            // [Mt,2dim] out (fusion layers)
   float* hid;            // [M,ffn]   out: gelu_tanh(fc1)
   float* x;              // [M,dim]   residual stream, updated in place
+  // Optional (NULL = use h_sa / h_ffn): the modulation rows e[0], e[1]
+  // ([dim] shift, scale) of norm1 and e[3], e[4] of norm2; q|k|v then read
+  // mod_rows(layernorm(x)) at block entry (ovi_dit.cpp:208-209) and fc1
+  // mod_rows(layernorm(x)) after the cross-attention update (216-217).
+  const float* shift_sa;
+  const float* scale_sa;
+  const float* shift_ffn;
+  const float* scale_ffn;
+  float eps;             // layernorm epsilon (the reference's kEps, 1e-6)
 } sd_dit_block_io;
 
 // One Linear's arrays for sd_dit_block_create (all host or all device).

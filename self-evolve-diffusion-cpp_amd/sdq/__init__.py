@@ -291,10 +291,13 @@ class Linear(ctypes.Structure):
                 ("out", ctypes.c_int64), ("in_", ctypes.c_int64)]
 
 
+_BLOCK_PTRS = ("h_sa", "att", "gate_sa", "xq", "ctx", "tn", "xt", "h_ffn", "gate_ffn", "qkv", "cq",
+               "ckv", "kvt", "hid", "x", "shift_sa", "scale_sa", "shift_ffn", "scale_ffn")
+
+
 class BlockIO(ctypes.Structure):
-    _fields_ = [("M", ctypes.c_int64), ("Mc", ctypes.c_int64), ("Mt", ctypes.c_int64)] + [
-        (n, ctypes.c_void_p) for n in ("h_sa", "att", "gate_sa", "xq", "ctx", "tn", "xt",
-                                       "h_ffn", "gate_ffn", "qkv", "cq", "ckv", "kvt", "hid", "x")]
+    _fields_ = ([("M", ctypes.c_int64), ("Mc", ctypes.c_int64), ("Mt", ctypes.c_int64)] +
+                [(n, ctypes.c_void_p) for n in _BLOCK_PTRS] + [("eps", ctypes.c_float)])
 
 
 def load_host_library(path: str = HOST_LIB_PATH):
@@ -366,8 +369,9 @@ class DitBlock:
         """io: M, Mc, Mt and the device tensors named in BlockIO."""
         b = BlockIO()
         b.M, b.Mc, b.Mt = int(io.get("M", 0)), int(io.get("Mc", 0)), int(io.get("Mt", 0))
-        for name, _ in BlockIO._fields_[3:]:
+        for name in _BLOCK_PTRS:
             setattr(b, name, _ptr(io.get(name)))
+        b.eps = float(io.get("eps", 1e-6))
         _hcheck(_host.sd_dit_block_forward(self.h, ctypes.byref(b), _stream(stream)))
 
     def ops(self, M, Mc=0, Mt=0) -> float:

@@ -161,3 +161,43 @@ def test_block_fullsize_sampled(sdq_dev, oracle):
     x = L(h, "fc2", epilogue="gated", gate=inp["gate_ffn"], resid=x)
     assert_bitexact(d["x"][rt].cpu().numpy(), x, "residual stream rows")
     blk.free()
+
+
+def test_block_with_norms_folded(sdq_dev, oracle):
+    """The block with its norm1 / norm2 + modulation folded into q|k|v's and
+    fc1's quantizers (io shift_sa/scale_sa, shift_ffn/scale_ffn): q|k|v read
+    mod_rows(layernorm(x)) at block entry, fc1 the same of x after the
+    cross-attention update; bit-exact against the oracle's layernorm,
+    mod_rows and Linears (GELU hidden state: tolerance, then fc2 on it)."""
+    import torch
+
+    import sdq
+
+    dim, ffn, M, Mc, Mt = 512, 1408, 300, 77, 45
+    lin = _weights(oracle, dim, ffn, 900, True)
+    inp = _inputs(oracle, M, Mc, Mt, dim, 1000)
+    e = [oracle.randn(dim, 1100 + i) * np.float32(0.3) for i in range(4)]
+    blk = sdq.DitBlock(lin, True)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(sdq_dev) for k, v in inp.items()}
+    ed = [torch.from_numpy(a).to(sdq_dev) for a in e]
+    outs = dict(qkv=torch.empty((M, 3 * dim), device=sdq_dev), cq=torch.empty((M, dim), device=sdq_dev),
+                ckv=torch.empty((Mc, 2 * dim), device=sdq_dev),
+                kvt=torch.empty((Mt, 2 * dim), device=sdq_dev),
+                hid=torch.empty((M, ffn), device=sdq_dev))
+    blk.forward(M=M, Mc=Mc, Mt=Mt, **d, **outs, shift_sa=ed[0], scale_sa=ed[1], shift_ffn=ed[2],
+                scale_ffn=ed[3], eps=1e-6)
+    torch.cuda.synchronize()
+    L = lambda A, n, **kw: oracle.linear(A, lin[n][0], lin[n][1], bias=lin[n][2], **kw)  # noqa
+    h_sa = oracle.mod_rows(oracle.layernorm(inp["x"], 1e-6), e[0], e[1])
+    assert_bitexact(outs["qkv"].cpu().numpy(), np.concatenate([L(h_sa, n) for n in "qkv"], 1),
+                    "q|k|v of the normed x")
+    x = L(inp["att"], "o", epilogue="gated", gate=inp["gate_sa"], resid=inp["x"])
+    x = L(inp["xt"], "co", epilogue="resid", resid=x)
+    h_ffn = oracle.mod_rows(oracle.layernorm(x, 1e-6), e[2], e[3])
+    hid = outs["hid"].cpu().numpy()
+    want_hid = L(h_ffn, "fc1", epilogue="gelu")
+    err = np.abs(hid.astype(np.float64) - want_hid.astype(np.float64))
+    assert np.all(err <= 1e-6 * (1.0 + np.abs(want_hid))), float(err.max())
+    x = L(hid, "fc2", epilogue="gated", gate=inp["gate_ffn"], resid=x)
+    assert_bitexact(d["x"].cpu().numpy(), x, "residual stream with folded norms")
+    blk.free()
