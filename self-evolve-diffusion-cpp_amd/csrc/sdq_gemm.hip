@@ -1270,9 +1270,29 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
                                                     2 * aux.cu_count, s);
       return run_tiled<128, 128, 2, 2, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     case kCfg256x256:
-      if (persist)
+      if (persist) {
+        // A last round of 256x256 tiles under half full: the rows of the
+        // full rounds (whole m-tiles) run here, the rest as 128x128 tiles (a
+        // quarter of the work each, two per CU) right after. Not with row
+        // maxima (the two tile widths write different column chunks).
+        const int64_t tn = ceil_div(N, 256), T = ceil_div(M, 256) * tn;
+        const int64_t G = aux.cu_count > 0 ? aux.cu_count : 256;
+        const int64_t full = (T / G) * G, tail = T - full;
+        const int64_t Ma = (full / tn) * 256;
+        if (!epi_r.rmax && tail > 0 && 2 * tail < G && Ma > 0 && Ma < M &&
+            !std::getenv("SDQ_NO_TAIL")) {
+          hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r,
+                                                              Y, aux.cu_count, s);
+          if (e != hipSuccess) return e;
+          EpiArgs et = epi_r;
+          if (et.resid) et.resid += Ma * N;
+          return run_persist<128, 128, 2, 2, 2, 4, 2>(
+              wt, cols, at + (Ma / kFragRows) * KFp * kFragBytes, as + Ma, M - Ma, N, KFp, et,
+              static_cast<char*>(Y) + Ma * N * 4, 2 * aux.cu_count, s);
+        }
         return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y,
                                                     aux.cu_count, s);
+      }
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;
   }
