@@ -281,6 +281,29 @@ def bench_twin(torch, sdq, args):
                                       "weight_GB": round(lw / 1e9, 3),
                                       "weight_stream_GBps": round(lw / ms / 1e6, 1),
                                       "repack_ms_total": round(t_repack * 1e3, 1)}
+    # CFG batching (denoise.cpp:95-98 runs the conditional and unconditional
+    # forwards one after the other): both forwards' rows stacked, 2M tokens
+    # and 2 text contexts per Linear, one weight stream for the pair
+    # (bit-identical per row; the attention between the Linears keeps the
+    # two halves apart). 28 layers, two streams as above.
+    layers = 28
+    iov2 = _block_io(torch, dev, 2 * Mv, 2 * Mc, 2 * Ma, dim, ffn)
+    ioa2 = _block_io(torch, dev, 2 * Ma, 2 * Mc, 2 * Mv, dim, ffn)
+
+    def fn_cfg():
+        cur = torch.cuda.current_stream()
+        sv.wait_stream(cur)
+        sa.wait_stream(cur)
+        for i in range(layers):
+            blocks[2 * i].forward(stream=sv.cuda_stream, **iov2)
+            blocks[2 * i + 1].forward(stream=sa.cuda_stream, **ioa2)
+            sv.wait_stream(sa)
+            sa.wait_stream(sv)
+        cur.wait_stream(sv)
+        cur.wait_stream(sa)
+    ms_cfg = _timed(torch, fn_cfg, 2, max(args.steps // 10, 3))
+    res["cfg_batched_28"] = {"ms_per_cond_uncond_pair": round(ms_cfg, 4),
+                             "two_separate_passes_ms": round(2 * res["layers"]["28"]["ms_per_pass"], 4)}
     res["value"] = res["layers"]["28"]["ms_per_pass"]
     return res
 
