@@ -43,11 +43,13 @@ def parse():
     ap.add_argument("--cpu-sample-rows", type=int, default=4096)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 FETCH/WRITE_SIZE summary used for roofline.traffic")
-    ap.add_argument("--config", default="ns", choices=["ns", "block", "ffn", "cross", "twin"],
+    ap.add_argument("--config", default="ns",
+                    choices=["ns", "block", "ffn", "cross", "twin", "load"],
                     help="ns: the north-star qGEMM (the driver's bench line); block: one DiT "
                          "block's linear stack at 720p/121f; ffn: the 256x256/9f FFN pair; "
                          "cross: text/cross-attention and AdaLN projections; twin: the "
-                         "full twin-backbone linear stack (28 and 30 layers)")
+                         "full twin-backbone linear stack (28 and 30 layers); load: weight "
+                         "upload of 8 blocks from host memory")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run a few steps plus a 1 GiB torch copy (the counter calibration "
                          "kernel) and exit; used under rocprofv3 --pmc")
@@ -308,6 +310,48 @@ def bench_twin(torch, sdq, args):
     return res
 
 
+def bench_load(torch, sdq, args):
+    """Weight upload from host memory (§8(f) rank 4): 8 DiT blocks at the real
+    widths (dim 3072, FFN 14336, fusion: 1.46 GB of int8 + scales, host arrays
+    like load_sdcpp's views), one block at a time (per Linear: host concat,
+    pageable copy, repack) vs one streamed upload (pinned ring, async copies,
+    repack overlap)."""
+    import numpy as np
+
+    dim, ffn, nb = 3072, 14336, 8
+    rng = np.random.default_rng(5)
+    names = ("q", "k", "v", "o", "cq", "ck", "cv", "co", "kf", "vf", "fc1", "fc2")
+    lins = []
+    for b in range(nb):
+        lin = {}
+        for n in names:
+            out, inp = (ffn, dim) if n == "fc1" else ((dim, ffn) if n == "fc2" else (dim, dim))
+            lin[n] = (rng.integers(-127, 128, (out, inp), dtype=np.int8),
+                      rng.uniform(1e-4, 1e-3, out).astype(np.float32),
+                      rng.standard_normal(out).astype(np.float32))
+        lins.append(lin)
+    nbytes = sum(q.nbytes + s.nbytes for lin in lins for q, s, _ in lin.values())
+    sdq.DitBlock(lins[0], True).free()  # warm up the path
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    one = [sdq.DitBlock(lin, True) for lin in lins]
+    torch.cuda.synchronize()
+    t_one = time.perf_counter() - t0
+    for blk in one:
+        blk.free()
+    t0 = time.perf_counter()
+    many = sdq.DitBlock.create_many(lins, True)
+    torch.cuda.synchronize()
+    t_many = time.perf_counter() - t0
+    for blk in many:
+        blk.free()
+    return {"metric": "DiT block weight upload from host memory", "unit": "GB/s",
+            "value": round(nbytes / t_many / 1e9, 2), "dtype": "int8",
+            "config": {"workload": f"{nb} blocks dim={dim} ffn={ffn} fusion, {nbytes / 1e9:.2f} GB",
+                       "streamed_s": round(t_many, 3), "block_by_block_s": round(t_one, 3),
+                       "block_by_block_GBps": round(nbytes / t_one / 1e9, 2)}}
+
+
 def cpu_baseline(args, K, N):
     """The reference's sd::qgemm (oracle/_ref) on a row sample of the same
     workload; best of 3 after one warmup (tests/test_core.cpp:40-49)."""
@@ -365,9 +409,10 @@ def main():
     if args.config != "ns":
         sdq.init(0)
         fn = {"block": bench_block, "ffn": bench_ffn, "cross": bench_cross,
-              "twin": bench_twin}[args.config]
+              "twin": bench_twin, "load": bench_load}[args.config]
         line = fn(torch, sdq, args)
-        line.update({"n_gpus": 1, "data": "synthetic, resident in HBM"})
+        line.update({"n_gpus": 1, "data": "synthetic, host memory" if args.config == "load"
+                     else "synthetic, resident in HBM"})
         print(json.dumps(line), flush=True)
         return
     M, K, N = args.M, args.K, args.N

@@ -100,6 +100,23 @@ int sdq_weight_upload(const int8_t* q, const float* scale, int64_t N, int64_t K,
 /* Same from DEVICE memory (q and scale already resident in HBM). */
 int sdq_weight_upload_device(const int8_t* q_dev, const float* scale_dev, int64_t N, int64_t K,
                              void* stream, sdq_weight** out);
+/* Many weights at once, streamed: each source is 1-4 parts concatenated
+ * along N (e.g. q|k|v), host arrays as load_sdcpp yields them (views into the
+ * mmapped pack; scales may be unaligned). Host copies into a ring of pinned
+ * staging buffers (several threads), asynchronous H2D on a copy stream and the
+ * GPU repack of the previous weight overlap. out[i] receives source i's
+ * handle; on error no handle is returned. Same device contents as one
+ * sdq_weight_upload per (concatenated) weight.
+ * Replaces: the per-tensor page-in + lin() + upload of OviDit::load_impl
+ * (src/model/ovi_dit.cpp:397-415, 505-530) for a whole pack. */
+typedef struct sdq_weight_src {
+  int nparts;              /* 1..4 */
+  const int8_t* q[4];      /* [rows[i], K] int8, row-major */
+  const float* scale[4];   /* [rows[i]] f32, any alignment */
+  int64_t rows[4];
+  int64_t K;
+} sdq_weight_src;
+int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out);
 int sdq_weight_free(sdq_weight* w);
 int sdq_weight_dims(const sdq_weight* w, int64_t* N, int64_t* K);
 /* Unpack the device copy back to row-major int8 [N,K] + f32 [N] in host

@@ -18,6 +18,7 @@
 #include <set>
 #include <vector>
 #include <string>
+#include <thread>
 #include <utility>
 
 #include "sdq_internal.h"
@@ -466,6 +467,114 @@ int sdq_weight_upload(const int8_t* q, const float* scale, int64_t N, int64_t K,
   }
   *out = w;
   return SDQ_OK;
+}
+
+namespace {
+
+// memcpy split over up to `threads` host threads (page-cache or mmap reads
+// run faster in parallel).
+void par_memcpy(char* dst, const char* src, size_t bytes, int threads) {
+  constexpr size_t kMinPerThread = size_t(4) << 20;
+  const int t = (int)std::min<size_t>((size_t)threads, std::max<size_t>(1, bytes / kMinPerThread));
+  if (t <= 1) {
+    std::memcpy(dst, src, bytes);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const size_t chunk = (bytes + t - 1) / t;
+  for (int i = 0; i < t; i++) {
+    const size_t a = (size_t)i * chunk, b = std::min(bytes, a + chunk);
+    if (a < b) pool.emplace_back([=] { std::memcpy(dst + a, src + a, b - a); });
+  }
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out) {
+  if (!out || (n > 0 && !src)) return set_error(SDQ_ERR_INVALID, "null src or out");
+  if (n < 0) return set_error(SDQ_ERR_INVALID, "negative count");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  if (n == 0) return SDQ_OK;
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  // layout of one staged weight: int8 rows, then the scales at soff
+  std::vector<int64_t> Ns(n);
+  size_t slot = 0;
+  for (int i = 0; i < n; i++) {
+    const sdq_weight_src& w = src[i];
+    if (w.nparts < 1 || w.nparts > 4 || w.K < 0)
+      return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": bad parts or K");
+    int64_t N = 0;
+    for (int p = 0; p < w.nparts; p++) {
+      if (w.rows[p] < 0 || (w.rows[p] * w.K > 0 && !w.q[p]) || (w.rows[p] > 0 && !w.scale[p]))
+        return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": null part");
+      N += w.rows[p];
+    }
+    Ns[i] = N;
+    slot = std::max(slot, (size_t)round_up(N * w.K, 256) + (size_t)N * 4 + 16);
+  }
+  constexpr int kSlots = 3;
+  const int nslots = std::min(n, kSlots);
+  const int threads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  hipStream_t s = static_cast<hipStream_t>(stream), cs = nullptr;
+  std::vector<char*> pin(nslots, nullptr), dst(nslots, nullptr);
+  std::vector<hipEvent_t> copied(nslots, nullptr), repacked(nslots, nullptr);
+  hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+  for (int k = 0; k < nslots && e == hipSuccess; k++) {
+    e = hipHostMalloc(reinterpret_cast<void**>(&pin[k]), slot, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&dst[k]), slot);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&copied[k], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&repacked[k], hipEventDisableTiming);
+  }
+  for (int i = 0; i < n && e == hipSuccess && rc == SDQ_OK; i++) {
+    const sdq_weight_src& w = src[i];
+    const int k = i % nslots;
+    const int64_t N = Ns[i], K = w.K;
+    const size_t soff = (size_t)round_up(N * K, 256);
+    if ((rc = alloc_weight(dev, N, K, &out[i]))) break;
+    // the pinned slot is free once its previous H2D copy has finished
+    if (i >= nslots && (e = hipEventSynchronize(copied[k])) != hipSuccess) break;
+    size_t r = 0;
+    for (int p = 0; p < w.nparts; p++) {
+      par_memcpy(pin[k] + r * (size_t)K, reinterpret_cast<const char*>(w.q[p]),
+                 (size_t)(w.rows[p] * K), threads);
+      std::memcpy(pin[k] + soff + r * 4, w.scale[p], (size_t)w.rows[p] * 4);
+      r += (size_t)w.rows[p];
+    }
+    // the device slot is free once the repack that read it has run
+    if (i >= nslots && (e = hipStreamWaitEvent(cs, repacked[k], 0)) != hipSuccess) break;
+    if ((e = hipMemcpyAsync(dst[k], pin[k], soff + (size_t)N * 4, hipMemcpyHostToDevice, cs)) !=
+        hipSuccess)
+      break;
+    if ((e = hipEventRecord(copied[k], cs)) != hipSuccess) break;
+    if ((e = hipStreamWaitEvent(s, copied[k], 0)) != hipSuccess) break;
+    e = launch_repack_weight(reinterpret_cast<int8_t*>(dst[k]), reinterpret_cast<float*>(dst[k] + soff),
+                             N, K, out[i]->Np, out[i]->KFp, out[i]->frags, out[i]->scale, s);
+    if (e == hipSuccess) e = hipEventRecord(repacked[k], s);
+  }
+  if (e == hipSuccess && rc == SDQ_OK) e = hipStreamSynchronize(s);
+  if (cs) (void)hipStreamSynchronize(cs);
+  if (s) (void)hipStreamSynchronize(s);
+  for (int k = 0; k < nslots; k++) {
+    if (pin[k]) (void)hipHostFree(pin[k]);
+    if (dst[k]) (void)hipFree(dst[k]);
+    if (copied[k]) (void)hipEventDestroy(copied[k]);
+    if (repacked[k]) (void)hipEventDestroy(repacked[k]);
+  }
+  if (cs) (void)hipStreamDestroy(cs);
+  if (e != hipSuccess && rc == SDQ_OK) rc = hip_error(e, "batch weight upload");
+  if (rc != SDQ_OK) {
+    const std::string msg = t_err;
+    for (int i = 0; i < n; i++) {
+      if (out[i]) sdq_weight_free(out[i]);
+      out[i] = nullptr;
+    }
+    t_err = msg;
+  }
+  return rc;
 }
 
 int sdq_weight_upload_device(const int8_t* q_dev, const float* scale_dev, int64_t N, int64_t K,

@@ -16,14 +16,55 @@ void need(bool ok, const std::string& msg) {
 
 }  // namespace
 
+void DitBlock::check_shapes(const LinearPart* l, bool fusion) {
+  const int64_t dim = l[Q].in, ffn = l[FC1].out;
+  for (int i : {Q, K, V, O, CQ, CK, CV, CO})
+    need(l[i].in == dim && l[i].out == dim, "attention Linears must be [dim,dim]");
+  if (fusion) need(l[KF].in == dim && l[KF].out == dim && l[VF].in == dim && l[VF].out == dim,
+                   "fusion Linears must be [dim,dim]");
+  need(l[FC1].in == dim && l[FC2].in == ffn && l[FC2].out == dim, "ffn shapes");
+}
+
+std::vector<DitBlock> DitBlock::create_many(
+    const std::vector<std::array<LinearPart, kCount>>& blocks, bool fusion) {
+  std::vector<std::vector<LinearPart>> sets;
+  for (const auto& l : blocks) {
+    check_shapes(l.data(), fusion);
+    sets.push_back({l[Q], l[K], l[V]});
+    sets.push_back({l[O]});
+    sets.push_back({l[CQ]});
+    sets.push_back({l[CK], l[CV]});
+    if (fusion) sets.push_back({l[KF], l[VF]});
+    sets.push_back({l[CO]});
+    sets.push_back({l[FC1]});
+    sets.push_back({l[FC2]});
+  }
+  std::vector<QLinear> q = QLinear::upload_many(sets);
+  std::vector<DitBlock> out;
+  out.reserve(blocks.size());
+  size_t j = 0;
+  for (size_t b = 0; b < blocks.size(); b++) {
+    DitBlock d;
+    d.fusion_ = fusion;
+    d.dim_ = blocks[b][Q].in;
+    d.ffn_ = blocks[b][FC1].out;
+    d.qkv_ = std::move(q[j++]);
+    d.o_ = std::move(q[j++]);
+    d.cq_ = std::move(q[j++]);
+    d.ckv_ = std::move(q[j++]);
+    if (fusion) d.kvf_ = std::move(q[j++]);
+    d.co_ = std::move(q[j++]);
+    d.fc1_ = std::move(q[j++]);
+    d.fc2_ = std::move(q[j++]);
+    out.push_back(std::move(d));
+  }
+  return out;
+}
+
 DitBlock::DitBlock(const LinearPart (&l)[kCount], bool fusion, bool on_device) : fusion_(fusion) {
+  check_shapes(l, fusion);
   dim_ = l[Q].in;
   ffn_ = l[FC1].out;
-  for (int i : {Q, K, V, O, CQ, CK, CV, CO})
-    need(l[i].in == dim_ && l[i].out == dim_, "attention Linears must be [dim,dim]");
-  if (fusion) need(l[KF].in == dim_ && l[KF].out == dim_ && l[VF].in == dim_ && l[VF].out == dim_,
-                   "fusion Linears must be [dim,dim]");
-  need(l[FC1].in == dim_ && l[FC2].in == ffn_ && l[FC2].out == dim_, "ffn shapes");
   qkv_ = QLinear(std::vector<LinearPart>{l[Q], l[K], l[V]}, on_device);
   o_ = QLinear(std::vector<LinearPart>{l[O]}, on_device);
   cq_ = QLinear(std::vector<LinearPart>{l[CQ]}, on_device);
@@ -75,11 +116,12 @@ double DitBlock::ops(int64_t M, int64_t Mc, int64_t Mt) const {
   return o;
 }
 
-DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack,
-                             const std::string& prefix, int layer, int64_t dim, int64_t ffn_dim,
-                             bool fusion) {
+namespace {
+
+// The block's Linears as lin() checks them (ovi_dit.cpp:397-415, 505-530).
+void block_parts(const std::unordered_map<std::string, Tensor>& pack, const std::string& prefix,
+                 int layer, int64_t dim, int64_t ffn_dim, bool fusion, LinearPart* l) {
   const std::string B = prefix + "blocks." + std::to_string(layer) + ".";
-  LinearPart l[DitBlock::kCount];
   l[DitBlock::Q] = linear_part_from_pack(pack, B + "self_attn.q", dim, dim);
   l[DitBlock::K] = linear_part_from_pack(pack, B + "self_attn.k", dim, dim);
   l[DitBlock::V] = linear_part_from_pack(pack, B + "self_attn.v", dim, dim);
@@ -94,7 +136,26 @@ DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack
   }
   l[DitBlock::FC1] = linear_part_from_pack(pack, B + "ffn.0", dim, ffn_dim);
   l[DitBlock::FC2] = linear_part_from_pack(pack, B + "ffn.2", ffn_dim, dim);
+}
+
+}  // namespace
+
+DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                             const std::string& prefix, int layer, int64_t dim, int64_t ffn_dim,
+                             bool fusion) {
+  LinearPart l[DitBlock::kCount];
+  block_parts(pack, prefix, layer, dim, ffn_dim, fusion, l);
   return DitBlock(l, fusion, false);
+}
+
+std::vector<DitBlock> dit_blocks_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                                           const std::string& prefix,
+                                           const std::vector<int>& layers, int64_t dim,
+                                           int64_t ffn_dim, bool fusion) {
+  std::vector<std::array<LinearPart, DitBlock::kCount>> parts(layers.size());
+  for (size_t i = 0; i < layers.size(); i++)
+    block_parts(pack, prefix, layers[i], dim, ffn_dim, fusion, parts[i].data());
+  return DitBlock::create_many(parts, fusion);
 }
 
 }  // namespace gpu
@@ -141,6 +202,26 @@ int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_
       l[i].in = lin[i].in;
     }
     *out = new sd_dit_block{sd::gpu::DitBlock(l, fusion != 0, on_device != 0)};
+  });
+}
+
+int sd_dit_block_create_many(const sd_linear* lin, int nblocks, int fusion, sd_dit_block** out) {
+  if (!lin || !out || nblocks < 0) {
+    t_dit_err = "sd_dit_block_create_many: null argument or negative count";
+    return SDQ_ERR_INVALID;
+  }
+  for (int b = 0; b < nblocks; b++) out[b] = nullptr;
+  return guarded([&] {
+    using sd::gpu::DitBlock;
+    std::vector<std::array<sd::gpu::LinearPart, DitBlock::kCount>> parts(nblocks);
+    for (int b = 0; b < nblocks; b++)
+      for (int i = 0; i < DitBlock::kCount; i++) {
+        if (!fusion && (i == DitBlock::KF || i == DitBlock::VF)) continue;
+        const sd_linear& s = lin[b * DitBlock::kCount + i];
+        parts[b][i] = sd::gpu::LinearPart{s.w, s.scale, s.bias, s.out, s.in};
+      }
+    std::vector<DitBlock> blocks = DitBlock::create_many(parts, fusion != 0);
+    for (int b = 0; b < nblocks; b++) out[b] = new sd_dit_block{std::move(blocks[b])};
   });
 }
 

@@ -50,6 +50,50 @@ void QLinear::upload_bias(const float* b, bool on_device) {
   bias_dev_ = static_cast<float*>(p);
 }
 
+std::vector<QLinear> QLinear::upload_many(const std::vector<std::vector<LinearPart>>& linears) {
+  std::vector<sdq_weight_src> src(linears.size());
+  for (size_t i = 0; i < linears.size(); i++) {
+    const std::vector<LinearPart>& parts = linears[i];
+    if (parts.empty() || parts.size() > 4)
+      throw std::runtime_error("QLinear::upload_many: 1-4 parts per Linear");
+    sdq_weight_src& w = src[i];
+    w = sdq_weight_src{};
+    w.nparts = (int)parts.size();
+    w.K = parts[0].in;
+    bool any_bias = false, all_bias = true;
+    for (size_t p = 0; p < parts.size(); p++) {
+      if (!parts[p].w || !parts[p].scale || parts[p].out <= 0 || parts[p].in != w.K)
+        throw std::runtime_error("QLinear: parts must share in_features and have weights");
+      w.q[p] = parts[p].w;
+      w.scale[p] = parts[p].scale;
+      w.rows[p] = parts[p].out;
+      any_bias = any_bias || parts[p].bias;
+      all_bias = all_bias && parts[p].bias;
+    }
+    if (any_bias && !all_bias) throw std::runtime_error("QLinear: bias on some parts only");
+  }
+  std::vector<sdq_weight*> handles(linears.size(), nullptr);
+  check(sdq_weight_upload_batch(src.data(), (int)src.size(), nullptr, handles.data()),
+        "QLinear::upload_many");
+  std::vector<QLinear> out(linears.size());
+  for (size_t i = 0; i < linears.size(); i++) {  // each takes its handle first (freed on throw)
+    out[i].w_ = handles[i];
+    out[i].K_ = src[i].K;
+    for (const LinearPart& p : linears[i]) out[i].N_ += p.out;
+  }
+  for (size_t i = 0; i < linears.size(); i++) {
+    if (!linears[i][0].bias) continue;
+    std::vector<float> b((size_t)out[i].N_);
+    size_t r = 0;
+    for (const LinearPart& p : linears[i]) {
+      std::memcpy(b.data() + r, p.bias, (size_t)p.out * 4);
+      r += (size_t)p.out;
+    }
+    out[i].upload_bias(b.data(), false);
+  }
+  return out;
+}
+
 QLinear::QLinear(const std::vector<LinearPart>& parts, bool on_device) {
   if (parts.empty()) throw std::runtime_error("QLinear: no parts");
   K_ = parts[0].in;

@@ -20,9 +20,11 @@
 // (shift_sa/scale_sa, shift_ffn/scale_ffn below: then h_sa / h_ffn are not
 // read and x itself is normalized, bit-exact with the reference build).
 #pragma once
+#include <array>
 #include <cstdint>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "sd/qlinear.h"
 #include "sd/tensor.h"
@@ -75,6 +77,9 @@ typedef struct sd_dit_block sd_dit_block;
 // Order of `lin`: self q, k, v, o; cross q, k, v, o; k_fusion, v_fusion;
 // ffn.0, ffn.2 (the fusion pair is ignored when fusion == 0).
 int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_block** out);
+// nblocks blocks from host arrays (lin: 12 per block, same order) in one
+// streamed weight upload; out[i] receives block i.
+int sd_dit_block_create_many(const sd_linear* lin, int nblocks, int fusion, sd_dit_block** out);
 int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void* stream);
 int sd_dit_block_free(sd_dit_block* b);
 // 2*M*N*K summed over the block's Linears for these row counts.
@@ -93,6 +98,10 @@ class DitBlock {
   enum Lin { Q, K, V, O, CQ, CK, CV, CO, KF, VF, FC1, FC2, kCount };
   // lin[Lin] = the block's Linears (host or device arrays).
   DitBlock(const LinearPart (&lin)[kCount], bool fusion, bool on_device);
+  // Many blocks from host arrays in one streamed weight upload
+  // (QLinear::upload_many).
+  static std::vector<DitBlock> create_many(const std::vector<std::array<LinearPart, kCount>>& blocks,
+                                           bool fusion);
   int64_t dim() const { return dim_; }
   int64_t ffn_dim() const { return ffn_; }
   bool fusion() const { return fusion_; }
@@ -101,6 +110,8 @@ class DitBlock {
   double ops(int64_t M, int64_t Mc, int64_t Mt) const;
 
  private:
+  DitBlock() = default;
+  static void check_shapes(const LinearPart* l, bool fusion);
   QLinear qkv_, o_, cq_, ckv_, kvf_, co_, fc1_, fc2_;
   int64_t dim_ = 0, ffn_ = 0;
   bool fusion_ = false;
@@ -114,6 +125,12 @@ class DitBlock {
 DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                              const std::string& prefix, int layer, int64_t dim, int64_t ffn_dim,
                              bool fusion);
+// Blocks `layers` of a backbone, all uploaded in one stream (the pack's
+// int8 views are copied through pinned buffers while the GPU repacks).
+std::vector<DitBlock> dit_blocks_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                                           const std::string& prefix,
+                                           const std::vector<int>& layers, int64_t dim,
+                                           int64_t ffn_dim, bool fusion);
 
 }  // namespace gpu
 }  // namespace sd

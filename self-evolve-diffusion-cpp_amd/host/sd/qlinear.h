@@ -38,6 +38,9 @@ class QLinear {
   // on its own weight row and scale. Parts in host memory, or in device
   // memory with on_device (then the concatenation and repack stay on the GPU).
   explicit QLinear(const std::vector<LinearPart>& parts, bool on_device = false);
+  // Many Linears (each one or more parts, host arrays) in one streamed upload
+  // (sdq_weight_upload_batch: pinned staging, async copies, repack overlap).
+  static std::vector<QLinear> upload_many(const std::vector<std::vector<LinearPart>>& linears);
   QLinear(const QLinear&) = delete;
   QLinear& operator=(const QLinear&) = delete;
   QLinear(QLinear&& o) noexcept;

@@ -59,6 +59,7 @@ SIGNATURES = {
     "sdq_weight_upload": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
     "sdq_weight_upload_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
     "sdq_weight_free": (ctypes.c_int, [_vp]),
+    "sdq_weight_upload_batch": (ctypes.c_int, [_vp, ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
     "sdq_weight_dims": (ctypes.c_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
@@ -198,6 +199,40 @@ def make_epilogue(kind="none", bias=None, gate=None, resid=None, gate_fma=True):
     return e
 
 
+class WeightSrc(ctypes.Structure):
+    _fields_ = [("nparts", ctypes.c_int), ("q", ctypes.c_void_p * 4), ("scale", ctypes.c_void_p * 4),
+                ("rows", ctypes.c_int64 * 4), ("K", ctypes.c_int64)]
+
+
+def upload_batch(sources, stream=None):
+    """sources: list of lists of (q int8 [rows,K], scale f32 [rows] or raw bytes)
+    host parts; returns one Weight per source (sdq_weight_upload_batch)."""
+    load_library()
+    n = len(sources)
+    arr = (WeightSrc * max(n, 1))()
+    keep = []
+    for i, parts in enumerate(sources):
+        arr[i].nparts = len(parts)
+        arr[i].K = parts[0][0].shape[1]
+        for p, (q, sc) in enumerate(parts):
+            q = np.ascontiguousarray(q, np.int8)
+            keep.append(q)
+            arr[i].q[p] = q.ctypes.data
+            if isinstance(sc, (bytes, bytearray, memoryview)):
+                buf = (ctypes.c_char * len(sc)).from_buffer_copy(bytes(sc))
+                keep.append(buf)
+                arr[i].scale[p] = ctypes.addressof(buf)
+            else:
+                sc = np.ascontiguousarray(sc, np.float32)
+                keep.append(sc)
+                arr[i].scale[p] = sc.ctypes.data
+            arr[i].rows[p] = q.shape[0]
+    handles = (ctypes.c_void_p * max(n, 1))()
+    _check(_lib.sdq_weight_upload_batch(arr, n, _stream(stream), handles))
+    return [Weight(ctypes.c_void_p(handles[i]), sum(arr[i].rows[p] for p in range(arr[i].nparts)),
+                   arr[i].K) for i in range(n)]
+
+
 def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, gate_fma=True,
             stream=None):
     """out = epilogue(qgemm(A, W) + bias) on device tensors (stream-ordered)."""
@@ -314,6 +349,9 @@ def load_host_library(path: str = HOST_LIB_PATH):
     h.sd_dit_block_create.restype = ctypes.c_int
     h.sd_dit_block_create.argtypes = [ctypes.POINTER(Linear), ctypes.c_int, ctypes.c_int,
                                       ctypes.POINTER(ctypes.c_void_p)]
+    h.sd_dit_block_create_many.restype = ctypes.c_int
+    h.sd_dit_block_create_many.argtypes = [ctypes.POINTER(Linear), ctypes.c_int, ctypes.c_int,
+                                           ctypes.POINTER(ctypes.c_void_p)]
     h.sd_dit_block_forward.restype = ctypes.c_int
     h.sd_dit_block_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO), ctypes.c_void_p]
     h.sd_dit_block_free.restype = ctypes.c_int
@@ -364,6 +402,35 @@ class DitBlock:
         _hcheck(h.sd_dit_block_create(arr, 1 if fusion else 0, 1 if on_device else 0,
                                       ctypes.byref(self.h)))
         self.fusion = fusion
+
+    @classmethod
+    def create_many(cls, lins, fusion: bool):
+        """Blocks from host arrays in one streamed weight upload
+        (sd_dit_block_create_many); lins: list of the dicts __init__ takes."""
+        h = load_host_library()
+        n = len(lins)
+        arr = (Linear * (len(BLOCK_LINEARS) * max(n, 1)))()
+        keep = []
+        for b, lin in enumerate(lins):
+            for i, name in enumerate(BLOCK_LINEARS):
+                if name not in lin:
+                    if name in ("kf", "vf") and not fusion:
+                        continue
+                    raise ValueError(f"DitBlock: missing Linear {name}")
+                q, s, bias = (None if a is None else np.ascontiguousarray(a) for a in lin[name])
+                keep += [q, s, bias]
+                j = b * len(BLOCK_LINEARS) + i
+                arr[j].w, arr[j].scale, arr[j].bias = _ptr(q), _ptr(s), _ptr(bias)
+                arr[j].out, arr[j].in_ = q.shape
+        handles = (ctypes.c_void_p * max(n, 1))()
+        _hcheck(h.sd_dit_block_create_many(arr, n, 1 if fusion else 0, handles))
+        out = []
+        for b in range(n):
+            blk = cls.__new__(cls)
+            blk.h = ctypes.c_void_p(handles[b])
+            blk.fusion = fusion
+            out.append(blk)
+        return out
 
     def forward(self, stream=None, **io):
         """io: M, Mc, Mt and the device tensors named in BlockIO."""

@@ -201,3 +201,26 @@ def test_block_with_norms_folded(sdq_dev, oracle):
     x = L(hid, "fc2", epilogue="gated", gate=inp["gate_ffn"], resid=x)
     assert_bitexact(d["x"].cpu().numpy(), x, "residual stream with folded norms")
     blk.free()
+
+
+def test_block_create_many_matches_single(sdq_dev, oracle):
+    """Blocks built in one streamed upload (sd_dit_block_create_many) compute
+    what blocks built one by one compute, bit for bit."""
+    dim, ffn, M, Mc, Mt = 384, 1024, 130, 33, 20
+    lins = [_weights(oracle, dim, ffn, 1200 + 50 * b, True) for b in range(3)]
+    inp = _inputs(oracle, M, Mc, Mt, dim, 1400)
+    import sdq
+
+    many = sdq.DitBlock.create_many(lins, True)
+    for b in range(3):
+        one = sdq.DitBlock(lins[b], True)
+        a = _run_block(many[b], sdq_dev, inp, M, Mc, Mt, dim, ffn, True)
+        c = _run_block(one, sdq_dev, inp, M, Mc, Mt, dim, ffn, True)
+        for k in a:
+            assert_bitexact(a[k][:Mt] if k == "kvt" else a[k], c[k][:Mt] if k == "kvt" else c[k],
+                            f"block {b} {k}")
+        one.free()
+    _check_small(oracle, _run_block(many[0], sdq_dev, inp, M, Mc, Mt, dim, ffn, True), lins[0],
+                 inp, True, Mt)
+    for blk in many:
+        blk.free()

@@ -431,3 +431,35 @@ def test_tiny_m_special_rows_and_unaligned(sdq_dev, oracle):
     torch.cuda.synchronize()
     assert_bitexact(Ybuf[1:].view(M, N).cpu().numpy(), oracle.linear(A, q, s, bias=bias),
                     "unaligned tiny M")
+
+
+# ------------------------------------------------------ streamed batch upload
+def test_weight_upload_batch_equals_single_uploads(sdq_dev):
+    """sdq_weight_upload_batch (pinned ring, async copies, repack overlap) gives
+    the same device weights as sdq_weight_upload of the concatenated parts:
+    multi-part sources (q|k|v style), odd shapes, unaligned scale bytes, and
+    more sources than staging slots."""
+    import sdq
+
+    rng = np.random.default_rng(77)
+    shapes = [[(64, 96)], [(13, 31)], [(100, 257), (28, 257), (1, 257)], [(300, 1024)],
+              [(256, 3072), (256, 3072)], [(5, 8)], [(1000, 64)]]
+    sources, whole = [], []
+    for parts in shapes:
+        src, qs, ss = [], [], []
+        for (n, k) in parts:
+            q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+            s = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
+            src.append((q, memoryview(b"\x00" + s.tobytes())[1:]))  # unaligned scale bytes
+            qs.append(q)
+            ss.append(s)
+        sources.append(src)
+        whole.append((np.concatenate(qs), np.concatenate(ss)))
+    ws = sdq.upload_batch(sources)
+    for w, (q, s) in zip(ws, whole):
+        q2, s2 = w.export()
+        assert_bitexact(q2, q, "batch q")
+        assert_bitexact(s2, s, "batch scale")
+        single = sdq.Weight.from_host(q, s)
+        q3, s3 = single.export()
+        assert_bitexact(q3, q2, "single vs batch")
