@@ -166,6 +166,18 @@ int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2,
                   float* x, int64_t M, const float* shift, const float* scale, float eps,
                   const float* gate, int gate_fma, float* hid, void* stream);
 
+/* The q / k glue between the q|k|v GEMM and the attention
+ * (src/model/ovi_dit.cpp:182-185): in place on L rows of x (row stride ld
+ * floats, C columns, e.g. the q or k columns of a q|k|v row),
+ *   x = rmsnorm(x, w, eps)        src/core/tensor.cpp:112-123
+ *   x = apply_rope(x, heads)      src/model/blocks.cpp:86-100
+ * where cs [L][nr][2] holds (cosf, sinf) of each token's nr rotated pair
+ * angles (the reference's RopeFreqs.ang through the same libm calls, done by
+ * the caller); nr = 0 / cs = NULL skips the rotation (cross-attention q, k).
+ * Bit-exact with the reference build. Stream-ordered. */
+int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
+                     int heads, const float* cs, int nr, void* stream);
+
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
 

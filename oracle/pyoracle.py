@@ -46,6 +46,12 @@ def _load():
     lib.orc_gelu_tanh.argtypes = [_f32p, _i64]
     lib.orc_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
     lib.orc_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
+    lib.orc_rmsnorm.argtypes = [_f32p, _i64, _i64, _i64, _f32p, ctypes.c_float]
+    lib.orc_rope_cs.argtypes = [_f32p, _i64, _f32p]
+    lib.orc_rope.argtypes = [_f32p, _i64, _i64, _i64, ctypes.c_int, _f32p, ctypes.c_int]
+    lib.orc_rope_freqs_3d.argtypes = [ctypes.c_int] * 4 + [ctypes.c_float, _f32p]
+    lib.orc_rope_freqs_1d.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                      _f32p]
     lib.orc_quantize_rowwise.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
     lib.orc_quant_rows.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
     lib.orc_randu.argtypes = [_f32p, _i64, ctypes.c_uint64]
@@ -205,6 +211,45 @@ def mod_rows(x, shift, scale):
     return y
 
 
+def rmsnorm(x, w, eps=1e-6):
+    """tensor.cpp:112-123 over the last dim (returns a new array)."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    M, N = y.shape
+    lib().orc_rmsnorm(y, M, N, N, np.ascontiguousarray(w, np.float32), eps)
+    return y
+
+
+def rope_cs(ang):
+    """(cosf, sinf) of a [L, nr] angle table -> [L, nr, 2]."""
+    ang = np.ascontiguousarray(ang, np.float32)
+    cs = np.empty(ang.shape + (2,), np.float32)
+    lib().orc_rope_cs(ang, ang.size, cs)
+    return cs
+
+
+def rope(x, cs, heads):
+    """blocks.cpp:86-100 with the (cos, sin) table cs [L, nr, 2]."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    L, C = y.shape
+    lib().orc_rope(y, L, C, C, heads, np.ascontiguousarray(cs, np.float32), cs.shape[1])
+    return y
+
+
+def rope_freqs_3d(T, H, W, head_dim, theta=10000.0):
+    d = head_dim
+    nr = (d - 4 * (d // 6)) // 2 + (2 * (d // 6)) // 2 * 2
+    ang = np.empty((T * H * W, nr), np.float32)
+    assert lib().orc_rope_freqs_3d(T, H, W, d, theta, ang) == nr
+    return ang
+
+
+def rope_freqs_1d(L, head_dim, theta=10000.0, scaling=1.0):
+    nr = (head_dim - 4 * (head_dim // 6)) // 2
+    ang = np.empty((L, nr), np.float32)
+    assert lib().orc_rope_freqs_1d(L, head_dim, theta, scaling, ang) == nr
+    return ang
+
+
 def quantize_rowwise(W):
     W = np.ascontiguousarray(W, np.float32)
     N, K = W.shape
@@ -283,6 +328,15 @@ class Ref:
         L.sdref_layernorm.restype = ctypes.c_int
         L.sdref_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
         L.sdref_mod_rows.restype = ctypes.c_int
+        L.sdref_rmsnorm.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_float]
+        L.sdref_rmsnorm.restype = ctypes.c_int
+        L.sdref_apply_rope.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_int, ctypes.c_int]
+        L.sdref_apply_rope.restype = ctypes.c_int
+        L.sdref_rope_freqs_3d.argtypes = [ctypes.c_int] * 4 + [ctypes.c_float, _f32p]
+        L.sdref_rope_freqs_3d.restype = ctypes.c_int
+        L.sdref_rope_freqs_1d.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                          ctypes.c_float, _f32p]
+        L.sdref_rope_freqs_1d.restype = ctypes.c_int
         self.L = L
         self.set_nthreads(nthreads or nthreads_default())
 
@@ -329,6 +383,31 @@ class Ref:
                                  np.ascontiguousarray(scale, np.float32), L, C, y) != 0:
             raise RuntimeError("reference mod_rows threw")
         return y
+
+    def rmsnorm(self, x, w, eps=1e-6):
+        y = np.array(x, np.float32, copy=True, order="C")
+        M, N = y.shape
+        if self.L.sdref_rmsnorm(y, M, N, np.ascontiguousarray(w, np.float32), eps) != 0:
+            raise RuntimeError("reference rmsnorm threw")
+        return y
+
+    def apply_rope(self, x, ang, heads):
+        y = np.array(x, np.float32, copy=True, order="C")
+        L, C = y.shape
+        ang = np.ascontiguousarray(ang, np.float32)
+        if self.L.sdref_apply_rope(y, L, C, ang, ang.shape[1], heads) != 0:
+            raise RuntimeError("reference apply_rope threw")
+        return y
+
+    def rope_freqs_3d(self, T, H, W, head_dim, theta=10000.0):
+        ang = np.empty((T * H * W, head_dim), np.float32)
+        nr = self.L.sdref_rope_freqs_3d(T, H, W, head_dim, theta, ang)
+        return np.ascontiguousarray(ang.ravel()[:T * H * W * nr].reshape(T * H * W, nr))
+
+    def rope_freqs_1d(self, L, head_dim, theta=10000.0, scaling=1.0):
+        ang = np.empty((L, head_dim), np.float32)
+        nr = self.L.sdref_rope_freqs_1d(L, head_dim, theta, scaling, ang)
+        return np.ascontiguousarray(ang.ravel()[:L * nr].reshape(L, nr))
 
     def randu(self, n, seed):
         x = np.empty((n,), np.float32)

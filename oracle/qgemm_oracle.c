@@ -31,6 +31,13 @@
  *                          float64 closed form within tolerance.
  *   orc_mod_rows         - compiled reference mod_rows (oracle/_ref) bit-exact;
  *                          float64 x*(1+h)+s rounded once.
+ *   orc_rmsnorm          - compiled reference sd::rmsnorm (oracle/_ref) bit-exact;
+ *                          float64 closed form within tolerance.
+ *   orc_rope, orc_rope_cs - compiled reference blk::apply_rope bit-exact; rotation
+ *                          preserves each pair's norm (float64 check); angle 0 is
+ *                          the identity.
+ *   orc_rope_freqs_3d/1d - compiled reference rope_freqs_3d / rope_freqs_1d
+ *                          bit-exact; float64 closed form within tolerance.
  *   orc_quantize_rowwise - compiled reference sd::quantize_rowwise bit-exact,
  *                          reference golden replica (lround) bit-exact.
  *   orc_quant_rows       - closed form of the packer's numpy expression
@@ -255,6 +262,88 @@ void orc_mod_rows(const float* x, const float* shift, const float* scale, int64_
       const float a = 1.f + scale[c];
       y[l * C + c] = fmaf(x[l * C + c], a, shift[c]);
     }
+}
+
+/* src/core/tensor.cpp:112-123 rmsnorm, in place over the last dim, as the
+ * reference build compiles it (pinned against oracle/_ref): ss is a serial
+ * float sum of the rounded r*r (not contracted); inv = 1/sqrtf(ss/N + eps);
+ * r = fl(fl(r*inv)*w). Rows of stride ld (>= N). */
+void orc_rmsnorm(float* x, int64_t M, int64_t N, int64_t ld, const float* w, float eps) {
+  for (int64_t i = 0; i < M; i++) {
+    float* r = x + i * ld;
+    float ss = 0.f;
+    for (int64_t k = 0; k < N; k++) {
+      const float rr = r[k] * r[k];
+      ss = ss + rr;
+    }
+    const float inv = 1.f / sqrtf(ss / (float)N + eps);
+    for (int64_t k = 0; k < N; k++) {
+      const float t = r[k] * inv;
+      r[k] = t * w[k];
+    }
+  }
+}
+
+/* (cos, sin) of n rotation angles, as apply_rope evaluates them
+ * (src/model/blocks.cpp:93: std::cos / std::sin of a float = cosf / sinf). */
+void orc_rope_cs(const float* ang, int64_t n, float* cs) {
+  for (int64_t i = 0; i < n; i++) {
+    cs[2 * i] = cosf(ang[i]);
+    cs[2 * i + 1] = sinf(ang[i]);
+  }
+}
+
+/* src/model/blocks.cpp:86-100 apply_rope with the (cos, sin) table of
+ * orc_rope_cs: pair j < nr of each head turns by its angle; the reference
+ * build contracts the rotation to q0 = fmaf(r0, c, -fl(r1*s)),
+ * q1 = fmaf(r0, s, fl(r1*c)) (pinned against oracle/_ref). Rows of stride
+ * ld, C = heads * head_dim columns. */
+void orc_rope(float* x, int64_t L, int64_t C, int64_t ld, int heads, const float* cs, int nr) {
+  const int64_t hd = C / heads;
+  for (int64_t l = 0; l < L; l++)
+    for (int h = 0; h < heads; h++)
+      for (int j = 0; j < nr; j++) {
+        const float c = cs[2 * (l * nr + j)], s = cs[2 * (l * nr + j) + 1];
+        float* q = x + l * ld + h * hd + 2 * j;
+        const float r0 = q[0], r1 = q[1];
+        const float r1s = r1 * s, r1c = r1 * c;
+        q[0] = fmaf(r0, c, -r1s);
+        q[1] = fmaf(r0, s, r1c);
+      }
+}
+
+/* src/model/blocks.cpp:46-67 rope_freqs_3d: angles [T*H*W][n_rot] of the
+ * t, h, w axes (t_real = d - 4*(d/6), s_real = 2*(d/6); freq_j =
+ * powf(theta, -2j/real)); returns n_rot. */
+int orc_rope_freqs_3d(int T, int H, int W, int d, float theta, float* ang) {
+  const int t_real = d - 4 * (d / 6), s_real = 2 * (d / 6);
+  const int ct = t_real / 2, cs = s_real / 2, nr = ct + 2 * cs;
+  float ft[4096], fs[4096];
+  if (ct > 4096 || cs > 4096) return -1;
+  for (int j = 0; j < ct; j++) ft[j] = powf(theta, (-2.f * (float)j) / (float)t_real);
+  for (int j = 0; j < cs; j++) fs[j] = powf(theta, (-2.f * (float)j) / (float)s_real);
+  for (int t = 0; t < T; t++)
+    for (int h = 0; h < H; h++)
+      for (int w = 0; w < W; w++) {
+        float* r = ang + (((int64_t)t * H + h) * W + w) * nr;
+        int j = 0;
+        for (; j < ct; j++) r[j] = (float)t * ft[j];
+        for (; j < ct + cs; j++) r[j] = (float)h * fs[j - ct];
+        for (; j < nr; j++) r[j] = (float)w * fs[j - ct - cs];
+      }
+  return nr;
+}
+
+/* src/model/blocks.cpp:69-84 rope_freqs_1d (audio): the t-axis part only,
+ * angle = fl(fl(l * scaling) * powf(theta, -2j/t_real)); returns n_rot. */
+int orc_rope_freqs_1d(int L, int d, float theta, float scaling, float* ang) {
+  const int t_real = d - 4 * (d / 6), nr = t_real / 2;
+  for (int l = 0; l < L; l++)
+    for (int j = 0; j < nr; j++) {
+      const float ls = (float)l * scaling;
+      ang[(int64_t)l * nr + j] = ls * powf(theta, (-2.f * (float)j) / (float)t_real);
+    }
+  return nr;
 }
 
 /* src/model/ovi_dit.cpp:132-142 gelu_tanh_inplace (nn.GELU(approximate='tanh')).

@@ -62,6 +62,8 @@ struct Workspace {
   size_t rmax_bytes = 0;
   float2* st = nullptr;  // layernorm row statistics (mean, 1/std)
   size_t st_bytes = 0;
+  float* rinv = nullptr;  // rmsnorm 1/rms per row
+  size_t rinv_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -148,14 +150,21 @@ int workspace(int dev, hipStream_t s, size_t at_bytes, size_t as_bytes, size_t c
   return SDQ_OK;
 }
 
-// The (device, stream) workspace's row-maxima buffer, at least `bytes`.
-int rmax_buffer(int dev, hipStream_t s, size_t bytes, float** out) {
+// A float buffer of the (device, stream) workspace (member buf / have),
+// grown to at least `bytes`.
+int ws_floats(int dev, hipStream_t s, float* Workspace::*buf, size_t Workspace::*have,
+              size_t bytes, float** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace& w = g_ws[{dev, s}];
-  int rc = grow(s, reinterpret_cast<void**>(&w.rmax), &w.rmax_bytes, bytes);
+  int rc = grow(s, reinterpret_cast<void**>(&(w.*buf)), &(w.*have), bytes);
   if (rc) return rc;
-  *out = w.rmax;
+  *out = w.*buf;
   return SDQ_OK;
+}
+
+// The (device, stream) workspace's row-maxima buffer, at least `bytes`.
+int rmax_buffer(int dev, hipStream_t s, size_t bytes, float** out) {
+  return ws_floats(dev, s, &Workspace::rmax, &Workspace::rmax_bytes, bytes, out);
 }
 
 int check_weight(const sdq_weight* w, int64_t K) {
@@ -664,6 +673,38 @@ int sdq_qlinear_lnmod(const sdq_weight* w, const float* x, int64_t M, int64_t K,
   const LnMod lm{shift, scale, eps};
   return qlinear_device(w, x, M, K, epi, Y, static_cast<hipStream_t>(stream), nullptr, nullptr,
                         &lm);
+}
+
+int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
+                     int heads, const float* cs, int nr, void* stream) {
+  if (L < 0) return set_error(SDQ_ERR_INVALID, "negative L");
+  if (L == 0) return SDQ_OK;
+  if (!x || !w) return set_error(SDQ_ERR_INVALID, "null x or weight");
+  if (C <= 0 || ld < C || heads <= 0 || C % heads != 0 || (C / heads) % 2 != 0)
+    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need C > 0, ld >= C, C = heads * even head_dim");
+  if (nr < 0 || nr > C / heads / 2 || (nr > 0 && !cs))
+    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need 0 <= nr <= head_dim/2 and a table");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  float* inv = nullptr;
+  if ((rc = ws_floats(dev, s, &Workspace::rinv, &Workspace::rinv_bytes, (size_t)L * 4, &inv)))
+    return rc;
+  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  hipError_t e = launch_rmsnorm_rope(x, L, C, ld, w, eps, heads, nr > 0 ? cs : nullptr, nr, inv, s);
+  if (e != hipSuccess) return hip_error(e, "rmsnorm_rope launch");
+  if (t_prof) {
+    hipEvent_t p1 = prof_mark(s);
+    if (p0 && p1) {
+      t_recs.push_back({"rmsnorm_rope", p0, p1});
+    } else {
+      for (hipEvent_t ev : {p0, p1})
+        if (ev) (void)hipEventDestroy(ev);
+    }
+  }
+  return SDQ_OK;
 }
 
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream) {

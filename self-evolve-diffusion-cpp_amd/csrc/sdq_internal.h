@@ -92,6 +92,12 @@ hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, in
                                         int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
                                         const float* shift, const float* scale, float eps,
                                         float2* st, hipStream_t s);
+// In place on L rows of stride ld (C columns): rmsnorm with weight w, then
+// RoPE of each head's first nr pairs with the (cos, sin) table cs [L][nr]
+// (cs == nullptr: no RoPE). inv: [L] scratch.
+hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
+                               float eps, int heads, const float* cs, int nr, float* inv,
+                               hipStream_t s);
 // Same output, with the row maxima already known: max_c rmax[row*rstride + c]
 // over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
 // read once.

@@ -1,0 +1,114 @@
+// Serial per-row float sums in column order, the way the reference's CPU
+// loops accumulate (bit-exact): the layernorm mean and variance
+// (blocks.cpp:18-43) and the rmsnorm sum of squares (tensor.cpp:112-123).
+// Device-side helpers shared by the quantizer and the block-glue kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sdq {
+namespace rowsum {
+
+// One wave per 8 rows: the 64 lanes load 8-row x 32-column tiles coalesced
+// (lane l: row l & 7, 16 bytes at column 4*(l >> 3)), D tiles in flight in
+// registers; each tile is transposed through LDS and lanes 0-7 add their
+// row's 32 values in order. A row's K dependent adds bound the latency for
+// few rows (~700 cycles per 32-column tile); HBM bandwidth for many.
+// tiles in flight per wave: 32 for few rows (latency), 16 for many (more
+// waves per SIMD; bandwidth-bound there)
+constexpr int kLnDepthFew = 32, kLnDepthMany = 16;
+
+// 4 values of row r at columns c .. c+3, 0 past K; every lane issues its
+// load(s) (the address is clamped into the row), so the tile loop has no
+// branches and its loads stay in flight across iterations. VEC: K % 4 == 0
+// and 16-byte aligned rows (one 16-byte load).
+template <bool VEC>
+__device__ __forceinline__ float4 load4(const float* __restrict__ r, int64_t c, int64_t K) {
+  float4 v;
+  if constexpr (VEC) {
+    v = *reinterpret_cast<const float4*>(r + (c + 4 <= K ? c : K - 4));
+  } else {
+    v.x = r[c < K ? c : K - 1];
+    v.y = r[c + 1 < K ? c + 1 : K - 1];
+    v.z = r[c + 2 < K ? c + 2 : K - 1];
+    v.w = r[c + 3 < K ? c + 3 : K - 1];
+  }
+  v.x = c < K ? v.x : 0.f;
+  v.y = c + 1 < K ? v.y : 0.f;
+  v.z = c + 2 < K ? v.z : 0.f;
+  v.w = c + 3 < K ? v.w : 0.f;
+  return v;
+}
+
+// Serial sum of one 32-column tile of this lane's row (lanes 0-7) from the
+// transposed tile in LDS: PASS 0 adds the values, PASS 1 the rounded
+// (v - mu)^2, PASS 2 the rounded v^2; n = columns of the tile inside the row
+// (32 but for the last).
+template <int PASS>
+__device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int l, float acc,
+                                             float mu, int n) {
+  auto add = [&](float v) {
+    if constexpr (PASS == 0) {
+      acc = acc + v;
+    } else if constexpr (PASS == 1) {
+      const float d = v - mu;
+      const float dd = d * d;
+      acc = acc + dd;
+    } else {
+      const float vv = v * v;
+      acc = acc + vv;
+    }
+  };
+  if (n == 32) {
+    // all eight reads first (one LDS latency per tile), then the 32 adds
+    float4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = tb[q * 8 + l];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      add(v[q].x);
+      add(v[q].y);
+      add(v[q].z);
+      add(v[q].w);
+    }
+  } else {
+    for (int c = 0; c < n; c++) {
+      const float4 v = tb[(c >> 2) * 8 + l];
+      const int e = c & 3;
+      add(e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w)));
+    }
+  }
+  return acc;
+}
+
+template <bool VEC, int PASS, int D>
+__device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K, int l,
+                                         float4 (&tb)[2][64], float mu) {
+  const int j = l >> 3;
+  const int64_t nt = (K + 31) / 32;
+  float acc = 0.f;
+  float4 buf[D];
+#pragma unroll
+  for (int u = 0; u < D; u++) buf[u] = load4<VEC>(r, (int64_t)u * 32 + 4 * j, K);
+  for (int64_t t0 = 0; t0 < nt; t0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      const int64_t t = t0 + u;
+      tb[t & 1][l] = buf[u];
+      buf[u] = load4<VEC>(r, (t + D) * 32 + 4 * j, K);
+      __syncthreads();
+      if (l < 8 && t < nt) {
+        const int n = (int)((K - t * 32) < 32 ? (K - t * 32) : 32);
+        acc = ln_tile_sum<PASS>(tb[t & 1], l, acc, mu, n);
+      }
+    }
+  }
+  return acc;
+}
+
+
+}  // namespace rowsum
+}  // namespace sdq

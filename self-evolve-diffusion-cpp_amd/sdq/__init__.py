@@ -64,6 +64,8 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_rmsnorm_rope": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int,
+                                        _vp, ctypes.c_int, _vp]),
     "sdq_ffn": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _vp, _vp]),
     "sdq_qlinear_lnmod": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, ctypes.c_float,
                                          ctypes.POINTER(Epilogue), _vp, _vp]),
@@ -274,6 +276,18 @@ def ffn_lnmod(fc1: Weight, b1, fc2: Weight, b2, x, shift, scale, gate, hid, eps=
     _check(_lib.sdq_ffn_lnmod(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(x), M, _ptr(shift),
                               _ptr(scale), eps, _ptr(gate), 1 if gate_fma else 0, _ptr(hid),
                               _stream(stream)))
+    return x
+
+
+def rmsnorm_rope(x, C, w, heads, cs=None, eps=1e-6, col0=0, stream=None):
+    """In place: columns [col0, col0+C) of every row of the device tensor x
+    (rows of x.shape[1] floats) get rmsnorm(w, eps) then RoPE with the
+    (cos, sin) table cs [L, nr, 2] (None: no rotation)."""
+    L, ld = x.shape
+    nr = 0 if cs is None else cs.shape[1]
+    p = ctypes.c_void_p(x.data_ptr() + 4 * col0)
+    _check(_lib.sdq_rmsnorm_rope(p, L, C, ld, _ptr(w), eps, heads, _ptr(cs), nr,
+                                 _stream(stream)))
     return x
 
 

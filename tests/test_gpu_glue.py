@@ -1,0 +1,61 @@
+"""Block glue on the GPU against the oracle (pinned to the reference build):
+sdq_rmsnorm_rope = rmsnorm (tensor.cpp:112-123) then apply_rope
+(blocks.cpp:86-100) on the q / k columns of a q|k|v row, bit-exact, with the
+(cosf, sinf) table of the reference's rope angles."""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("L,rope", [(60, "3d"), (157, "1d"), (300, "none"), (27280, "3d")])
+def test_rmsnorm_rope_bitexact(sdq_dev, oracle, L, rope):
+    import torch
+
+    import sdq
+
+    heads, hd = 24, 128
+    C = heads * hd
+    print(f"[rmsnorm_rope] L={L} rope={rope}", flush=True)
+    rng = np.random.default_rng(L)
+    qkv = (oracle.randn(L * 3 * C, 50 + L).reshape(L, 3 * C)
+           * rng.uniform(0.1, 30, (L, 1)).astype(np.float32)).astype(np.float32)
+    qkv[min(3, L - 1), :C] = 0.0  # zero q row: ss = 0, inv = 1/sqrt(eps)
+    wq = oracle.randn(C, 60)
+    wk = oracle.randn(C, 61)
+    if rope == "3d":
+        T = max(1, L // 20)
+        ang = oracle.rope_freqs_3d(T, 4, 5, hd, 10000.0)
+        ang = np.resize(ang, (L, ang.shape[1])).astype(np.float32)
+    elif rope == "1d":
+        ang = oracle.rope_freqs_1d(L, hd, 10000.0, 0.19676)
+    else:
+        ang = None
+    cs = None if ang is None else oracle.rope_cs(ang)
+    d = torch.from_numpy(qkv).to(sdq_dev)
+    cs_d = None if cs is None else torch.from_numpy(cs).to(sdq_dev)
+    sdq.rmsnorm_rope(d, C, torch.from_numpy(wq).to(sdq_dev), heads, cs_d, col0=0)
+    sdq.rmsnorm_rope(d, C, torch.from_numpy(wk).to(sdq_dev), heads, cs_d, col0=C)
+    torch.cuda.synchronize()
+    got = d.cpu().numpy()
+    rows = np.arange(L) if L <= 400 else np.r_[0:8, 255:258, L // 2, L - 2, L - 1]
+    for part, w in ((0, wq), (1, wk)):
+        x = qkv[rows, part * C:(part + 1) * C]
+        want = oracle.rmsnorm(x, w, 1e-6)
+        if cs is not None:
+            want = oracle.rope(want, cs[rows], heads)
+        assert_bitexact(got[rows, part * C:(part + 1) * C], want, f"part {part}")
+    assert_bitexact(got[:, 2 * C:], qkv[:, 2 * C:], "v untouched")
+
+
+def test_rmsnorm_rope_errors(sdq_dev):
+    import torch
+
+    import sdq
+
+    x = torch.zeros((4, 96), device=sdq_dev)
+    w = torch.ones(96, device=sdq_dev)
+    with pytest.raises(sdq.SdqError, match="head_dim"):
+        sdq.rmsnorm_rope(x, 96, w, 5)  # 96 columns do not split into 5 heads

@@ -337,3 +337,47 @@ def test_mod_rows_matches_reference_build_and_closed_form(oracle, ref):
     assert (bits(got[fin]) == bits(once[fin])).mean() > 0.9999
     two = (x * (np.float32(1) + scale) + shift).astype(np.float32)  # planted: two roundings
     assert np.any(bits(two) != bits(got))
+
+
+def test_rmsnorm_matches_reference_build(oracle, ref):
+    x = _ln_rows(45, M=16, N=3072)
+    w = np.random.default_rng(46).standard_normal(3072).astype(np.float32)
+    want = ref.rmsnorm(x, w, 1e-6)
+    got = oracle.rmsnorm(x, w, 1e-6)
+    assert_bitexact(got, want, "rmsnorm vs reference build")
+    xd = x.astype(np.float64)
+    yd = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * w
+    ok = np.isfinite(yd).all(1) & (np.abs(x).max(1) < 1e10)
+    assert np.allclose(got[ok], yd[ok], rtol=2e-4, atol=2e-4)
+    # planted: a contracted sum of squares differs (on plain random rows)
+    xr = oracle.randn(64 * 3072, 48).reshape(64, 3072)
+    good = oracle.rmsnorm(xr, w, 1e-6)
+    fused = np.zeros(64, np.float32)
+    for k in range(3072):
+        fused = (xr[:, k].astype(np.float64) * xr[:, k] + fused).astype(np.float32)
+    inv = np.float32(1) / np.sqrt(fused / np.float32(3072) + np.float32(1e-6))
+    assert np.any(bits((xr * inv[:, None]) * w) != bits(good))
+
+
+def test_rope_tables_and_rotation_match_reference_build(oracle, ref):
+    # video: T x H x W tokens, audio: 1-D with the temporal scaling factor
+    a3 = oracle.rope_freqs_3d(3, 4, 5, 128, 10000.0)
+    assert_bitexact(a3, ref.rope_freqs_3d(3, 4, 5, 128, 10000.0), "rope_freqs_3d")
+    a1 = oracle.rope_freqs_1d(157, 128, 10000.0, 0.19676)
+    assert_bitexact(a1, ref.rope_freqs_1d(157, 128, 10000.0, 0.19676), "rope_freqs_1d")
+    assert a3.shape[1] == 64 and a1.shape[1] == 22
+    heads, hd = 24, 128
+    for ang in (a3, a1):
+        L = ang.shape[0]
+        x = oracle.randn(L * heads * hd, 47).reshape(L, heads * hd)
+        want = ref.apply_rope(x, ang, heads)
+        got = oracle.rope(x, oracle.rope_cs(ang), heads)
+        assert_bitexact(got, want, "apply_rope")
+        # a rotation keeps each pair's length; angle 0 (token 0) is the identity
+        nr = ang.shape[1]
+        p0 = x.reshape(L, heads, hd)[:, :, :2 * nr].astype(np.float64).reshape(L, heads, nr, 2)
+        p1 = got.reshape(L, heads, hd)[:, :, :2 * nr].astype(np.float64).reshape(L, heads, nr, 2)
+        assert np.allclose((p0 ** 2).sum(-1), (p1 ** 2).sum(-1), rtol=1e-5, atol=1e-6)
+        assert_bitexact(got[0], x[0], "angle 0")
+        assert_bitexact(got.reshape(L, heads, hd)[:, :, 2 * nr:], x.reshape(L, heads, hd)[:, :, 2 * nr:],
+                        "unrotated pairs")
