@@ -178,6 +178,18 @@ int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2,
 int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
                      int heads, const float* cs, int nr, void* stream);
 
+/* Scaled dot-product attention, non-causal (src/model/blocks.cpp:112-199
+ * sdpa, called by ovi_dit.cpp:186, 200, 241, 249): for every head h,
+ *   out[i, h] = sum_j softmax_j(q[i, h] . k[j, h] / sqrt(head_dim)) v[j, h]
+ * with q [Lq, ldq], k, v [Lk, ldk / ldv], out [Lq, ldo] row-major (e.g. the
+ * q, k, v column blocks of a q|k|v tensor), head h in columns
+ * h*head_dim .. h*head_dim+head_dim-1; head_dim = 128. fp32 MFMA with an
+ * online softmax: equal to the reference within rounding (its serial sums
+ * are not reproduced). 16-byte aligned rows. Stream-ordered. */
+int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+             float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
+             void* stream);
+
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
 

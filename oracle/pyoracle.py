@@ -47,6 +47,8 @@ def _load():
     lib.orc_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
     lib.orc_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
     lib.orc_rmsnorm.argtypes = [_f32p, _i64, _i64, _i64, _f32p, ctypes.c_float]
+    lib.orc_sdpa.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64,
+                             ctypes.c_int, ctypes.c_int, _f32p]
     lib.orc_rope_cs.argtypes = [_f32p, _i64, _f32p]
     lib.orc_rope.argtypes = [_f32p, _i64, _i64, _i64, ctypes.c_int, _f32p, ctypes.c_int]
     lib.orc_rope_freqs_3d.argtypes = [ctypes.c_int] * 4 + [ctypes.c_float, _f32p]
@@ -219,6 +221,19 @@ def rmsnorm(x, w, eps=1e-6):
     return y
 
 
+def sdpa(q, k, v, heads):
+    """blocks.cpp:112-199 (non-causal) on contiguous q [Lq, C], k, v [Lk, C]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    Lq, C = q.shape
+    Lk = k.shape[0]
+    out = np.empty((Lq, C), np.float32)
+    p = np.empty((max(Lk, 1),), np.float32)
+    lib().orc_sdpa(q, C, k, C, v, C, out, C, Lq, Lk, heads, C // heads, p)
+    return out
+
+
 def rope_cs(ang):
     """(cosf, sinf) of a [L, nr] angle table -> [L, nr, 2]."""
     ang = np.ascontiguousarray(ang, np.float32)
@@ -337,6 +352,8 @@ class Ref:
         L.sdref_rope_freqs_1d.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                           ctypes.c_float, _f32p]
         L.sdref_rope_freqs_1d.restype = ctypes.c_int
+        L.sdref_sdpa.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_int, _f32p]
+        L.sdref_sdpa.restype = ctypes.c_int
         self.L = L
         self.set_nthreads(nthreads or nthreads_default())
 
@@ -408,6 +425,15 @@ class Ref:
         ang = np.empty((L, head_dim), np.float32)
         nr = self.L.sdref_rope_freqs_1d(L, head_dim, theta, scaling, ang)
         return np.ascontiguousarray(ang.ravel()[:L * nr].reshape(L, nr))
+
+    def sdpa(self, q, k, v, heads):
+        q = np.ascontiguousarray(q, np.float32)
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        out = np.empty(q.shape, np.float32)
+        if self.L.sdref_sdpa(q, k, v, q.shape[0], k.shape[0], q.shape[1], heads, out) != 0:
+            raise RuntimeError("reference sdpa threw")
+        return out
 
     def randu(self, n, seed):
         x = np.empty((n,), np.float32)

@@ -36,6 +36,9 @@
  *   orc_rope, orc_rope_cs - compiled reference blk::apply_rope bit-exact; rotation
  *                          preserves each pair's norm (float64 check); angle 0 is
  *                          the identity.
+ *   orc_sdpa             - compiled reference blk::sdpa (oracle/_ref) bit-exact
+ *                          (AVX2 path); float64 softmax attention within
+ *                          tolerance; rows of p sum to 1.
  *   orc_rope_freqs_3d/1d - compiled reference rope_freqs_3d / rope_freqs_1d
  *                          bit-exact; float64 closed form within tolerance.
  *   orc_quantize_rowwise - compiled reference sd::quantize_rowwise bit-exact,
@@ -344,6 +347,43 @@ int orc_rope_freqs_1d(int L, int d, float theta, float scaling, float* ang) {
       ang[(int64_t)l * nr + j] = ls * powf(theta, (-2.f * (float)j) / (float)t_real);
     }
   return nr;
+}
+
+/* src/model/blocks.cpp:112-199 sdpa (non-causal), as the reference build's
+ * AVX2 path evaluates it: per head and query row i, s[j] = fl(dot * scale)
+ * with dot a serial fused multiply-add chain over d (scale = 1/sqrtf(hd));
+ * mx = max_j s[j]; p[j] = expf(s[j] - mx); sum = serial float sum of p;
+ * p[j] = fl(p[j] * fl(1/sum)); out[i, d] = serial fma chain over j of
+ * p[j] * v[j, d]. Rows of stride ldq / ldk / ldv / ldo floats; head h uses
+ * columns h*hd .. h*hd+hd-1. p: scratch of Lk floats. */
+void orc_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+              float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int hd, float* p) {
+  const float scale = 1.f / sqrtf((float)hd);
+  for (int h = 0; h < heads; h++)
+    for (int64_t i = 0; i < Lq; i++) {
+      const float* qi = q + i * ldq + (int64_t)h * hd;
+      float mx = -INFINITY;
+      for (int64_t j = 0; j < Lk; j++) {
+        const float* kj = k + j * ldk + (int64_t)h * hd;
+        float acc = 0.f;
+        for (int d = 0; d < hd; d++) acc = fmaf(qi[d], kj[d], acc);
+        p[j] = acc * scale;
+        mx = p[j] > mx ? p[j] : mx;
+      }
+      float sum = 0.f;
+      for (int64_t j = 0; j < Lk; j++) {
+        p[j] = expf(p[j] - mx);
+        sum = sum + p[j];
+      }
+      const float inv = 1.f / sum;
+      for (int64_t j = 0; j < Lk; j++) p[j] = p[j] * inv;
+      float* o = out + i * ldo + (int64_t)h * hd;
+      for (int d = 0; d < hd; d++) {
+        float acc = 0.f;
+        for (int64_t j = 0; j < Lk; j++) acc = fmaf(p[j], v[j * ldv + (int64_t)h * hd + d], acc);
+        o[d] = acc;
+      }
+    }
 }
 
 /* src/model/ovi_dit.cpp:132-142 gelu_tanh_inplace (nn.GELU(approximate='tanh')).

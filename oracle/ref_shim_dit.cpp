@@ -98,4 +98,17 @@ int sdref_rope_freqs_1d(int L, int hd, float theta, float scaling, float* ang) {
   }
 }
 
+// blk::sdpa(q, k, v, heads, out) (blocks.cpp:112-199) on contiguous [L, C].
+int sdref_sdpa(const float* q, const float* k, const float* v, int64_t Lq, int64_t Lk, int64_t C,
+               int heads, float* out) {
+  try {
+    sd::Tensor o;
+    sd::blk::sdpa(fview(q, {Lq, C}), fview(k, {Lk, C}), fview(v, {Lk, C}), heads, o, false);
+    std::memcpy(out, o.data, (size_t)(Lq * C) * 4);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
 }  // extern "C"

@@ -707,6 +707,41 @@ int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
   return SDQ_OK;
 }
 
+int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
+             float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
+             void* stream) {
+  if (Lq < 0 || Lk < 0) return set_error(SDQ_ERR_INVALID, "negative Lq or Lk");
+  if (Lq == 0) return SDQ_OK;
+  if (Lk == 0) return set_error(SDQ_ERR_INVALID, "sdpa: no keys");
+  if (head_dim != 128) return set_error(SDQ_ERR_INVALID, "sdpa: head_dim must be 128");
+  if (heads <= 0) return set_error(SDQ_ERR_INVALID, "sdpa: heads must be positive");
+  if (!q || !k || !v || !out) return set_error(SDQ_ERR_INVALID, "sdpa: null pointer");
+  const int64_t C = (int64_t)heads * head_dim;
+  if (ldq < C || ldk < C || ldv < C || ldo < C)
+    return set_error(SDQ_ERR_INVALID, "sdpa: row strides must cover heads * head_dim");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || ldq % 4 || ldk % 4 ||
+      ldv % 4 || ldo % 4)
+    return set_error(SDQ_ERR_INVALID, "sdpa: 16-byte aligned rows required");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s);
+  if (e != hipSuccess) return hip_error(e, "sdpa launch");
+  if (t_prof) {
+    hipEvent_t p1 = prof_mark(s);
+    if (p0 && p1) {
+      t_recs.push_back({"sdpa", p0, p1});
+    } else {
+      for (hipEvent_t ev : {p0, p1})
+        if (ev) (void)hipEventDestroy(ev);
+    }
+  }
+  return SDQ_OK;
+}
+
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream) {
   return qlinear_device(w, A, M, K, nullptr, Y, static_cast<hipStream_t>(stream));
 }

@@ -96,4 +96,191 @@ hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// Scaled dot-product attention (src/model/blocks.cpp:112-199, non-causal):
+// out[i, head] = softmax_j(q_i . k_j / sqrt(hd)) v_j, head_dim 128, fp32
+// throughout: v_mfma_f32_32x32x2_f32 and an online softmax (running max and
+// sum per query, the accumulator rescaled when the max moves). The reference
+// sums in a fixed serial order, so results agree within rounding, not bit
+// for bit.
+//
+// Work: a workgroup of NW waves takes 32*NW queries of one head; each wave
+// 32 queries. Per 32-key block, K (32 x 128) and V^T (128 x 32) are staged
+// in LDS (double-buffered, prefetched through registers) and every wave
+//   S^T = K . Q^T    32 keys x 32 queries: lane (query j = l & 31, half
+//                    h = l >> 5) holds 16 keys of its query, so the softmax
+//                    of a query is one lane plus its partner lane l ^ 32;
+//                    MFMA step s takes dim 64h + s in both operands (Q stays
+//                    in 64 VGPRs, K is read 16 bytes at a time).
+//   O^T += V^T . P^T 128 dims x 32 queries in four 32 x 32 tiles; step t's
+//                    key in half h is 8(t/4) + 4h + t%4, exactly the key of
+//                    the lane's S^T register t, so P feeds the MFMA with no
+//                    shuffle.
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int kHd = 128;      // head dim
+constexpr int kKB = 32;       // keys per block
+constexpr int kKPad = 132;    // LDS row of K (floats): conflict-free 16-byte reads
+constexpr int kVPad = 36;     // LDS row of V^T
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64)
+sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
+            const float* __restrict__ V, int64_t ldv, float* __restrict__ O, int64_t ldo,
+            int64_t Lq, int64_t Lk, int qgroups, float scale_log2e) {
+  __shared__ __attribute__((aligned(16))) float ks[2][kKB][kKPad];
+  __shared__ __attribute__((aligned(16))) float vt[2][kHd][kVPad];
+  constexpr int NT = NW * 64;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int head = blockIdx.x / qgroups, qg = blockIdx.x - head * qgroups;
+  const int64_t q0 = ((int64_t)qg * NW + w) * 32;
+  const int j = lane & 31, h = lane >> 5;
+  const int64_t col = (int64_t)head * kHd;
+
+  // this lane's query row, dims 64h .. 64h+63
+  float qr[64];
+  {
+    const int64_t qi = q0 + j;
+    const float* src = Q + (qi < Lq ? qi : 0) * ldq + col + 64 * h;
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+      const float4 v = qi < Lq ? reinterpret_cast<const float4*>(src)[c] : float4{0.f, 0.f, 0.f, 0.f};
+      qr[4 * c] = v.x;
+      qr[4 * c + 1] = v.y;
+      qr[4 * c + 2] = v.z;
+      qr[4 * c + 3] = v.w;
+    }
+  }
+  // cooperative block load: 32 keys x 32 float4 each of K and V
+  constexpr int PER = (kKB * kHd / 4 + NT - 1) / NT;
+  float4 pk[PER], pv[PER];
+  auto fetch = [&](int64_t kb) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int f = tid + c * NT;
+      const int key = f >> 5, d4 = f & 31;
+      const int64_t kr = kb * kKB + key;
+      const bool ok = f < kKB * kHd / 4 && kr < Lk;
+      pk[c] = ok ? *reinterpret_cast<const float4*>(K + kr * ldk + col + 4 * d4)
+                 : float4{0.f, 0.f, 0.f, 0.f};
+      pv[c] = ok ? *reinterpret_cast<const float4*>(V + kr * ldv + col + 4 * d4)
+                 : float4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto stash = [&](int b) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int f = tid + c * NT;
+      if (f < kKB * kHd / 4) {
+        const int key = f >> 5, d4 = f & 31;
+        *reinterpret_cast<float4*>(&ks[b][key][4 * d4]) = pk[c];
+        vt[b][4 * d4][key] = pv[c].x;
+        vt[b][4 * d4 + 1][key] = pv[c].y;
+        vt[b][4 * d4 + 2][key] = pv[c].z;
+        vt[b][4 * d4 + 3][key] = pv[c].w;
+      }
+    }
+  };
+
+  v16f acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) acc[t] = v16f{};
+  float m = -INFINITY, lsum = 0.f;
+  const int64_t nkb = (Lk + kKB - 1) / kKB;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int64_t kb = 0; kb < nkb; kb++) {
+    const int b = (int)(kb & 1);
+    if (kb + 1 < nkb) fetch(kb + 1);
+    // S^T = K . Q^T (keys x queries)
+    v16f st = v16f{};
+    const float* krow = &ks[b][j][64 * h];
+#pragma unroll
+    for (int s4 = 0; s4 < 16; s4++) {
+      const float4 kv = *reinterpret_cast<const float4*>(krow + 4 * s4);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qr[4 * s4], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qr[4 * s4 + 1], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qr[4 * s4 + 2], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qr[4 * s4 + 3], st, 0, 0, 0);
+    }
+    // online softmax (base 2): register r holds key kb*32 + 8(r/4) + 4h + r%4
+    float t[16];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int64_t key = kb * kKB + 8 * (r >> 2) + 4 * h + (r & 3);
+      t[r] = key < Lk ? st[r] * scale_log2e : -INFINITY;
+      mloc = mloc < t[r] ? t[r] : mloc;
+    }
+    const float mo = __shfl_xor(mloc, 32);
+    const float mnew = fmaxf(m, fmaxf(mloc, mo));
+    const float alpha = exp2f(m - mnew);  // m = -inf at the first block: 0
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      t[r] = exp2f(t[r] - mnew);
+      ps += t[r];
+    }
+    lsum = lsum * alpha + ps;
+    m = mnew;
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++) acc[tt] *= alpha;
+    // O^T += V^T . P^T
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++) {
+      const float* vrow = &vt[b][32 * tt + j][4 * h];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float4 vv = *reinterpret_cast<const float4*>(vrow + 8 * u);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, t[4 * u], acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, t[4 * u + 1], acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, t[4 * u + 2], acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, t[4 * u + 3], acc[tt], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave is done with buffer b^1's previous block
+    if (kb + 1 < nkb) stash(b ^ 1);
+    __syncthreads();
+  }
+  // out[query][dim]: lane holds dims 32tt + 8(r/4) + 4h + r%4 of query j
+  const float inv = 1.f / (lsum + __shfl_xor(lsum, 32));
+  const int64_t qi = q0 + j;
+  if (qi < Lq) {
+    float* dst = O + qi * ldo + col;
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float4 o = {acc[tt][4 * g] * inv, acc[tt][4 * g + 1] * inv, acc[tt][4 * g + 2] * inv,
+                          acc[tt][4 * g + 3] * inv};
+        *reinterpret_cast<float4*>(dst + 32 * tt + 8 * g + 4 * h) = o;
+      }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                       int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
+                       hipStream_t s) {
+  if (Lq <= 0) return hipSuccess;
+  if (Lk <= 0 || heads <= 0) return hipErrorInvalidValue;
+  const float scale_log2e = (1.f / sqrtf((float)kHd)) * 1.4426950408889634f;
+  if (Lq >= 1024) {
+    constexpr int NW = 8;
+    const int qgroups = (int)ceil_div(Lq, 32 * NW);
+    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads)), dim3(NW * 64), 0, s, q,
+                       ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups, scale_log2e);
+  } else {
+    constexpr int NW = 2;
+    const int qgroups = (int)ceil_div(Lq, 32 * NW);
+    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads)), dim3(NW * 64), 0, s, q,
+                       ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups, scale_log2e);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace sdq

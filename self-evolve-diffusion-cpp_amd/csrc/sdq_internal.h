@@ -98,6 +98,11 @@ hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, in
 hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
                                float eps, int heads, const float* cs, int nr, float* inv,
                                hipStream_t s);
+// Attention, head_dim 128 (launch_sdpa rejects nothing else; the API checks):
+// out[i, head cols] = softmax(q_i . k_j / sqrt(128)) v_j over j < Lk.
+hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                       int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
+                       hipStream_t s);
 // Same output, with the row maxima already known: max_c rmax[row*rstride + c]
 // over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
 // read once.

@@ -64,6 +64,8 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_sdpa": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
+                                ctypes.c_int, ctypes.c_int, _vp]),
     "sdq_rmsnorm_rope": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int,
                                         _vp, ctypes.c_int, _vp]),
     "sdq_ffn": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _vp, _vp]),
@@ -277,6 +279,17 @@ def ffn_lnmod(fc1: Weight, b1, fc2: Weight, b2, x, shift, scale, gate, hid, eps=
                               _ptr(scale), eps, _ptr(gate), 1 if gate_fma else 0, _ptr(hid),
                               _stream(stream)))
     return x
+
+
+def sdpa(q, k, v, out, heads, qcol=0, kcol=0, vcol=0, stream=None):
+    """out = attention(q, k, v) over `heads` heads of 128 columns, taken from
+    column offsets qcol / kcol / vcol of the device tensors q, k, v (e.g. one
+    q|k|v tensor passed three times)."""
+    Lq, Lk = q.shape[0], k.shape[0]
+    P = lambda t, c: ctypes.c_void_p(t.data_ptr() + 4 * c)  # noqa: E731
+    _check(_lib.sdq_sdpa(P(q, qcol), q.shape[1], P(k, kcol), k.shape[1], P(v, vcol), v.shape[1],
+                         _ptr(out), out.shape[1], Lq, Lk, heads, 128, _stream(stream)))
+    return out
 
 
 def rmsnorm_rope(x, C, w, heads, cs=None, eps=1e-6, col0=0, stream=None):

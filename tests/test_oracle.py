@@ -381,3 +381,23 @@ def test_rope_tables_and_rotation_match_reference_build(oracle, ref):
         assert_bitexact(got[0], x[0], "angle 0")
         assert_bitexact(got.reshape(L, heads, hd)[:, :, 2 * nr:], x.reshape(L, heads, hd)[:, :, 2 * nr:],
                         "unrotated pairs")
+
+
+def test_sdpa_matches_reference_build(oracle, ref):
+    heads, hd = 4, 128
+    for (Lq, Lk, seed) in ((37, 53, 60), (64, 7, 61), (5, 130, 62)):
+        rng = np.random.default_rng(seed)
+        q = (rng.standard_normal((Lq, heads * hd)) * 0.5).astype(np.float32)
+        k = (rng.standard_normal((Lk, heads * hd)) * 0.5).astype(np.float32)
+        v = rng.standard_normal((Lk, heads * hd)).astype(np.float32)
+        got = oracle.sdpa(q, k, v, heads)
+        assert_bitexact(got, ref.sdpa(q, k, v, heads), f"sdpa {Lq}x{Lk}")
+        # float64 softmax attention
+        want = np.empty_like(got, np.float64)
+        for h in range(heads):
+            sl = slice(h * hd, (h + 1) * hd)
+            s = q[:, sl].astype(np.float64) @ k[:, sl].astype(np.float64).T / np.sqrt(hd)
+            pr = np.exp(s - s.max(1, keepdims=True))
+            pr /= pr.sum(1, keepdims=True)
+            want[:, sl] = pr @ v[:, sl]
+        assert np.allclose(got, want, rtol=1e-4, atol=1e-5)
