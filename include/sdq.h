@@ -173,10 +173,22 @@ int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2,
  *   x = apply_rope(x, heads)      src/model/blocks.cpp:86-100
  * where cs [L][nr][2] holds (cosf, sinf) of each token's nr rotated pair
  * angles (the reference's RopeFreqs.ang through the same libm calls, done by
- * the caller); nr = 0 / cs = NULL skips the rotation (cross-attention q, k).
- * Bit-exact with the reference build. Stream-ordered. */
+ * the caller); nr = 0 / cs = NULL skips the rotation (cross-attention q, k),
+ * w = NULL skips the rmsnorm (the fusion attention's late rotation of q,
+ * ovi_dit.cpp:247). Bit-exact with the reference build. Stream-ordered. */
 int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
                      int heads, const float* cs, int nr, void* stream);
+
+/* blk::layernorm (src/model/blocks.cpp:18-43) on the GPU, bit-exact with the
+ * reference build: y = fmaf(fl((x - mu)*inv), w, b) with serial-sum row
+ * statistics; w, b nullable (1, 0). x, y [M,K] contiguous device arrays
+ * (may be the same). Used for the fusion target's pre-norm (ovi_dit.cpp:243)
+ * and norm3 (263). */
+int sdq_layernorm(const float* x, int64_t M, int64_t K, const float* w, const float* b, float eps,
+                  float* y, void* stream);
+
+/* x += y elementwise (add_inplace, src/model/ovi_dit.cpp:144-149), n floats. */
+int sdq_add(float* x, const float* y, int64_t n, void* stream);
 
 /* Scaled dot-product attention, non-causal (src/model/blocks.cpp:112-199
  * sdpa, called by ovi_dit.cpp:186, 200, 241, 249): for every head h,

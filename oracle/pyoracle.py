@@ -45,6 +45,8 @@ def _load():
     lib.orc_add.argtypes = [_f32p, _f32p, _i64]
     lib.orc_gelu_tanh.argtypes = [_f32p, _i64]
     lib.orc_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
+    lib.orc_layernorm_affine.argtypes = [_f32p, _i64, _i64, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_float, _f32p]
     lib.orc_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
     lib.orc_rmsnorm.argtypes = [_f32p, _i64, _i64, _i64, _f32p, ctypes.c_float]
     lib.orc_sdpa.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64,
@@ -194,12 +196,18 @@ def gelu_tanh(x):
     return x
 
 
-def layernorm(x, eps=1e-6):
-    """blocks.cpp:18-43 with no affine (the DiT's norm1/norm2)."""
+def layernorm(x, eps=1e-6, w=None, b=None):
+    """blocks.cpp:18-43 (no affine unless w / b: norm3, the fusion pre-norm)."""
     x = np.ascontiguousarray(x, np.float32)
     M, N = x.shape
     y = np.empty_like(x)
-    lib().orc_layernorm(x, M, N, eps, y)
+    if w is None and b is None:
+        lib().orc_layernorm(x, M, N, eps, y)
+    else:
+        w = None if w is None else np.ascontiguousarray(w, np.float32)
+        b = None if b is None else np.ascontiguousarray(b, np.float32)
+        lib().orc_layernorm_affine(x, M, N, None if w is None else w.ctypes.data,
+                                   None if b is None else b.ctypes.data, eps, y)
     return y
 
 
@@ -339,7 +347,8 @@ class Ref:
             ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
             ctypes.POINTER(ctypes.c_int), ctypes.c_char_p, ctypes.c_int]
         L.sdref_sdcpp_lookup.restype = ctypes.c_int
-        L.sdref_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
+        L.sdref_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, ctypes.c_void_p,
+                                      ctypes.c_void_p, _f32p]
         L.sdref_layernorm.restype = ctypes.c_int
         L.sdref_mod_rows.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _f32p]
         L.sdref_mod_rows.restype = ctypes.c_int
@@ -384,11 +393,14 @@ class Ref:
         self.L.sdref_quantize_rowwise(W, N, K, q, s)
         return q, s
 
-    def layernorm(self, x, eps=1e-6):
+    def layernorm(self, x, eps=1e-6, w=None, b=None):
         x = np.ascontiguousarray(x, np.float32)
         M, N = x.shape
         y = np.empty_like(x)
-        if self.L.sdref_layernorm(x, M, N, eps, y) != 0:
+        w = None if w is None else np.ascontiguousarray(w, np.float32)
+        b = None if b is None else np.ascontiguousarray(b, np.float32)
+        if self.L.sdref_layernorm(x, M, N, eps, None if w is None else w.ctypes.data,
+                                  None if b is None else b.ctypes.data, y) != 0:
             raise RuntimeError("reference layernorm threw")
         return y
 

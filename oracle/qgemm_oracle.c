@@ -26,8 +26,9 @@
  *                          y*g+x rounded once (exact for fp32 inputs).
  *   orc_add              - numpy float32 add.
  *   orc_gelu_tanh        - float64 closed form within tolerance only.
- *   orc_layernorm        - compiled reference blk::layernorm (oracle/_ref)
- *                          bit-exact, incl. zero, constant, tiny and huge rows;
+ *   orc_layernorm(_affine) - compiled reference blk::layernorm (oracle/_ref)
+ *                          bit-exact, with and without the affine, incl. zero,
+ *                          constant, tiny and huge rows;
  *                          float64 closed form within tolerance.
  *   orc_mod_rows         - compiled reference mod_rows (oracle/_ref) bit-exact;
  *                          float64 x*(1+h)+s rounded once.
@@ -235,7 +236,17 @@ void orc_add(float* x, const float* y, int64_t n) {
  * and the variance are serial float sums in k order; the variance adds the
  * rounded d*d (not contracted); inv = 1/sqrtf(var/N + eps); the output is
  * (x - mu)*inv*1 + 0 (the +0 turns -0 into +0). */
+void orc_layernorm_affine(const float* x, int64_t M, int64_t N, const float* w, const float* b,
+                          float eps, float* y);
 void orc_layernorm(const float* x, int64_t M, int64_t N, float eps, float* y) {
+  orc_layernorm_affine(x, M, N, NULL, NULL, eps, y);
+}
+
+/* The same with the affine (w, b nullable: 1 and 0), as the reference build
+ * contracts its output: y = fmaf(fl((x - mu)*inv), w, b) (pinned against
+ * oracle/_ref; with w = 1, b = 0 this is t + 0). */
+void orc_layernorm_affine(const float* x, int64_t M, int64_t N, const float* w, const float* b,
+                          float eps, float* y) {
   for (int64_t i = 0; i < M; i++) {
     const float* r = x + i * N;
     float mu = 0.f;
@@ -250,7 +261,7 @@ void orc_layernorm(const float* x, int64_t M, int64_t N, float eps, float* y) {
     const float inv = 1.f / sqrtf(var / (float)N + eps);
     for (int64_t k = 0; k < N; k++) {
       const float t = (r[k] - mu) * inv;
-      y[i * N + k] = t * 1.f + 0.f;
+      y[i * N + k] = fmaf(t, w ? w[k] : 1.f, b ? b[k] : 0.f);
     }
   }
 }

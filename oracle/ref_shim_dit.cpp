@@ -26,11 +26,14 @@ sd::Tensor fview(const float* p, std::initializer_list<int64_t> shape) {
 
 extern "C" {
 
-// blk::layernorm(x, y, nullptr, nullptr, eps) on caller buffers [M,N].
-int sdref_layernorm(const float* x, int64_t M, int64_t N, float eps, float* y) {
+// blk::layernorm(x, y, w, b, eps) on caller buffers [M,N] (w, b nullable).
+int sdref_layernorm(const float* x, int64_t M, int64_t N, float eps, const float* w,
+                    const float* b, float* y) {
   try {
-    sd::Tensor out;
-    sd::blk::layernorm(fview(x, {M, N}), out, nullptr, nullptr, eps);
+    sd::Tensor out, tw, tb;
+    if (w) tw = fview(w, {N});
+    if (b) tb = fview(b, {N});
+    sd::blk::layernorm(fview(x, {M, N}), out, w ? &tw : nullptr, b ? &tb : nullptr, eps);
     std::memcpy(y, out.data, (size_t)(M * N) * 4);
     return 0;
   } catch (const std::exception&) {

@@ -679,7 +679,8 @@ int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
                      int heads, const float* cs, int nr, void* stream) {
   if (L < 0) return set_error(SDQ_ERR_INVALID, "negative L");
   if (L == 0) return SDQ_OK;
-  if (!x || !w) return set_error(SDQ_ERR_INVALID, "null x or weight");
+  if (!x) return set_error(SDQ_ERR_INVALID, "null x");
+  if (!w && (nr <= 0 || !cs)) return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: nothing to do");
   if (C <= 0 || ld < C || heads <= 0 || C % heads != 0 || (C / heads) % 2 != 0)
     return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need C > 0, ld >= C, C = heads * even head_dim");
   if (nr < 0 || nr > C / heads / 2 || (nr > 0 && !cs))
@@ -690,7 +691,7 @@ int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
   if ((rc = ensure_device(dev))) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   float* inv = nullptr;
-  if ((rc = ws_floats(dev, s, &Workspace::rinv, &Workspace::rinv_bytes, (size_t)L * 4, &inv)))
+  if (w && (rc = ws_floats(dev, s, &Workspace::rinv, &Workspace::rinv_bytes, (size_t)L * 4, &inv)))
     return rc;
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   hipError_t e = launch_rmsnorm_rope(x, L, C, ld, w, eps, heads, nr > 0 ? cs : nullptr, nr, inv, s);
@@ -705,6 +706,48 @@ int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
     }
   }
   return SDQ_OK;
+}
+
+int sdq_layernorm(const float* x, int64_t M, int64_t K, const float* w, const float* b, float eps,
+                  float* y, void* stream) {
+  if (M < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative dims");
+  if (M == 0) return SDQ_OK;
+  if (K == 0 || !x || !y) return set_error(SDQ_ERR_INVALID, "layernorm: null data or K = 0");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  float2* st = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace& ws = g_ws[{dev, s}];
+    if ((rc = grow(s, reinterpret_cast<void**>(&ws.st), &ws.st_bytes, (size_t)M * sizeof(float2))))
+      return rc;
+    st = ws.st;
+  }
+  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  hipError_t e = launch_ln_stats(x, M, K, eps, st, s);
+  if (e == hipSuccess) e = launch_ln_apply(x, M, K, st, w, b, y, s);
+  if (e != hipSuccess) return hip_error(e, "layernorm launch");
+  if (t_prof) {
+    hipEvent_t p1 = prof_mark(s);
+    if (p0 && p1) {
+      t_recs.push_back({"layernorm", p0, p1});
+    } else {
+      for (hipEvent_t ev : {p0, p1})
+        if (ev) (void)hipEventDestroy(ev);
+    }
+  }
+  return SDQ_OK;
+}
+
+int sdq_add(float* x, const float* y, int64_t n, void* stream) {
+  if (n < 0) return set_error(SDQ_ERR_INVALID, "negative n");
+  if (n == 0) return SDQ_OK;
+  if (!x || !y) return set_error(SDQ_ERR_INVALID, "add: null pointer");
+  hipError_t e = launch_add(x, y, n, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? SDQ_OK : hip_error(e, "add launch");
 }
 
 int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,

@@ -50,9 +50,13 @@ rms_rope_apply_kernel(float* __restrict__ x, int64_t L, int64_t C, int64_t ld,
   const int64_t row = idx / np, p = idx - row * np;
   const int64_t c0 = 2 * p;
   float* q = x + row * ld + c0;
-  const float iv = inv[row];
-  const float a = q[0] * iv, b = q[1] * iv;
-  float y0 = a * w[c0], y1 = b * w[c0 + 1];
+  float y0 = q[0], y1 = q[1];
+  if (w) {
+    const float iv = inv[row];
+    const float a = y0 * iv, b = y1 * iv;
+    y0 = a * w[c0];
+    y1 = b * w[c0 + 1];
+  }
   const int j = (int)(c0 % hd) / 2;  // pair index inside the head
   if (cs && j < nr) {
     const float2 t = cs[row * nr + j];  // (cos, sin)
@@ -75,11 +79,13 @@ hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const
                                hipStream_t s) {
   if (L <= 0) return hipSuccess;
   if (C <= 0 || ld < C || heads <= 0 || C % heads || (C / heads) % 2 || nr < 0 ||
-      nr > C / heads / 2 || !w || !inv)
+      nr > C / heads / 2 || (!w && !cs) || (w && !inv))
     return hipErrorInvalidValue;
   const bool vec = aligned16(x) && ld % 4 == 0 && C % 4 == 0, few = L <= 4096;
   const dim3 g((unsigned)ceil_div(L, 8)), b(64);
-  if (vec && few)
+  if (!w) {
+    // rotation only
+  } else if (vec && few)
     hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthFew>), g, b, 0, s, x, L, C, ld, eps, inv);
   else if (vec)
     hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthMany>), g, b, 0, s, x, L, C, ld, eps, inv);
@@ -96,6 +102,43 @@ hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const
   return hipGetLastError();
 }
 
+
+namespace {
+
+__global__ void __launch_bounds__(256)
+ln_apply_kernel(const float* x, int64_t M, int64_t K, const float2* __restrict__ st,
+                const float* __restrict__ w, const float* __restrict__ b, float* y) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * K) return;
+  const int64_t row = idx / K, k = idx - row * K;
+  const float2 s2 = st[row];
+  const float d = x[idx] - s2.x;
+  const float t = d * s2.y;
+  y[idx] = __builtin_fmaf(t, w ? w[k] : 1.f, b ? b[k] : 0.f);
+}
+
+__global__ void __launch_bounds__(256)
+add_kernel(float* x, const float* y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] + y[i];
+}
+
+}  // namespace
+
+hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* st, const float* w,
+                           const float* b, float* y, hipStream_t s) {
+  const int64_t n = M * K;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ln_apply_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, x, M, K,
+                     st, w, b, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(add_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Scaled dot-product attention (src/model/blocks.cpp:112-199, non-causal):

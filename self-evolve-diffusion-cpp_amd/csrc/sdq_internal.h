@@ -92,12 +92,22 @@ hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, in
                                         int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
                                         const float* shift, const float* scale, float eps,
                                         float2* st, hipStream_t s);
-// In place on L rows of stride ld (C columns): rmsnorm with weight w, then
-// RoPE of each head's first nr pairs with the (cos, sin) table cs [L][nr]
-// (cs == nullptr: no RoPE). inv: [L] scratch.
+// In place on L rows of stride ld (C columns): rmsnorm with weight w (w ==
+// nullptr: none), then RoPE of each head's first nr pairs with the (cos, sin)
+// table cs [L][nr] (cs == nullptr: no RoPE). inv: [L] scratch.
 hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
                                float eps, int heads, const float* cs, int nr, float* inv,
                                hipStream_t s);
+// Per-row (mean, 1/std) of blocks.cpp:18-43 into st[M] (bit-exact serial
+// sums); rows of K floats, contiguous.
+hipError_t launch_ln_stats(const float* A, int64_t M, int64_t K, float eps, float2* st,
+                           hipStream_t s);
+// y = fmaf(fl((x - mu)*inv), w, b) with st from launch_ln_stats (w, b
+// nullable: 1, 0). x, y: [M, K] contiguous (may alias).
+hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* st, const float* w,
+                           const float* b, float* y, hipStream_t s);
+// x[i] += y[i], i < n.
+hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s);
 // Attention, head_dim 128 (launch_sdpa rejects nothing else; the API checks):
 // out[i, head cols] = softmax(q_i . k_j / sqrt(128)) v_j over j < Lk.
 hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,

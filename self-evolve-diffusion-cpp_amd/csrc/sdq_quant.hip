@@ -487,12 +487,10 @@ hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t 
   return hipGetLastError();
 }
 
-hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, int64_t Mp,
-                                        int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
-                                        const float* shift, const float* scale, float eps,
-                                        float2* st, hipStream_t s) {
-  if (!shift || !scale || !st || K <= 0) return hipErrorInvalidValue;
-  const int vec = (aligned16(A) && aligned16(shift) && aligned16(scale) && (K % 4) == 0) ? 1 : 0;
+hipError_t launch_ln_stats(const float* A, int64_t M, int64_t K, float eps, float2* st,
+                           hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  if (K <= 0 || !st) return hipErrorInvalidValue;
   const bool vx = aligned16(A) && (K % 4) == 0, few = M <= 4096;
   const dim3 g((unsigned)ceil_div(M, 8)), b(64);
   if (vx && few)
@@ -503,7 +501,16 @@ hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, in
     hipLaunchKernelGGL((ln_stats_kernel<false, kLnDepthFew>), g, b, 0, s, A, M, K, eps, st);
   else
     hipLaunchKernelGGL((ln_stats_kernel<false, kLnDepthMany>), g, b, 0, s, A, M, K, eps, st);
-  hipError_t e = hipGetLastError();
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, int64_t Mp,
+                                        int64_t KFp, int8_t* at, float* as, const ColCopy& cc,
+                                        const float* shift, const float* scale, float eps,
+                                        float2* st, hipStream_t s) {
+  if (!shift || !scale || !st || K <= 0) return hipErrorInvalidValue;
+  const int vec = (aligned16(A) && aligned16(shift) && aligned16(scale) && (K % 4) == 0) ? 1 : 0;
+  hipError_t e = launch_ln_stats(A, M, K, eps, st, s);
   if (e != hipSuccess) return e;
   const int64_t units = Mp / kQuantRows;
   LnModArgs lm{st, shift, scale};

@@ -64,6 +64,8 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
+    "sdq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "sdq_sdpa": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
                                 ctypes.c_int, ctypes.c_int, _vp]),
     "sdq_rmsnorm_rope": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int,
@@ -278,6 +280,17 @@ def ffn_lnmod(fc1: Weight, b1, fc2: Weight, b2, x, shift, scale, gate, hid, eps=
     _check(_lib.sdq_ffn_lnmod(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(x), M, _ptr(shift),
                               _ptr(scale), eps, _ptr(gate), 1 if gate_fma else 0, _ptr(hid),
                               _stream(stream)))
+    return x
+
+
+def layernorm(x, y, w=None, b=None, eps=1e-6, stream=None):
+    M, K = x.shape
+    _check(_lib.sdq_layernorm(_ptr(x), M, K, _ptr(w), _ptr(b), eps, _ptr(y), _stream(stream)))
+    return y
+
+
+def add_(x, y, stream=None):
+    _check(_lib.sdq_add(_ptr(x), _ptr(y), x.numel(), _stream(stream)))
     return x
 
 

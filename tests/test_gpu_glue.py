@@ -121,3 +121,55 @@ def test_sdpa_errors(sdq_dev):
     q = torch.zeros((4, 96), device=sdq_dev)
     with pytest.raises(sdq.SdqError, match="row strides"):
         sdq.sdpa(q, q, q, q, 1)  # 96 columns < one head of 128
+
+
+@pytest.mark.parametrize("M,K,affine", [(1, 3072, True), (157, 3072, True), (300, 3072, False),
+                                        (77, 100, True), (2000, 3072, True)])
+def test_layernorm_bitexact(sdq_dev, oracle, M, K, affine):
+    """sdq_layernorm against the oracle's layernorm (pinned to the reference
+    build's blk::layernorm, affine output fmaf(t, w, b)), bit-exact; ragged K,
+    a constant row (variance 0) and large offsets included."""
+    import torch
+
+    import sdq
+
+    print(f"[layernorm] M={M} K={K} affine={affine}", flush=True)
+    rng = np.random.default_rng(M * 3 + K)
+    x = (oracle.randn(M * K, 70 + M).reshape(M, K)
+         * rng.uniform(0.1, 20, (M, 1)) + rng.uniform(-50, 50, (M, 1))).astype(np.float32)
+    x[M // 2] = np.float32(3.25)
+    w = oracle.randn(K, 71) if affine else None
+    b = oracle.randn(K, 72) if affine else None
+    want = oracle.layernorm(x, 1e-6, w, b)
+    xd = torch.from_numpy(x).to(sdq_dev)
+    y = torch.full_like(xd, float("nan"))
+    dev = (lambda a: None if a is None else torch.from_numpy(a).to(sdq_dev))
+    sdq.layernorm(xd, y, dev(w), dev(b), 1e-6)
+    sdq.layernorm(xd, xd, dev(w), dev(b), 1e-6)  # in place
+    torch.cuda.synchronize()
+    assert_bitexact(y.cpu().numpy(), want, "layernorm")
+    assert_bitexact(xd.cpu().numpy(), want, "layernorm in place")
+
+
+def test_rope_only_and_add(sdq_dev, oracle):
+    """The fusion attention's late rotation of q (no rmsnorm, w = NULL) and
+    the x += y of its two attention outputs, bit-exact."""
+    import torch
+
+    import sdq
+
+    heads, hd, L = 3, 128, 130
+    C = heads * hd
+    x = oracle.randn(L * C, 80).reshape(L, C) * np.float32(4.0)
+    y = oracle.randn(L * C, 81).reshape(L, C)
+    cs = oracle.rope_cs(oracle.rope_freqs_1d(L, hd, 10000.0, 1.0))
+    xd = torch.from_numpy(x).to(sdq_dev)
+    sdq.rmsnorm_rope(xd, C, None, heads, torch.from_numpy(cs).to(sdq_dev))
+    torch.cuda.synchronize()
+    assert_bitexact(xd.cpu().numpy(), oracle.rope(x, cs, heads), "rope only")
+    xd = torch.from_numpy(x).to(sdq_dev)
+    sdq.add_(xd, torch.from_numpy(y).to(sdq_dev))
+    torch.cuda.synchronize()
+    assert_bitexact(xd.cpu().numpy(), oracle.add(x, y), "add")
+    with pytest.raises(sdq.SdqError, match="nothing to do"):
+        sdq.rmsnorm_rope(xd, C, None, heads, None)

@@ -401,3 +401,16 @@ def test_sdpa_matches_reference_build(oracle, ref):
             pr /= pr.sum(1, keepdims=True)
             want[:, sl] = pr @ v[:, sl]
         assert np.allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+def test_affine_layernorm_matches_reference_build(oracle, ref):
+    x = _ln_rows(49)
+    rng = np.random.default_rng(50)
+    w = rng.standard_normal(3072).astype(np.float32)
+    b = rng.standard_normal(3072).astype(np.float32)
+    want = ref.layernorm(x, 1e-6, w, b)
+    got = oracle.layernorm(x, 1e-6, w, b)
+    assert_bitexact(got, want, "affine layernorm vs reference build")
+    t = oracle.layernorm(x, 1e-6)  # the no-affine output is t + 0 = fmaf(t, 1, 0)
+    two = (t * w + b).astype(np.float32)  # planted: two roundings
+    assert np.any(bits(two) != bits(got))
