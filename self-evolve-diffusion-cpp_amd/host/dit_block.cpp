@@ -1,6 +1,7 @@
 // sd::gpu::DitBlock — see sd/dit_block.h.
 #include "sd/dit_block.h"
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -106,6 +107,169 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
     check(sdq_ffn(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.h_ffn,
                   io.M, io.gate_ffn, 1, io.hid, io.x, s),
           "DitBlock ffn");
+}
+
+DeviceFloats::DeviceFloats(size_t n) {
+  void* p = nullptr;
+  check(sdq_device_alloc(n * sizeof(float), &p), "DeviceFloats");
+  p_ = static_cast<float*>(p);
+}
+
+DeviceFloats& DeviceFloats::operator=(DeviceFloats&& o) noexcept {
+  if (this != &o) {
+    sdq_device_free(p_);
+    p_ = o.p_;
+    o.p_ = nullptr;
+  }
+  return *this;
+}
+
+DeviceFloats::~DeviceFloats() { sdq_device_free(p_); }
+
+void DitBlock::set_norms(const sd_dit_norms& n) {
+  const float* v[kNorms] = {n.sa_nq, n.sa_nk, n.ca_nq, n.ca_nk, n.ln3_w,
+                            n.ln3_b, n.nk_fusion, n.pnf_w, n.pnf_b};
+  need(v[SA_NQ] && v[SA_NK] && v[CA_NQ] && v[CA_NK], "attention norm weights are required");
+  if (fusion_)
+    need(v[NK_F] && v[PNF_W] && v[PNF_B], "fusion blocks need norm_k_fusion and pre_attn_norm_fusion");
+  else
+    need(v[LN3_W] && v[LN3_B], "norm3 weight and bias are required");
+  std::vector<float> h((size_t)kNorms * dim_, 0.f);
+  for (int i = 0; i < kNorms; i++)
+    if (v[i]) std::copy(v[i], v[i] + dim_, h.begin() + (size_t)i * dim_);
+  DeviceFloats d(h.size());
+  check(sdq_memcpy(d.get(), h.data(), h.size() * sizeof(float), SDQ_H2D, nullptr), "norm upload");
+  check(sdq_stream_sync(nullptr), "norm upload");
+  norms_ = std::move(d);
+}
+
+namespace {
+
+// Workspace carve-up (floats, each region 256-byte aligned): a [M,3dim]
+// (self: q|k|v; cross: q, text attention output, norm3 output or target
+// attention output), att [M,dim], ckv [Mc,2dim], tn [Mt,dim], kvt [Mt,2dim],
+// hid [M,ffn].
+struct Carve {
+  int64_t a, att, ckv, tn, kvt, hid, total;
+};
+
+int64_t up64(int64_t n) { return (n + 63) / 64 * 64; }
+
+Carve carve(int64_t M, int64_t Mc, int64_t Mt, int64_t C, int64_t F, bool fusion) {
+  Carve c{};
+  int64_t o = 0;
+  c.a = o, o += up64(3 * M * C);
+  c.att = o, o += up64(M * C);
+  c.ckv = o, o += up64(2 * Mc * C);
+  c.tn = o, o += fusion ? up64(Mt * C) : 0;
+  c.kvt = o, o += fusion ? up64(2 * Mt * C) : 0;
+  c.hid = o, o += up64(M * F);
+  c.total = o;
+  return c;
+}
+
+}  // namespace
+
+size_t DitBlock::workspace_bytes(int64_t M, int64_t Mc, int64_t Mt) const {
+  return (size_t)carve(M, Mc, Mt, dim_, ffn_, fusion_).total * sizeof(float);
+}
+
+// block_self_fwd (ovi_dit.cpp:205-212) with self_attn_fwd (176-188):
+// q|k|v = mlin(mod_rows(layernorm(x), e0, e1)); rmsnorm + RoPE on q and k;
+// x += o(sdpa(q, k, v)) * e2.
+void DitBlock::self_phase(const sd_dit_block_step& st, float* ws, void* s) const {
+  const int64_t C = dim_, M = st.M;
+  const Carve c = carve(M, st.Mc, st.Mt, C, ffn_, fusion_);
+  float* qkv = ws + c.a;
+  float* att = ws + c.att;
+  sdq_epilogue epi{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
+  check(sdq_qlinear_lnmod(qkv_.handle(), st.x, M, C, st.e, st.e + C, st.eps, &epi, qkv, s),
+        "self q|k|v");
+  check(sdq_rmsnorm_rope(qkv, M, C, 3 * C, norm(SA_NQ), st.eps, st.heads, st.cs, st.nr, s),
+        "self rmsnorm+rope q");
+  check(sdq_rmsnorm_rope(qkv + C, M, C, 3 * C, norm(SA_NK), st.eps, st.heads, st.cs, st.nr, s),
+        "self rmsnorm+rope k");
+  check(sdq_sdpa(qkv, 3 * C, qkv + C, 3 * C, qkv + 2 * C, 3 * C, att, C, M, M, st.heads,
+                 (int)(C / st.heads), s),
+        "self sdpa");
+  o_.forward_device(att, M, SDQ_EPI_GATED, st.e + 2 * C, st.x, st.x, s);
+}
+
+// Non-fusion blocks (block_vanilla_fwd, ovi_dit.cpp:259-268 with
+// cross_text_fwd 191-201): x += o(sdpa(rmsnorm(q(norm3(x))), rmsnorm(k(ctx)),
+// v(ctx))). Fusion blocks (fusion_cross_ffn, 229-256): q on x itself; the
+// text attention uses q unrotated, then q is rotated with this branch's
+// table for the attention on the target's k_fusion (rmsnorm + the target's
+// table) and v_fusion of layernorm(target; pre_attn_norm_fusion); x +=
+// o(text + target attention). Then ffn_fwd (214-222).
+void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) const {
+  const int64_t C = dim_, M = st.M, Mc = st.Mc, Mt = st.Mt;
+  const int hd = (int)(C / st.heads);
+  const Carve c = carve(M, Mc, Mt, C, ffn_, fusion_);
+  float* cq = ws + c.a;
+  float* xt = ws + c.a + M * C;
+  float* aux = ws + c.a + 2 * M * C;  // norm3 output, then the target attention
+  float* ckv = ws + c.ckv;
+  const float* qin = st.x;
+  if (!fusion_) {
+    check(sdq_layernorm(st.x, M, C, norm(LN3_W), norm(LN3_B), st.eps, aux, s), "norm3");
+    qin = aux;
+  }
+  cq_.forward_device(qin, M, SDQ_EPI_NONE, nullptr, nullptr, cq, s);
+  ckv_.forward_device(st.ctx, Mc, SDQ_EPI_NONE, nullptr, nullptr, ckv, s);
+  check(sdq_rmsnorm_rope(cq, M, C, C, norm(CA_NQ), st.eps, st.heads, nullptr, 0, s), "cross norm q");
+  check(sdq_rmsnorm_rope(ckv, Mc, C, 2 * C, norm(CA_NK), st.eps, st.heads, nullptr, 0, s),
+        "cross norm k");
+  check(sdq_sdpa(cq, C, ckv, 2 * C, ckv + C, 2 * C, xt, C, M, Mc, st.heads, hd, s), "text sdpa");
+  if (fusion_) {
+    float* tn = ws + c.tn;
+    float* kvt = ws + c.kvt;
+    check(sdq_layernorm(st.target, Mt, C, norm(PNF_W), norm(PNF_B), st.eps, tn, s),
+          "pre_attn_norm_fusion");
+    kvf_.forward_device(tn, Mt, SDQ_EPI_NONE, nullptr, nullptr, kvt, s);
+    check(sdq_rmsnorm_rope(kvt, Mt, C, 2 * C, norm(NK_F), st.eps, st.heads, st.cs_tgt, st.nr_tgt,
+                           s),
+          "norm_k_fusion + target rope");
+    check(sdq_rmsnorm_rope(cq, M, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
+    check(sdq_sdpa(cq, C, kvt, 2 * C, kvt + C, 2 * C, aux, C, M, Mt, st.heads, hd, s),
+          "target sdpa");
+    check(sdq_add(xt, aux, M * C, s), "text + target");
+  }
+  co_.forward_device(xt, M, SDQ_EPI_RESID, nullptr, st.x, st.x, s);
+  const float* e = st.e;
+  check(sdq_ffn_lnmod(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), st.x,
+                      M, e + 3 * C, e + 4 * C, st.eps, e + 5 * C, 1, ws + c.hid, s),
+        "ffn");
+}
+
+void DitBlock::forward_step(const sd_dit_block_step& st, int phases, void* s) const {
+  need(norms_.get() != nullptr, "norm weights not set (set_norms)");
+  need(phases >= 1 && phases <= 3, "phases must be SD_DIT_SELF, SD_DIT_CROSS_FFN or both");
+  need(st.M >= 0 && st.Mc > 0 && st.Mt >= 0, "row counts (M >= 0, Mc > 0)");
+  need(st.heads > 0 && dim_ % st.heads == 0 && dim_ / st.heads == 128, "head_dim must be 128");
+  need(st.x && st.e, "x and e are required");
+  need(st.ws && st.ws_bytes >= workspace_bytes(st.M, st.Mc, st.Mt), "workspace too small");
+  if (st.M == 0) return;
+  const int64_t hd = dim_ / st.heads;
+  need(!st.cs || (st.nr > 0 && st.nr <= hd / 2), "rope table pairs out of range");
+  float* ws = static_cast<float*>(st.ws);
+  if (phases & SD_DIT_SELF) self_phase(st, ws, s);
+  if (phases & SD_DIT_CROSS_FFN) {
+    need(st.ctx, "ctx is required");
+    if (fusion_) {
+      need(st.target && st.Mt > 0, "fusion blocks need the target tokens");
+      need(!st.cs_tgt || (st.nr_tgt > 0 && st.nr_tgt <= hd / 2), "target rope pairs out of range");
+    }
+    cross_ffn_phase(st, ws, s);
+  }
+}
+
+double DitBlock::step_ops(int64_t M, int64_t Mc, int64_t Mt) const {
+  const double d = (double)dim_;
+  double o = ops(M, Mc, fusion_ ? Mt : 0);
+  o += 4.0 * M * M * d + 4.0 * M * Mc * d;
+  if (fusion_) o += 4.0 * M * Mt * d;
+  return o;
 }
 
 double DitBlock::ops(int64_t M, int64_t Mc, int64_t Mt) const {
@@ -240,6 +404,31 @@ int sd_dit_block_free(sd_dit_block* b) {
 
 double sd_dit_block_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {
   return b ? b->blk.ops(M, Mc, Mt) : 0.0;
+}
+
+int sd_dit_block_set_norms(sd_dit_block* b, const sd_dit_norms* n) {
+  if (!b || !n) {
+    t_dit_err = "sd_dit_block_set_norms: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { b->blk.set_norms(*n); });
+}
+
+size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {
+  return b && M >= 0 && Mc >= 0 && Mt >= 0 ? b->blk.workspace_bytes(M, Mc, Mt) : 0;
+}
+
+int sd_dit_block_step_forward(const sd_dit_block* b, const sd_dit_block_step* st, int phases,
+                              void* stream) {
+  if (!b || !st) {
+    t_dit_err = "sd_dit_block_step_forward: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { b->blk.forward_step(*st, phases, stream); });
+}
+
+double sd_dit_block_step_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {
+  return b ? b->blk.step_ops(M, Mc, Mt) : 0.0;
 }
 
 }  // extern "C"

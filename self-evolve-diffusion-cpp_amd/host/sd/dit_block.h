@@ -74,6 +74,44 @@ typedef struct sd_linear {
 
 typedef struct sd_dit_block sd_dit_block;
 
+// The block's normalization vectors, [dim] F32 host arrays each (copied by
+// sd_dit_block_set_norms). Names of OviDit::load_impl (ovi_dit.cpp:509-537).
+typedef struct sd_dit_norms {
+  const float* sa_nq;      // self_attn.norm_q.weight
+  const float* sa_nk;      // self_attn.norm_k.weight
+  const float* ca_nq;      // cross_attn.norm_q.weight
+  const float* ca_nk;      // cross_attn.norm_k.weight
+  const float* ln3_w;      // norm3.weight   (used by non-fusion blocks)
+  const float* ln3_b;      // norm3.bias
+  const float* nk_fusion;  // cross_attn.norm_k_fusion.weight        (fusion blocks)
+  const float* pnf_w;      // cross_attn.pre_attn_norm_fusion.weight (fusion blocks)
+  const float* pnf_b;      // cross_attn.pre_attn_norm_fusion.bias   (fusion blocks)
+} sd_dit_norms;
+
+// One whole block forward on device arrays (sd_dit_block_step_forward).
+typedef struct sd_dit_block_step {
+  int64_t M;             // tokens of this branch
+  int64_t Mc;            // text context rows (> 0)
+  int64_t Mt;            // target rows (fusion blocks: the other branch)
+  int heads;             // attention heads; head_dim = dim/heads must be 128
+  float eps;             // the reference's kEps (1e-6)
+  float* x;              // [M,dim] residual stream, updated in place
+  const float* ctx;      // [Mc,dim] text context (embed_ctx output)
+  const float* target;   // [Mt,dim] other branch's tokens (fusion blocks)
+  const float* e;        // [6,dim] modulation rows (time rows + ModulationAdd)
+  const float* cs;       // [M,nr,2] RoPE (cos, sin) of this branch (sd_rope_table_*)
+  int nr;                // pairs rotated per head (64 video, 22 audio)
+  const float* cs_tgt;   // [Mt,nr_tgt,2] RoPE table of the target branch (fusion)
+  int nr_tgt;
+  void* ws;              // device workspace, sd_dit_block_workspace_bytes bytes
+  size_t ws_bytes;
+} sd_dit_block_step;
+
+// Phases of sd_dit_block_step_forward: the self-attention branch
+// (block_self_fwd, ovi_dit.cpp:205-212) and the cross attention + FFN
+// (block_vanilla_fwd's rest, 259-268, or fusion_cross_ffn, 229-256).
+enum { SD_DIT_SELF = 1, SD_DIT_CROSS_FFN = 2, SD_DIT_ALL = 3 };
+
 // Order of `lin`: self q, k, v, o; cross q, k, v, o; k_fusion, v_fusion;
 // ffn.0, ffn.2 (the fusion pair is ignored when fusion == 0).
 int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_block** out);
@@ -82,6 +120,21 @@ int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_
 int sd_dit_block_create_many(const sd_linear* lin, int nblocks, int fusion, sd_dit_block** out);
 int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void* stream);
 int sd_dit_block_free(sd_dit_block* b);
+// Copies the block's norm vectors to the device (required before
+// sd_dit_block_step_forward; the fusion ones for fusion blocks, ln3 for others).
+int sd_dit_block_set_norms(sd_dit_block* b, const sd_dit_norms* n);
+// Device workspace bytes that sd_dit_block_step_forward needs for these rows.
+size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
+// The whole block on the GPU, stream-ordered, bit-exact with the reference
+// build except the attention (fp32 MFMA with an online softmax, within 2e-5 of
+// the reference's sdpa); phases = SD_DIT_SELF | SD_DIT_CROSS_FFN. A fusion
+// layer (ovi_dit.cpp:726-734) runs SELF on both branches, then CROSS_FFN of
+// the audio branch (target = video x), then of the video branch with target =
+// a copy of the audio x taken before the audio CROSS_FFN.
+int sd_dit_block_step_forward(const sd_dit_block* b, const sd_dit_block_step* st, int phases,
+                              void* stream);
+// 2*M*N*K of the Linears plus the attention products (4*Lq*Lk*dim per sdpa).
+double sd_dit_block_step_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
 // 2*M*N*K summed over the block's Linears for these row counts.
 double sd_dit_block_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
 // Thread-local text of the last sd_dit_block_* error.
@@ -92,6 +145,23 @@ const char* sd_dit_last_error(void);
 
 namespace sd {
 namespace gpu {
+
+// Owning device array of floats (sdq_device_alloc), move-only.
+class DeviceFloats {
+ public:
+  DeviceFloats() = default;
+  explicit DeviceFloats(size_t n);
+  DeviceFloats(const DeviceFloats&) = delete;
+  DeviceFloats& operator=(const DeviceFloats&) = delete;
+  DeviceFloats(DeviceFloats&& o) noexcept : p_(o.p_) { o.p_ = nullptr; }
+  DeviceFloats& operator=(DeviceFloats&& o) noexcept;
+  ~DeviceFloats();
+  float* get() const { return p_; }
+  explicit operator bool() const { return p_ != nullptr; }
+
+ private:
+  float* p_ = nullptr;
+};
 
 class DitBlock {
  public:
@@ -108,11 +178,21 @@ class DitBlock {
   // Runs the linear stack, stream-ordered (throws std::runtime_error).
   void forward_linears(const sd_dit_block_io& io, void* stream) const;
   double ops(int64_t M, int64_t Mc, int64_t Mt) const;
+  // The whole block (norms, RoPE, attention and Linears) on device arrays.
+  void set_norms(const sd_dit_norms& n);
+  size_t workspace_bytes(int64_t M, int64_t Mc, int64_t Mt) const;
+  void forward_step(const sd_dit_block_step& st, int phases, void* stream) const;
+  double step_ops(int64_t M, int64_t Mc, int64_t Mt) const;
 
  private:
   DitBlock() = default;
   static void check_shapes(const LinearPart* l, bool fusion);
+  enum Norm { SA_NQ, SA_NK, CA_NQ, CA_NK, LN3_W, LN3_B, NK_F, PNF_W, PNF_B, kNorms };
+  const float* norm(Norm n) const { return norms_.get() + n * dim_; }
+  void self_phase(const sd_dit_block_step& st, float* ws, void* s) const;
+  void cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) const;
   QLinear qkv_, o_, cq_, ckv_, kvf_, co_, fc1_, fc2_;
+  DeviceFloats norms_;
   int64_t dim_ = 0, ffn_ = 0;
   bool fusion_ = false;
 };

@@ -375,6 +375,50 @@ class BlockIO(ctypes.Structure):
                 [(n, ctypes.c_void_p) for n in _BLOCK_PTRS] + [("eps", ctypes.c_float)])
 
 
+# fields of sd_dit_norms (host/sd/dit_block.h), in order
+NORM_NAMES = ("sa_nq", "sa_nk", "ca_nq", "ca_nk", "ln3_w", "ln3_b", "nk_fusion", "pnf_w", "pnf_b")
+
+
+class DitNorms(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in NORM_NAMES]
+
+
+class BlockStep(ctypes.Structure):
+    _fields_ = [("M", ctypes.c_int64), ("Mc", ctypes.c_int64), ("Mt", ctypes.c_int64),
+                ("heads", ctypes.c_int), ("eps", ctypes.c_float), ("x", ctypes.c_void_p),
+                ("ctx", ctypes.c_void_p), ("target", ctypes.c_void_p), ("e", ctypes.c_void_p),
+                ("cs", ctypes.c_void_p), ("nr", ctypes.c_int), ("cs_tgt", ctypes.c_void_p),
+                ("nr_tgt", ctypes.c_int), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
+
+
+SELF, CROSS_FFN, ALL = 1, 2, 3
+
+
+def rope_table_3d(T, H, W, head_dim=128, theta=10000.0):
+    """(cos, sin) table [T*H*W, n_rot, 2] of the reference's rope_freqs_3d
+    (host library, sd_rope_table_3d)."""
+    h = load_host_library()
+    nr = h.sd_rope_table_3d(T, H, W, head_dim, theta, None)
+    if nr < 0:
+        raise ValueError("rope_table_3d: bad arguments")
+    cs = np.empty((T * H * W, nr, 2), np.float32)
+    if h.sd_rope_table_3d(T, H, W, head_dim, theta, _ptr(cs)) != nr:
+        raise ValueError("rope_table_3d failed")
+    return cs
+
+
+def rope_table_1d(L, head_dim=128, theta=10000.0, scaling=1.0):
+    """(cos, sin) table [L, n_rot, 2] of the reference's rope_freqs_1d."""
+    h = load_host_library()
+    nr = h.sd_rope_table_1d(L, head_dim, theta, scaling, None)
+    if nr < 0:
+        raise ValueError("rope_table_1d: bad arguments")
+    cs = np.empty((L, nr, 2), np.float32)
+    if h.sd_rope_table_1d(L, head_dim, theta, scaling, _ptr(cs)) != nr:
+        raise ValueError("rope_table_1d failed")
+    return cs
+
+
 def load_host_library(path: str = HOST_LIB_PATH):
     """Load libsd_host.so (raises if it has not been built)."""
     global _host
@@ -394,6 +438,20 @@ def load_host_library(path: str = HOST_LIB_PATH):
                                            ctypes.POINTER(ctypes.c_void_p)]
     h.sd_dit_block_forward.restype = ctypes.c_int
     h.sd_dit_block_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO), ctypes.c_void_p]
+    h.sd_dit_block_set_norms.restype = ctypes.c_int
+    h.sd_dit_block_set_norms.argtypes = [ctypes.c_void_p, ctypes.POINTER(DitNorms)]
+    h.sd_dit_block_workspace_bytes.restype = ctypes.c_size_t
+    h.sd_dit_block_workspace_bytes.argtypes = [ctypes.c_void_p, _i64, _i64, _i64]
+    h.sd_dit_block_step_forward.restype = ctypes.c_int
+    h.sd_dit_block_step_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockStep),
+                                            ctypes.c_int, ctypes.c_void_p]
+    h.sd_dit_block_step_ops.restype = ctypes.c_double
+    h.sd_dit_block_step_ops.argtypes = [ctypes.c_void_p, _i64, _i64, _i64]
+    for f in (h.sd_rope_table_3d, h.sd_rope_table_1d):
+        f.restype = ctypes.c_int
+    h.sd_rope_table_3d.argtypes = [ctypes.c_int] * 4 + [ctypes.c_float, ctypes.c_void_p]
+    h.sd_rope_table_1d.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                   ctypes.c_void_p]
     h.sd_dit_block_free.restype = ctypes.c_int
     h.sd_dit_block_free.argtypes = [ctypes.c_void_p]
     h.sd_dit_block_ops.restype = ctypes.c_double
@@ -483,6 +541,46 @@ class DitBlock:
 
     def ops(self, M, Mc=0, Mt=0) -> float:
         return _host.sd_dit_block_ops(self.h, M, Mc, Mt)
+
+    def set_norms(self, norms: dict):
+        """norms: {NORM_NAMES entry: host float32 [dim]} (sd_dit_block_set_norms)."""
+        n = DitNorms()
+        keep = []
+        for name in NORM_NAMES:
+            a = norms.get(name)
+            if a is not None:
+                a = np.ascontiguousarray(a, np.float32)
+                keep.append(a)
+            setattr(n, name, _ptr(a))
+        _hcheck(_host.sd_dit_block_set_norms(self.h, ctypes.byref(n)))
+
+    def workspace_bytes(self, M, Mc, Mt=0) -> int:
+        return _host.sd_dit_block_workspace_bytes(self.h, M, Mc, Mt)
+
+    def step_ops(self, M, Mc, Mt=0) -> float:
+        return _host.sd_dit_block_step_ops(self.h, M, Mc, Mt)
+
+    def step(self, x, ctx, e, heads, cs=None, target=None, cs_tgt=None, ws=None, phases=ALL,
+             eps=1e-6, stream=None):
+        """The whole block on device tensors (sd_dit_block_step_forward): x
+        [M,dim] in place, ctx [Mc,dim], e [6,dim], cs [M,nr,2] (RoPE table on
+        the device), target [Mt,dim] and cs_tgt for fusion blocks; ws a device
+        byte tensor of workspace_bytes (allocated here when None)."""
+        import torch
+
+        st = BlockStep()
+        st.M, st.Mc = x.shape[0], ctx.shape[0]
+        st.Mt = 0 if target is None else target.shape[0]
+        st.heads, st.eps = heads, eps
+        st.x, st.ctx, st.target, st.e = _ptr(x), _ptr(ctx), _ptr(target), _ptr(e)
+        st.cs, st.nr = _ptr(cs), (0 if cs is None else cs.shape[1])
+        st.cs_tgt, st.nr_tgt = _ptr(cs_tgt), (0 if cs_tgt is None else cs_tgt.shape[1])
+        if ws is None:
+            ws = torch.empty(self.workspace_bytes(st.M, st.Mc, st.Mt), dtype=torch.uint8,
+                             device=x.device)
+        st.ws, st.ws_bytes = _ptr(ws), ws.numel() * ws.element_size()
+        _hcheck(_host.sd_dit_block_step_forward(self.h, ctypes.byref(st), phases, _stream(stream)))
+        return x
 
     def free(self):
         if self.h is not None and self.h.value:

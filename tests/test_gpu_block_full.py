@@ -1,0 +1,150 @@
+"""The whole DiT block on the GPU (sd_dit_block_step_forward: norms,
+modulation, RoPE, attention and the int8 Linears) against the oracle's
+restatement of the reference's block (ovi_dit.cpp:205-268): block_self_fwd,
+then block_vanilla_fwd's cross attention + FFN, or fusion_cross_ffn.
+
+Every step of the oracle chain is pinned to the reference build; the GPU's
+steps are each bit-exact with it except the attention (fp32 MFMA, online
+softmax: within 2e-5 of the output scale) and GELU's tanhf. Those small
+differences move a few int8 rounding decisions in the next Linear's
+activation quantizer, so the block output is checked to a relative tolerance
+(1e-3 of the residual stream's scale); a dropped term, a wrong norm weight,
+a skipped rotation or a swapped operand moves it by far more."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("q", "k", "v", "o", "cq", "ck", "cv", "co", "kf", "vf", "fc1", "fc2")
+
+
+def _weights(oracle, dim, ffn, seed, fusion):
+    lin = {}
+    for i, n in enumerate(NAMES):
+        if n in ("kf", "vf") and not fusion:
+            continue
+        out, inp = (ffn, dim) if n == "fc1" else ((dim, ffn) if n == "fc2" else (dim, dim))
+        W = oracle.randn(out * inp, seed + 10 * i).reshape(out, inp) * np.float32(0.05)
+        q, s = oracle.quant_rows(W)
+        lin[n] = (q, s, oracle.randn(out, seed + 10 * i + 1) * np.float32(0.02))
+    return lin
+
+
+def _norms(oracle, dim, seed):
+    r = lambda k, a, b: (oracle.randu(dim, seed + k) * np.float32(b - a) + np.float32(a))  # noqa
+    return dict(sa_nq=r(1, 0.5, 1.5), sa_nk=r(2, 0.5, 1.5), ca_nq=r(3, 0.5, 1.5),
+                ca_nk=r(4, 0.5, 1.5), ln3_w=r(5, 0.5, 1.5), ln3_b=r(6, -0.2, 0.2),
+                nk_fusion=r(7, 0.5, 1.5), pnf_w=r(8, 0.5, 1.5), pnf_b=r(9, -0.2, 0.2))
+
+
+def _ref_block(o, x, ctx, e, lin, nm, heads, cs, fusion, target=None, cs_tgt=None, phases=3):
+    """ovi_dit.cpp:205-268 on the oracle, step by step."""
+    x = x.copy()
+    C = x.shape[1]
+    L = lambda A, n, **kw: o.linear(A, lin[n][0], lin[n][1], bias=lin[n][2], **kw)  # noqa
+    if phases & 1:  # block_self_fwd + self_attn_fwd
+        h = o.mod_rows(o.layernorm(x, 1e-6), e[0], e[1])
+        q, k, v = L(h, "q"), L(h, "k"), L(h, "v")
+        q, k = o.rmsnorm(q, nm["sa_nq"]), o.rmsnorm(k, nm["sa_nk"])
+        if cs is not None:
+            q, k = o.rope(q, cs, heads), o.rope(k, cs, heads)
+        att = o.sdpa(q, k, v, heads).astype(np.float32)
+        x = L(att, "o", epilogue="gated", gate=e[2], resid=x)
+    if phases & 2:
+        xin = x if fusion else o.layernorm(x, 1e-6, nm["ln3_w"], nm["ln3_b"])
+        q = o.rmsnorm(L(xin, "cq"), nm["ca_nq"])
+        k = o.rmsnorm(L(ctx, "ck"), nm["ca_nk"])
+        xt = o.sdpa(q, k, L(ctx, "cv"), heads).astype(np.float32)
+        if fusion:
+            tn = o.layernorm(target, 1e-6, nm["pnf_w"], nm["pnf_b"])
+            kt = o.rmsnorm(L(tn, "kf"), nm["nk_fusion"])
+            if cs is not None:
+                q = o.rope(q, cs, heads)
+            if cs_tgt is not None:
+                kt = o.rope(kt, cs_tgt, heads)
+            xt = o.add(xt, o.sdpa(q, kt, L(tn, "vf"), heads).astype(np.float32))
+        x = L(xt, "co", epilogue="resid", resid=x)
+        h = o.mod_rows(o.layernorm(x, 1e-6), e[3], e[4])
+        x = L(o.gelu_tanh(L(h, "fc1")), "fc2", epilogue="gated", gate=e[5], resid=x)
+    return x
+
+
+def _case(sdq_dev, oracle, dim, ffn, heads, M, Mc, Mt, fusion, rope, seed, phases=3):
+    import torch
+
+    import sdq
+
+    print(f"[block-full] dim={dim} ffn={ffn} M={M} Mc={Mc} Mt={Mt} fusion={fusion} "
+          f"rope={rope} phases={phases}", flush=True)
+    lin = _weights(oracle, dim, ffn, seed, fusion)
+    nm = _norms(oracle, dim, seed + 500)
+    x = oracle.randn(M * dim, seed + 1).reshape(M, dim)
+    ctx = oracle.randn(Mc * dim, seed + 2).reshape(Mc, dim)
+    e = (oracle.randn(6 * dim, seed + 3).reshape(6, dim) * np.float32(0.3)).astype(np.float32)
+    target = oracle.randn(Mt * dim, seed + 4).reshape(Mt, dim) if fusion else None
+    if rope == "3d":
+        cs = sdq.rope_table_3d(1, M // 4, 4)[:M] if M % 4 == 0 else sdq.rope_table_1d(M)
+        cs_t = sdq.rope_table_1d(Mt, 128, 10000.0, 0.19676) if fusion else None
+    else:
+        cs, cs_t = None, None
+    want = _ref_block(oracle, x, ctx, e, lin, nm, heads, cs, fusion, target, cs_t, phases)
+
+    blk = sdq.DitBlock(lin, fusion)
+    blk.set_norms(nm)
+    dv = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(sdq_dev)  # noqa
+    xd = dv(x)
+    blk.step(xd, dv(ctx), dv(e), heads, cs=dv(cs), target=dv(target), cs_tgt=dv(cs_t),
+             phases=phases)
+    torch.cuda.synchronize()
+    got = xd.cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got.astype(np.float64) - want) / (np.abs(want).max() + 1e-30)
+    print(f"  max rel err {err.max():.3e}", flush=True)
+    assert err.max() <= 1e-3, float(err.max())
+    assert np.abs(want - x).max() > 0.05 * np.abs(want).max()  # x moved far beyond the tolerance
+    blk.free()
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+def test_block_small(sdq_dev, oracle, fusion):
+    _case(sdq_dev, oracle, 256, 512, 2, 100, 37, 60, fusion, "3d", 11 + fusion)
+
+
+@pytest.mark.parametrize("phases", [1, 2])
+def test_block_phases(sdq_dev, oracle, phases):
+    _case(sdq_dev, oracle, 256, 512, 2, 64, 20, 33, True, "3d", 40 + phases, phases)
+
+
+def test_block_no_rope_ragged(sdq_dev, oracle):
+    _case(sdq_dev, oracle, 384, 768, 3, 77, 5, 0, False, "none", 61)
+
+
+def test_block_real_width(sdq_dev, oracle):
+    """dim 3072, ffn 14336, 24 heads (the Wan2.2 5B width), audio-sized rows
+    against video-sized fusion target."""
+    _case(sdq_dev, oracle, 3072, 14336, 24, 157, 64, 300, True, "3d", 71)
+
+
+def test_block_step_errors(sdq_dev, oracle):
+    import torch
+
+    import sdq
+
+    lin = _weights(oracle, 256, 512, 5, False)
+    blk = sdq.DitBlock(lin, False)
+    x = torch.zeros((8, 256), device=sdq_dev)
+    ctx = torch.zeros((4, 256), device=sdq_dev)
+    e = torch.zeros((6, 256), device=sdq_dev)
+    with pytest.raises(RuntimeError, match="norm weights not set"):
+        blk.step(x, ctx, e, 2)
+    nm = _norms(oracle, 256, 9)
+    blk.set_norms(nm)
+    with pytest.raises(RuntimeError, match="head_dim must be 128"):
+        blk.step(x, ctx, e, 4)
+    small = torch.empty(16, dtype=torch.uint8, device=sdq_dev)
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        blk.step(x, ctx, e, 2, ws=small)
+    bad = dict(nm)
+    bad.pop("ln3_b")
+    with pytest.raises(RuntimeError, match="norm3"):
+        blk.set_norms(bad)

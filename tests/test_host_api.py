@@ -183,3 +183,30 @@ def test_qlinear_from_pack(tmp_path, sdq_dev, oracle, mode):
     else:
         want = oracle.linear(x, q, s, bias=bias, epilogue="gelu")
         assert np.all(np.abs(got - want) <= 1e-6 * (1 + np.abs(want)))
+
+
+@pytest.mark.parametrize("grid", [(1, 1, 1), (3, 4, 5), (31, 45, 80)])
+def test_rope_table_3d_matches_oracle(oracle, grid):
+    """The host library's RoPE (cos, sin) table equals cosf/sinf of the
+    oracle's rope_freqs_3d angles (both pinned to the reference build's
+    rope_freqs_3d and apply_rope), bit for bit; 31x45x80 is the 720p/121-frame
+    token grid."""
+    import sdq
+
+    T, H, W = grid
+    cs = sdq.rope_table_3d(T, H, W)
+    want = oracle.rope_cs(oracle.rope_freqs_3d(T, H, W, 128, 10000.0))
+    assert cs.shape == (T * H * W, 64, 2)
+    assert np.array_equal(cs.view(np.uint32), want.reshape(cs.shape).view(np.uint32))
+
+
+@pytest.mark.parametrize("L,scaling", [(157, 0.19676), (1000, 1.0)])
+def test_rope_table_1d_matches_oracle(oracle, L, scaling):
+    import sdq
+
+    cs = sdq.rope_table_1d(L, 128, 10000.0, scaling)
+    want = oracle.rope_cs(oracle.rope_freqs_1d(L, 128, 10000.0, scaling))
+    assert cs.shape == (L, 22, 2)
+    assert np.array_equal(cs.view(np.uint32), want.reshape(cs.shape).view(np.uint32))
+    with pytest.raises(ValueError):
+        sdq.rope_table_1d(L, 127)
