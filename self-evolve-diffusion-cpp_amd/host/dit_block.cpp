@@ -230,7 +230,8 @@ void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) 
     check(sdq_rmsnorm_rope(kvt, Mt, C, 2 * C, norm(NK_F), st.eps, st.heads, st.cs_tgt, st.nr_tgt,
                            s),
           "norm_k_fusion + target rope");
-    check(sdq_rmsnorm_rope(cq, M, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
+    if (st.cs)
+      check(sdq_rmsnorm_rope(cq, M, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
     check(sdq_sdpa(cq, C, kvt, 2 * C, kvt + C, 2 * C, aux, C, M, Mt, st.heads, hd, s),
           "target sdpa");
     check(sdq_add(xt, aux, M * C, s), "text + target");
