@@ -162,12 +162,32 @@ def bench_block(torch, sdq, args):
     fn_ln = lambda: blk.forward(**io, **mods, eps=1e-6)  # noqa: E731
     ms_ln = _timed(torch, fn_ln, max(args.warmup // 5, 2), max(args.steps // 10, 3))
     split_ln = _kernel_split(sdq, fn_ln, 2)
+    # the whole block (sd_dit_block_step_forward): norms, RoPE (31x22x40 token
+    # grid), the three attentions and the Linears, audio rows as fusion target
+    import numpy as np
+
+    norms = {n: np.ones(dim, np.float32) for n in sdq.NORM_NAMES}
+    blk.set_norms(norms)
+    heads = dim // 128
+    cs = torch.from_numpy(sdq.rope_table_3d(31, 22, 40)).to(dev)
+    cs_a = torch.from_numpy(sdq.rope_table_1d(Mt, 128, 10000.0, 0.19676)).to(dev)
+    e6 = torch.randn((6, dim), device=dev) * 0.3
+    ws = torch.empty(blk.workspace_bytes(M, Mc, Mt), dtype=torch.uint8, device=dev)
+    xf = torch.randn((M, dim), device=dev)
+    fn_full = lambda: blk.step(xf, io["ctx"], e6, heads, cs=cs, target=io["tn"][:Mt],  # noqa: E731
+                               cs_tgt=cs_a, ws=ws)
+    ms_full = _timed(torch, fn_full, 1, 3)
+    split_full = _kernel_split(sdq, fn_full, 1)
+    ops_full = blk.step_ops(M, Mc, Mt)
     return {"metric": "DiT block int8 linear stack (config 3), TOPS", "value": round(ops / ms / 1e9, 2),
             "unit": "TOPS", "ms_per_block": round(ms, 4), "ops": ops, "dtype": "int8",
             "config": {"workload": "DiT block linears M=27280 dim=3072 ffn=14336 ctx=512 "
                                    "fusion=157", "kernel_ms_per_block": split,
                        "ms_per_block_norms_folded": round(ms_ln, 4),
-                       "kernel_ms_per_block_norms_folded": split_ln}}
+                       "kernel_ms_per_block_norms_folded": split_ln,
+                       "ms_per_block_full": round(ms_full, 3),
+                       "ops_block_full": ops_full,
+                       "kernel_ms_per_block_full": split_full}}
 
 
 def bench_ffn(torch, sdq, args):
