@@ -322,6 +322,59 @@ def bench_twin(torch, sdq, args):
                                       "weight_GB": round(lw / 1e9, 3),
                                       "weight_stream_GBps": round(lw / ms / 1e6, 1),
                                       "repack_ms_total": round(t_repack * 1e3, 1)}
+    # The whole twin backbone on the GPU (sd_dit_block_step_forward): norms,
+    # RoPE, the attentions and the Linears of every layer, in the order of a
+    # fusion layer (ovi_dit.cpp:726-734): both self phases (two streams),
+    # snapshots of both branches, then both cross+FFN phases, each reading
+    # the other's snapshot (two streams). 30 layers.
+    import numpy as np
+
+    layers = 30
+    heads = dim // 128
+    ones = {n: np.ones(dim, np.float32) for n in sdq.NORM_NAMES}
+    for b in blocks[:2 * layers]:
+        b.set_norms(ones)
+    cs_v = torch.from_numpy(sdq.rope_table_3d(3, 16, 16)).to(dev)  # 768 video tokens
+    cs_a = torch.from_numpy(sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)).to(dev)
+    xv, xa = torch.randn((Mv, dim), device=dev), torch.randn((Ma, dim), device=dev)
+    og_v, og_a = torch.empty_like(xv), torch.empty_like(xa)
+    ctx_v, ctx_a = torch.randn((Mc, dim), device=dev), torch.randn((Mc, dim), device=dev)
+    e_v = [torch.randn((6, dim), device=dev) * 0.1 for _ in range(layers)]
+    e_a = [torch.randn((6, dim), device=dev) * 0.1 for _ in range(layers)]
+    ws_v = torch.empty(blocks[0].workspace_bytes(Mv, Mc, Ma), dtype=torch.uint8, device=dev)
+    ws_a = torch.empty(blocks[1].workspace_bytes(Ma, Mc, Mv), dtype=torch.uint8, device=dev)
+
+    def fn_full():
+        cur = torch.cuda.current_stream()
+        sv.wait_stream(cur)
+        sa.wait_stream(cur)
+        for i in range(layers):
+            bv, ba = blocks[2 * i], blocks[2 * i + 1]
+            ba.step(xa, ctx_a, e_a[i], heads, cs=cs_a, ws=ws_a, phases=sdq.SELF,
+                    stream=sa.cuda_stream)
+            bv.step(xv, ctx_v, e_v[i], heads, cs=cs_v, ws=ws_v, phases=sdq.SELF,
+                    stream=sv.cuda_stream)
+            with torch.cuda.stream(sa):
+                og_a.copy_(xa)
+            with torch.cuda.stream(sv):
+                og_v.copy_(xv)
+            sv.wait_stream(sa)
+            sa.wait_stream(sv)
+            ba.step(xa, ctx_a, e_a[i], heads, cs=cs_a, target=og_v, cs_tgt=cs_v, ws=ws_a,
+                    phases=sdq.CROSS_FFN, stream=sa.cuda_stream)
+            bv.step(xv, ctx_v, e_v[i], heads, cs=cs_v, target=og_a, cs_tgt=cs_a, ws=ws_v,
+                    phases=sdq.CROSS_FFN, stream=sv.cuda_stream)
+            sv.wait_stream(sa)
+            sa.wait_stream(sv)
+        cur.wait_stream(sv)
+        cur.wait_stream(sa)
+    ms_full = _timed(torch, fn_full, 2, max(args.steps // 10, 3))
+    assert bool(torch.isfinite(xv).all()) and bool(torch.isfinite(xa).all())
+    ops_full = sum(blocks[2 * i].step_ops(Mv, Mc, Ma) + blocks[2 * i + 1].step_ops(Ma, Mc, Mv)
+                   for i in range(layers))
+    res["whole_blocks_30"] = {"ms_per_pass": round(ms_full, 4),
+                              "TFLOPs": round(ops_full / ms_full / 1e9, 2),
+                              "kernel_ms_per_pass": _kernel_split(sdq, fn_full, 1)}
     # CFG batching (denoise.cpp:95-98 runs the conditional and unconditional
     # forwards one after the other): both forwards' rows stacked, 2M tokens
     # and 2 text contexts per Linear, one weight stream for the pair
@@ -410,13 +463,23 @@ def cpu_baseline(args, K, N):
         q, s = pyoracle.quant_rows(W)
         cores = pyoracle.nthreads_default()
         fn, kind = (lambda: pyoracle.qgemm(A, q, s, cores)), "port"
-    fn()
-    best = 1e30
-    for _ in range(3):
-        t0 = time.perf_counter()
+    def best_of_3():
         fn()
-        best = min(best, time.perf_counter() - t0)
+        best = 1e30
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t0)
+        return best
+
+    best = best_of_3()
     tops = 2.0 * rows * K * N / best / 1e12
+    # the same at 8 threads, the thread count of the reference's own figures
+    tops8 = None
+    if kind == "reference" and int(cores) != 8:
+        ref.set_nthreads(8)
+        tops8 = round(2.0 * rows * K * N / best_of_3() / 1e12, 5)
+        ref.set_nthreads(int(cores))
     cpu = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -427,6 +490,7 @@ def cpu_baseline(args, K, N):
     except OSError:
         pass
     return {"value": round(tops, 5), "unit": "TOPS", "cores": int(cores), "kind": kind,
+            "value_8_threads": tops8,
             "sample": f"M={rows} rows of the {args.M}x{K}x{N} qgemm (same K,N; M>=2048 keeps "
                       f"the reference's widened-s16 path), best of 3 after 1 warmup, "
                       f"{best * 1e3:.1f} ms/call, host CPU: {cpu}"}

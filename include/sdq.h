@@ -179,6 +179,22 @@ int sdq_ffn_lnmod(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2,
 int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
                      int heads, const float* cs, int nr, void* stream);
 
+/* Several column blocks in one call, e.g. the q and k blocks of q|k|v with
+ * their own weights, or cross q, context k and fusion k: the same as
+ * sdq_rmsnorm_rope on each, but their serial row sums run side by side in one
+ * launch. Segments with L = 0 are skipped. */
+typedef struct sdq_rms_seg {
+  float* x;        /* first column of the block, rows of stride ld */
+  int64_t L;       /* rows */
+  int64_t ld;      /* row stride (floats), >= C */
+  const float* w;  /* [C] rmsnorm weight, or NULL: rotation only */
+  const float* cs; /* [L, nr, 2] (cos, sin) table, or NULL: no rotation */
+  int nr;          /* pairs rotated per head */
+} sdq_rms_seg;
+#define SDQ_MAX_RMS_SEGS 4
+int sdq_rmsnorm_rope_batch(const sdq_rms_seg* segs, int nseg, int64_t C, int heads, float eps,
+                           void* stream);
+
 /* blk::layernorm (src/model/blocks.cpp:18-43) on the GPU, bit-exact with the
  * reference build: y = fmaf(fl((x - mu)*inv), w, b) with serial-sum row
  * statistics; w, b nullable (1, 0). x, y [M,K] contiguous device arrays

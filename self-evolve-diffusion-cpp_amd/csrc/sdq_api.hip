@@ -675,26 +675,45 @@ int sdq_qlinear_lnmod(const sdq_weight* w, const float* x, int64_t M, int64_t K,
                         &lm);
 }
 
-int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
-                     int heads, const float* cs, int nr, void* stream) {
-  if (L < 0) return set_error(SDQ_ERR_INVALID, "negative L");
-  if (L == 0) return SDQ_OK;
-  if (!x) return set_error(SDQ_ERR_INVALID, "null x");
-  if (!w && (nr <= 0 || !cs)) return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: nothing to do");
-  if (C <= 0 || ld < C || heads <= 0 || C % heads != 0 || (C / heads) % 2 != 0)
-    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need C > 0, ld >= C, C = heads * even head_dim");
-  if (nr < 0 || nr > C / heads / 2 || (nr > 0 && !cs))
-    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need 0 <= nr <= head_dim/2 and a table");
+int sdq_rmsnorm_rope_batch(const sdq_rms_seg* segs, int nseg, int64_t C, int heads, float eps,
+                           void* stream) {
+  if (nseg < 0 || nseg > SDQ_MAX_RMS_SEGS || (nseg > 0 && !segs))
+    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: 0 to 4 segments");
+  if (C <= 0 || heads <= 0 || C % heads != 0 || (C / heads) % 2 != 0)
+    return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need C > 0, C = heads * even head_dim");
+  RmsSeg g[SDQ_MAX_RMS_SEGS];
+  int n = 0;
+  int64_t rows_w = 0;
+  for (int i = 0; i < nseg; i++) {
+    const sdq_rms_seg& a = segs[i];
+    if (a.L < 0) return set_error(SDQ_ERR_INVALID, "negative L");
+    if (a.L == 0) continue;
+    if (!a.x) return set_error(SDQ_ERR_INVALID, "null x");
+    if (!a.w && (a.nr <= 0 || !a.cs))
+      return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: nothing to do");
+    if (a.ld < C) return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need ld >= C");
+    if (a.nr < 0 || a.nr > C / heads / 2 || (a.nr > 0 && !a.cs))
+      return set_error(SDQ_ERR_INVALID, "rmsnorm_rope: need 0 <= nr <= head_dim/2 and a table");
+    g[n++] = RmsSeg{a.x, a.L, a.ld, a.w, a.nr > 0 ? a.cs : nullptr, a.nr, nullptr};
+    if (a.w) rows_w += a.L;
+  }
+  if (n == 0) return SDQ_OK;
   int dev = -1;
   int rc = current_device(&dev);
   if (rc) return rc;
   if ((rc = ensure_device(dev))) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   float* inv = nullptr;
-  if (w && (rc = ws_floats(dev, s, &Workspace::rinv, &Workspace::rinv_bytes, (size_t)L * 4, &inv)))
+  if (rows_w > 0 &&
+      (rc = ws_floats(dev, s, &Workspace::rinv, &Workspace::rinv_bytes, (size_t)rows_w * 4, &inv)))
     return rc;
+  for (int i = 0; i < n; i++)
+    if (g[i].w) {
+      g[i].inv = inv;
+      inv += g[i].L;
+    }
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_rmsnorm_rope(x, L, C, ld, w, eps, heads, nr > 0 ? cs : nullptr, nr, inv, s);
+  hipError_t e = launch_rmsnorm_rope_segs(g, n, C, heads, eps, s);
   if (e != hipSuccess) return hip_error(e, "rmsnorm_rope launch");
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);
@@ -706,6 +725,12 @@ int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
     }
   }
   return SDQ_OK;
+}
+
+int sdq_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w, float eps,
+                     int heads, const float* cs, int nr, void* stream) {
+  const sdq_rms_seg g{x, L, ld, w, cs, nr};
+  return sdq_rmsnorm_rope_batch(&g, 1, C, heads, eps, stream);
 }
 
 int sdq_layernorm(const float* x, int64_t M, int64_t K, const float* w, const float* b, float eps,

@@ -10,6 +10,9 @@
 // the host with the reference's own libm calls (apply_rope evaluates
 // std::cos / std::sin of float angles).
 #include "sdq_internal.h"
+
+#include <cstdlib>
+#include <type_traits>
 #include "sdq_rowsum.h"
 
 #pragma clang fp contract(off)
@@ -21,45 +24,65 @@ using rowsum::kLnDepthFew;
 using rowsum::kLnDepthMany;
 using rowsum::ln_pass;
 
+// Up to kMaxRmsSegs column blocks of strided rows in one launch (e.g. the q
+// and k blocks of q|k|v, or cross q, context k and fusion k): their serial
+// row sums run side by side instead of one chain after the other.
+struct RmsSegs {
+  RmsSeg s[kMaxRmsSegs];
+  int64_t blk0[kMaxRmsSegs + 1];   // first stats block (8 rows each) of segment i
+  int64_t item0[kMaxRmsSegs + 1];  // first apply item (one pair each) of segment i
+  int n;
+};
+
+__device__ __forceinline__ int seg_of(const int64_t* start, int n, int64_t v) {
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxRmsSegs; k++)
+    if (k < n && v >= start[k]) i = k;
+  return i;
+}
+
 // inv[row] = 1/sqrtf(sum_k fl(x[row,k]^2)/C + eps), rows of stride ld.
 template <bool VEC, int D>
 __global__ void __launch_bounds__(64)
-rms_stats_kernel(const float* __restrict__ x, int64_t L, int64_t C, int64_t ld, float eps,
-                 float* __restrict__ inv) {
+rms_stats_kernel(RmsSegs sg, int64_t C, float eps) {
   __shared__ float4 tb[2][64];
   const int l = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.x * 8 + (l & 7);
-  const bool ok = row < L;
-  const float* r = x + (ok ? row : 0) * ld;
+  const int i = seg_of(sg.blk0, sg.n, (int64_t)blockIdx.x);
+  const RmsSeg& g = sg.s[i];
+  const int64_t row = ((int64_t)blockIdx.x - sg.blk0[i]) * 8 + (l & 7);
+  const bool ok = row < g.L;
+  const float* r = g.x + (ok ? row : 0) * g.ld;
   const float ss = ln_pass<VEC, 2, D>(r, C, l, tb, 0.f);
   if (l < 8 && ok) {
     const float den = ss / (float)C + eps;
-    inv[row] = 1.f / sqrtf(den);
+    g.inv[row] = 1.f / sqrtf(den);
   }
 }
 
 // y = fl(fl(v*inv)*w) over the row, then the rotation of each head's first
 // nr pairs. One thread per pair; pairs never straddle heads (hd is even).
 __global__ void __launch_bounds__(256)
-rms_rope_apply_kernel(float* __restrict__ x, int64_t L, int64_t C, int64_t ld,
-                      const float* __restrict__ w, const float* __restrict__ inv,
-                      const float2* __restrict__ cs, int nr, int hd) {
+rms_rope_apply_kernel(RmsSegs sg, int64_t C, int hd) {
   const int64_t np = C / 2;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= L * np) return;
-  const int64_t row = idx / np, p = idx - row * np;
+  if (idx >= sg.item0[sg.n]) return;
+  const int i = seg_of(sg.item0, sg.n, idx);
+  const RmsSeg& g = sg.s[i];
+  const int64_t it = idx - sg.item0[i];
+  const int64_t row = it / np, p = it - row * np;
   const int64_t c0 = 2 * p;
-  float* q = x + row * ld + c0;
+  float* q = g.x + row * g.ld + c0;
   float y0 = q[0], y1 = q[1];
-  if (w) {
-    const float iv = inv[row];
+  if (g.w) {
+    const float iv = g.inv[row];
     const float a = y0 * iv, b = y1 * iv;
-    y0 = a * w[c0];
-    y1 = b * w[c0 + 1];
+    y0 = a * g.w[c0];
+    y1 = b * g.w[c0 + 1];
   }
   const int j = (int)(c0 % hd) / 2;  // pair index inside the head
-  if (cs && j < nr) {
-    const float2 t = cs[row * nr + j];  // (cos, sin)
+  if (g.cs && j < g.nr) {
+    const float2 t = reinterpret_cast<const float2*>(g.cs)[row * g.nr + j];  // (cos, sin)
     const float r1s = y1 * t.y, r1c = y1 * t.x;
     const float n0 = __builtin_fmaf(y0, t.x, -r1s);
     const float n1 = __builtin_fmaf(y0, t.y, r1c);
@@ -74,32 +97,52 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+hipError_t launch_rmsnorm_rope_segs(const RmsSeg* segs, int nseg, int64_t C, int heads, float eps,
+                                    hipStream_t s) {
+  if (nseg < 1 || nseg > kMaxRmsSegs || C <= 0 || heads <= 0 || C % heads || (C / heads) % 2)
+    return hipErrorInvalidValue;
+  RmsSegs st{};
+  st.n = nseg;
+  bool vec = C % 4 == 0, few = true, any_w = false;
+  for (int i = 0; i < nseg; i++) {
+    const RmsSeg& g = segs[i];
+    if (g.L < 0 || g.ld < C || g.nr < 0 || g.nr > C / heads / 2 || (!g.w && !g.cs) ||
+        (g.w && !g.inv) || (g.L > 0 && !g.x))
+      return hipErrorInvalidValue;
+    st.s[i] = g;
+    st.blk0[i + 1] = st.blk0[i] + (g.w ? ceil_div(g.L, 8) : 0);
+    st.item0[i + 1] = st.item0[i] + g.L * (C / 2);
+    vec = vec && aligned16(g.x) && g.ld % 4 == 0;
+    few = few && g.L <= 4096;
+    any_w = any_w || (g.w && g.L > 0);
+  }
+  // segments without a weight (rotation only) own no stats blocks
+  if (any_w) {
+    const dim3 g((unsigned)st.blk0[nseg]), b(64);
+    if (vec && few)
+      hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthFew>), g, b, 0, s, st, C, eps);
+    else if (vec)
+      hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthMany>), g, b, 0, s, st, C, eps);
+    else if (few)
+      hipLaunchKernelGGL((rms_stats_kernel<false, kLnDepthFew>), g, b, 0, s, st, C, eps);
+    else
+      hipLaunchKernelGGL((rms_stats_kernel<false, kLnDepthMany>), g, b, 0, s, st, C, eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int64_t items = st.item0[nseg];
+  if (items == 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_rope_apply_kernel, dim3((unsigned)ceil_div(items, 256)), dim3(256), 0, s,
+                     st, C, (int)(C / heads));
+  return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
                                float eps, int heads, const float* cs, int nr, float* inv,
                                hipStream_t s) {
   if (L <= 0) return hipSuccess;
-  if (C <= 0 || ld < C || heads <= 0 || C % heads || (C / heads) % 2 || nr < 0 ||
-      nr > C / heads / 2 || (!w && !cs) || (w && !inv))
-    return hipErrorInvalidValue;
-  const bool vec = aligned16(x) && ld % 4 == 0 && C % 4 == 0, few = L <= 4096;
-  const dim3 g((unsigned)ceil_div(L, 8)), b(64);
-  if (!w) {
-    // rotation only
-  } else if (vec && few)
-    hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthFew>), g, b, 0, s, x, L, C, ld, eps, inv);
-  else if (vec)
-    hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthMany>), g, b, 0, s, x, L, C, ld, eps, inv);
-  else if (few)
-    hipLaunchKernelGGL((rms_stats_kernel<false, kLnDepthFew>), g, b, 0, s, x, L, C, ld, eps, inv);
-  else
-    hipLaunchKernelGGL((rms_stats_kernel<false, kLnDepthMany>), g, b, 0, s, x, L, C, ld, eps, inv);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int64_t items = L * (C / 2);
-  hipLaunchKernelGGL(rms_rope_apply_kernel, dim3((unsigned)ceil_div(items, 256)), dim3(256), 0, s,
-                     x, L, C, ld, w, inv, reinterpret_cast<const float2*>(cs), nr,
-                     (int)(C / heads));
-  return hipGetLastError();
+  const RmsSeg g{x, L, ld, w, cs, nr, inv};
+  return launch_rmsnorm_rope_segs(&g, 1, C, heads, eps, s);
 }
 
 
@@ -354,17 +397,25 @@ hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk,
   if (Lq <= 0) return hipSuccess;
   if (Lk <= 0 || heads <= 0) return hipErrorInvalidValue;
   const float scale_log2e = (1.f / sqrtf((float)kHd)) * 1.4426950408889634f;
-  if (Lq >= 1024) {
-    constexpr int NW = 8;
+  // waves per workgroup (32 queries each); SDQ_SDPA_NW = 2, 4 or 8 overrides
+  static const int forced = [] {
+    const char* e = getenv("SDQ_SDPA_NW");
+    const int v = e ? atoi(e) : 0;
+    return v == 2 || v == 4 || v == 8 ? v : 0;
+  }();
+  const int nw = forced ? forced : Lq >= 1024 ? 8 : 2;
+  auto go = [&](auto nwc) {
+    constexpr int NW = decltype(nwc)::value;
     const int qgroups = (int)ceil_div(Lq, 32 * NW);
     hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads)), dim3(NW * 64), 0, s, q,
                        ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups, scale_log2e);
-  } else {
-    constexpr int NW = 2;
-    const int qgroups = (int)ceil_div(Lq, 32 * NW);
-    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads)), dim3(NW * 64), 0, s, q,
-                       ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups, scale_log2e);
-  }
+  };
+  if (nw == 8)
+    go(std::integral_constant<int, 8>{});
+  else if (nw == 4)
+    go(std::integral_constant<int, 4>{});
+  else
+    go(std::integral_constant<int, 2>{});
   return hipGetLastError();
 }
 

@@ -95,6 +95,20 @@ hipError_t launch_act_quant_frags_lnmod(const float* A, int64_t M, int64_t K, in
 // In place on L rows of stride ld (C columns): rmsnorm with weight w (w ==
 // nullptr: none), then RoPE of each head's first nr pairs with the (cos, sin)
 // table cs [L][nr] (cs == nullptr: no RoPE). inv: [L] scratch.
+// One column block of strided rows for launch_rmsnorm_rope_segs: L rows of
+// stride ld at x; w NULL = rotation only; cs NULL / nr 0 = no rotation; inv
+// [L] floats of scratch when w is set.
+struct RmsSeg {
+  float* x;
+  int64_t L, ld;
+  const float* w;
+  const float* cs;
+  int nr;
+  float* inv;
+};
+constexpr int kMaxRmsSegs = 4;
+hipError_t launch_rmsnorm_rope_segs(const RmsSeg* segs, int nseg, int64_t C, int heads, float eps,
+                                    hipStream_t s);
 hipError_t launch_rmsnorm_rope(float* x, int64_t L, int64_t C, int64_t ld, const float* w,
                                float eps, int heads, const float* cs, int nr, float* inv,
                                hipStream_t s);

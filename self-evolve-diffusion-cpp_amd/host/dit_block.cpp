@@ -185,10 +185,11 @@ void DitBlock::self_phase(const sd_dit_block_step& st, float* ws, void* s) const
   sdq_epilogue epi{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
   check(sdq_qlinear_lnmod(qkv_.handle(), st.x, M, C, st.e, st.e + C, st.eps, &epi, qkv, s),
         "self q|k|v");
-  check(sdq_rmsnorm_rope(qkv, M, C, 3 * C, norm(SA_NQ), st.eps, st.heads, st.cs, st.nr, s),
-        "self rmsnorm+rope q");
-  check(sdq_rmsnorm_rope(qkv + C, M, C, 3 * C, norm(SA_NK), st.eps, st.heads, st.cs, st.nr, s),
-        "self rmsnorm+rope k");
+  // q and k norms (+ RoPE) in one launch: two independent serial row-sum sets
+  const int nr = st.cs ? st.nr : 0;
+  const sdq_rms_seg qk[2] = {{qkv, M, 3 * C, norm(SA_NQ), st.cs, nr},
+                             {qkv + C, M, 3 * C, norm(SA_NK), st.cs, nr}};
+  check(sdq_rmsnorm_rope_batch(qk, 2, C, st.heads, st.eps, s), "self rmsnorm+rope q, k");
   check(sdq_sdpa(qkv, 3 * C, qkv + C, 3 * C, qkv + 2 * C, 3 * C, att, C, M, M, st.heads,
                  (int)(C / st.heads), s),
         "self sdpa");
@@ -217,19 +218,21 @@ void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) 
   }
   cq_.forward_device(qin, M, SDQ_EPI_NONE, nullptr, nullptr, cq, s);
   ckv_.forward_device(st.ctx, Mc, SDQ_EPI_NONE, nullptr, nullptr, ckv, s);
-  check(sdq_rmsnorm_rope(cq, M, C, C, norm(CA_NQ), st.eps, st.heads, nullptr, 0, s), "cross norm q");
-  check(sdq_rmsnorm_rope(ckv, Mc, C, 2 * C, norm(CA_NK), st.eps, st.heads, nullptr, 0, s),
-        "cross norm k");
-  check(sdq_sdpa(cq, C, ckv, 2 * C, ckv + C, 2 * C, xt, C, M, Mc, st.heads, hd, s), "text sdpa");
-  if (fusion_) {
+  float* kvt = ws + c.kvt;
+  if (fusion_) {  // the target's k|v first, so the three norms share one launch
     float* tn = ws + c.tn;
-    float* kvt = ws + c.kvt;
     check(sdq_layernorm(st.target, Mt, C, norm(PNF_W), norm(PNF_B), st.eps, tn, s),
           "pre_attn_norm_fusion");
     kvf_.forward_device(tn, Mt, SDQ_EPI_NONE, nullptr, nullptr, kvt, s);
-    check(sdq_rmsnorm_rope(kvt, Mt, C, 2 * C, norm(NK_F), st.eps, st.heads, st.cs_tgt, st.nr_tgt,
-                           s),
-          "norm_k_fusion + target rope");
+  }
+  // rmsnorm of cross q and context k (no rotation); fusion: rmsnorm_k_fusion
+  // + the target's rotation of k_fusion. Independent row sets, one launch.
+  const sdq_rms_seg nk[3] = {{cq, M, C, norm(CA_NQ), nullptr, 0},
+                             {ckv, Mc, 2 * C, norm(CA_NK), nullptr, 0},
+                             {kvt, Mt, 2 * C, norm(NK_F), st.cs_tgt, st.cs_tgt ? st.nr_tgt : 0}};
+  check(sdq_rmsnorm_rope_batch(nk, fusion_ ? 3 : 2, C, st.heads, st.eps, s), "cross norms");
+  check(sdq_sdpa(cq, C, ckv, 2 * C, ckv + C, 2 * C, xt, C, M, Mc, st.heads, hd, s), "text sdpa");
+  if (fusion_) {
     if (st.cs)
       check(sdq_rmsnorm_rope(cq, M, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
     check(sdq_sdpa(cq, C, kvt, 2 * C, kvt + C, 2 * C, aux, C, M, Mt, st.heads, hd, s),

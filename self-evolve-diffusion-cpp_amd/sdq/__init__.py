@@ -64,6 +64,8 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_rmsnorm_rope_batch": (ctypes.c_int, [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_float,
+                                              _vp]),
     "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
     "sdq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "sdq_sdpa": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
@@ -315,6 +317,23 @@ def rmsnorm_rope(x, C, w, heads, cs=None, eps=1e-6, col0=0, stream=None):
     _check(_lib.sdq_rmsnorm_rope(p, L, C, ld, _ptr(w), eps, heads, _ptr(cs), nr,
                                  _stream(stream)))
     return x
+
+
+class RmsSeg(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("L", ctypes.c_int64), ("ld", ctypes.c_int64),
+                ("w", ctypes.c_void_p), ("cs", ctypes.c_void_p), ("nr", ctypes.c_int)]
+
+
+def rmsnorm_rope_batch(segs, C, heads, eps=1e-6, stream=None):
+    """sdq_rmsnorm_rope_batch: segs = [(x, col0, w, cs)], each as in
+    rmsnorm_rope (x a device tensor whose rows hold the block at col0)."""
+    arr = (RmsSeg * max(len(segs), 1))()
+    for i, (x, col0, w, cs) in enumerate(segs):
+        arr[i].x = x.data_ptr() + 4 * col0
+        arr[i].L, arr[i].ld = x.shape[0], x.shape[1]
+        arr[i].w, arr[i].cs = _ptr(w), _ptr(cs)
+        arr[i].nr = 0 if cs is None else cs.shape[1]
+    _check(_lib.sdq_rmsnorm_rope_batch(arr, len(segs), C, heads, eps, _stream(stream)))
 
 
 def qlinear_host(w: Weight, A: np.ndarray, kind="none", bias=None, gate=None, resid=None,

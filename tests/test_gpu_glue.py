@@ -173,3 +173,39 @@ def test_rope_only_and_add(sdq_dev, oracle):
     assert_bitexact(xd.cpu().numpy(), oracle.add(x, y), "add")
     with pytest.raises(sdq.SdqError, match="nothing to do"):
         sdq.rmsnorm_rope(xd, C, None, heads, None)
+
+
+def test_rmsnorm_rope_batch_equals_single_calls(sdq_dev, oracle):
+    """sdq_rmsnorm_rope_batch over the q and k blocks of q|k|v (own weights,
+    3-D table), a 2C-stride context k block without rotation, a rotation-only
+    block and an empty one: bit-identical to one sdq_rmsnorm_rope call each."""
+    import torch
+
+    import sdq
+
+    heads, C = 3, 384
+    L, Lc = 300, 77
+    qkv = oracle.randn(L * 3 * C, 90).reshape(L, 3 * C) * np.float32(3.0)
+    kv = oracle.randn(Lc * 2 * C, 91).reshape(Lc, 2 * C)
+    q2 = oracle.randn(L * C, 92).reshape(L, C)
+    wq, wk, wc = oracle.randn(C, 93), oracle.randn(C, 94), oracle.randn(C, 95)
+    cs = oracle.rope_cs(oracle.rope_freqs_1d(L, 128, 10000.0, 1.0))
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(sdq_dev)  # noqa: E731
+    wq_d, wk_d, wc_d, cs_d = dv(wq), dv(wk), dv(wc), dv(cs)
+    a = [dv(qkv), dv(kv), dv(q2)]
+    b = [dv(qkv), dv(kv), dv(q2)]
+    empty = torch.zeros((0, C), device=sdq_dev)
+    sdq.rmsnorm_rope_batch([(a[0], 0, wq_d, cs_d), (a[0], C, wk_d, cs_d), (a[1], 0, wc_d, None),
+                            (empty, 0, wc_d, None)], C, heads)
+    sdq.rmsnorm_rope_batch([(a[2], 0, None, cs_d)], C, heads)
+    sdq.rmsnorm_rope(b[0], C, wq_d, heads, cs_d, col0=0)
+    sdq.rmsnorm_rope(b[0], C, wk_d, heads, cs_d, col0=C)
+    sdq.rmsnorm_rope(b[1], C, wc_d, heads, None, col0=0)
+    sdq.rmsnorm_rope(b[2], C, None, heads, cs_d)
+    torch.cuda.synchronize()
+    for x, y, name in zip(a, b, ("qkv", "ctx kv", "rope only")):
+        assert_bitexact(x.cpu().numpy(), y.cpu().numpy(), name)
+    want = oracle.rope(oracle.rmsnorm(qkv[:, :C], wq, 1e-6), cs, heads)
+    assert_bitexact(a[0].cpu().numpy()[:, :C], want, "q vs oracle")
+    with pytest.raises(sdq.SdqError, match="0 to 4 segments"):
+        sdq.rmsnorm_rope_batch([(a[2], 0, wq_d, None)] * 5, C, heads)
