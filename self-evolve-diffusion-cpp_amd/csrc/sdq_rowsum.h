@@ -62,17 +62,36 @@ __device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int 
     }
   };
   if (n == 32) {
-    // all eight reads first (one LDS latency per tile), then the 32 adds
+    // all eight reads first (one LDS latency per tile), then the 32 terms
+    // (the rounded squares, in place), then the 32 adds back to back: the
+    // chain then holds only the dependent adds
     float4 v[8];
 #pragma unroll
     for (int q = 0; q < 8; q++) v[q] = tb[q * 8 + l];
+    if constexpr (PASS != 0) {
+      auto term = [&](float x) {
+        if constexpr (PASS == 1) {
+          const float d = x - mu;
+          return d * d;
+        } else {
+          return x * x;
+        }
+      };
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        v[q].x = term(v[q].x);
+        v[q].y = term(v[q].y);
+        v[q].z = term(v[q].z);
+        v[q].w = term(v[q].w);
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-      add(v[q].x);
-      add(v[q].y);
-      add(v[q].z);
-      add(v[q].w);
+      acc = acc + v[q].x;
+      acc = acc + v[q].y;
+      acc = acc + v[q].z;
+      acc = acc + v[q].w;
     }
   } else {
     for (int c = 0; c < n; c++) {

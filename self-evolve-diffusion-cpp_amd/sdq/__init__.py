@@ -595,6 +595,10 @@ class DitBlock:
         st.cs, st.nr = _ptr(cs), (0 if cs is None else cs.shape[1])
         st.cs_tgt, st.nr_tgt = _ptr(cs_tgt), (0 if cs_tgt is None else cs_tgt.shape[1])
         if ws is None:
+            if stream is not None:
+                # a workspace allocated here would be freed on return while
+                # the side stream still uses it
+                raise ValueError("DitBlock.step: pass ws when running on a given stream")
             ws = torch.empty(self.workspace_bytes(st.M, st.Mc, st.Mt), dtype=torch.uint8,
                              device=x.device)
         st.ws, st.ws_bytes = _ptr(ws), ws.numel() * ws.element_size()

@@ -192,3 +192,71 @@ def test_block_step_errors(sdq_dev, oracle):
     bad.pop("ln3_b")
     with pytest.raises(RuntimeError, match="norm3"):
         blk.set_norms(bad)
+
+
+def test_fusion_layer_two_branches(sdq_dev, oracle):
+    """One fusion layer the way ovi_dit.cpp:726-734 runs it: audio self, video
+    self, a snapshot of the audio tokens, audio cross+FFN against the video
+    tokens, video cross+FFN against the snapshot. The GPU runs the two
+    branches' phases on two streams with snapshots of both; bit-exact against
+    the oracle chain in the reference's order (GPU attention and GELU steps)."""
+    import torch
+
+    import sdq
+
+    dim, ffn, heads, Mv, Ma, Mc = 256, 512, 2, 64, 40, 24
+    print(f"[fusion-layer] dim={dim} Mv={Mv} Ma={Ma}", flush=True)
+    lin_v, lin_a = _weights(oracle, dim, ffn, 300, True), _weights(oracle, dim, ffn, 400, True)
+    nm_v, nm_a = _norms(oracle, dim, 500), _norms(oracle, dim, 600)
+    xv = oracle.randn(Mv * dim, 1).reshape(Mv, dim)
+    xa = oracle.randn(Ma * dim, 2).reshape(Ma, dim)
+    cv = oracle.randn(Mc * dim, 3).reshape(Mc, dim)
+    ca = oracle.randn(Mc * dim, 4).reshape(Mc, dim)
+    ev = (oracle.randn(6 * dim, 5).reshape(6, dim) * np.float32(0.3)).astype(np.float32)
+    ea = (oracle.randn(6 * dim, 6).reshape(6, dim) * np.float32(0.3)).astype(np.float32)
+    cs_v = sdq.rope_table_3d(4, 4, 4)
+    cs_a = sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)
+    run = dict(sdpa=_gpu_sdpa(sdq_dev))
+
+    # the reference's order, on the oracle
+    ra = _ref_block(oracle, xa, ca, ea, lin_a, nm_a, heads, cs_a, True, phases=1,
+                    fc1_gelu=_gpu_fc1_gelu(lin_a), **run)
+    rv = _ref_block(oracle, xv, cv, ev, lin_v, nm_v, heads, cs_v, True, phases=1,
+                    fc1_gelu=_gpu_fc1_gelu(lin_v), **run)
+    og_audio = ra.copy()
+    ra = _ref_block(oracle, ra, ca, ea, lin_a, nm_a, heads, cs_a, True, rv, cs_v, phases=2,
+                    fc1_gelu=_gpu_fc1_gelu(lin_a), **run)
+    rv = _ref_block(oracle, rv, cv, ev, lin_v, nm_v, heads, cs_v, True, og_audio, cs_a, phases=2,
+                    fc1_gelu=_gpu_fc1_gelu(lin_v), **run)
+
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(sdq_dev)  # noqa: E731
+    bv, ba = sdq.DitBlock(lin_v, True), sdq.DitBlock(lin_a, True)
+    bv.set_norms(nm_v)
+    ba.set_norms(nm_a)
+    gxv, gxa, gcv, gca, gev, gea = dv(xv), dv(xa), dv(cv), dv(ca), dv(ev), dv(ea)
+    gcs_v, gcs_a = dv(cs_v), dv(cs_a)
+    wsv = torch.empty(bv.workspace_bytes(Mv, Mc, Ma), dtype=torch.uint8, device=sdq_dev)
+    wsa = torch.empty(ba.workspace_bytes(Ma, Mc, Mv), dtype=torch.uint8, device=sdq_dev)
+    sv, sa = torch.cuda.Stream(), torch.cuda.Stream()
+    cur = torch.cuda.current_stream()
+    sv.wait_stream(cur)
+    sa.wait_stream(cur)
+    ba.step(gxa, gca, gea, heads, cs=gcs_a, ws=wsa, phases=sdq.SELF, stream=sa.cuda_stream)
+    bv.step(gxv, gcv, gev, heads, cs=gcs_v, ws=wsv, phases=sdq.SELF, stream=sv.cuda_stream)
+    with torch.cuda.stream(sa):
+        og_a = gxa.clone()
+    with torch.cuda.stream(sv):
+        og_v = gxv.clone()
+    sv.wait_stream(sa)
+    sa.wait_stream(sv)
+    ba.step(gxa, gca, gea, heads, cs=gcs_a, target=og_v, cs_tgt=gcs_v, ws=wsa,
+            phases=sdq.CROSS_FFN, stream=sa.cuda_stream)
+    bv.step(gxv, gcv, gev, heads, cs=gcs_v, target=og_a, cs_tgt=gcs_a, ws=wsv,
+            phases=sdq.CROSS_FFN, stream=sv.cuda_stream)
+    cur.wait_stream(sv)
+    cur.wait_stream(sa)
+    torch.cuda.synchronize()
+    assert_bitexact(gxa.cpu().numpy(), ra, "audio branch")
+    assert_bitexact(gxv.cpu().numpy(), rv, "video branch")
+    bv.free()
+    ba.free()
