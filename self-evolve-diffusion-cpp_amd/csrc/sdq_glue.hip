@@ -185,11 +185,13 @@ hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Scaled dot-product attention (src/model/blocks.cpp:112-199, non-causal):
-// out[i, head] = softmax_j(q_i . k_j / sqrt(hd)) v_j, head_dim 128, fp32
-// throughout: v_mfma_f32_32x32x2_f32 and an online softmax (running max and
-// sum per query, the accumulator rescaled when the max moves). The reference
-// sums in a fixed serial order, so results agree within rounding, not bit
-// for bit.
+// out[i, head] = softmax_j(q_i . k_j / sqrt(hd)) v_j, head_dim 128: the
+// scores in fp32 (v_mfma_f32_32x32x2_f32; the softmax's exponential would
+// amplify any error in them), P.V as three bf16 products per fp32 product on
+// v_mfma_f32_32x32x16_bf16 (~2^-17 relative, P in [0, 1]), an online softmax
+// (running max and sum per query, the accumulator rescaled when the max
+// moves), fp32 accumulation. The reference sums in a fixed serial order, so
+// results agree within 2e-5 of the output scale, not bit for bit.
 //
 // Work: a workgroup of NW waves takes 32*NW queries of one head; each wave
 // 32 queries. Per 32-key block, K (32 x 128) and V^T (128 x 32) are staged
@@ -211,6 +213,7 @@ hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int kHd = 128;      // head dim
 constexpr int kKB = 32;       // keys per block
 constexpr int kKPad = 132;    // LDS row of K (floats): conflict-free 16-byte reads
@@ -353,17 +356,41 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     m = mnew;
 #pragma unroll
     for (int tt = 0; tt < 4; tt++) acc[tt] *= alpha;
-    // O^T += V^T . P^T
+    // O^T += V^T . P^T on the bf16 MFMA (32x32x16), each product split as
+    // V_hi.P_hi + V_hi.P_lo + V_lo.P_hi (x_hi = bf16(x), x_lo = bf16(x - x_hi):
+    // ~2^-17 relative per product, fp32 accumulation; P is in [0, 1], so no
+    // exponential amplifies it). Step s2 takes keys 16 s2 + 8(m/4) + 4h + m%4,
+    // m = 0..7, exactly the lane's P registers t[8 s2 + m] and its two V^T
+    // float4s at keys 16 s2 + 4h and 16 s2 + 8 + 4h.
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++) {
-      const float* vrow = &vt[b][32 * tt + j][4 * h];
+    for (int s2 = 0; s2 < 2; s2++) {
+      v8bf ph, pl;
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const float4 vv = *reinterpret_cast<const float4*>(vrow + 8 * u);
-        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, t[4 * u], acc[tt], 0, 0, 0);
-        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, t[4 * u + 1], acc[tt], 0, 0, 0);
-        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, t[4 * u + 2], acc[tt], 0, 0, 0);
-        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, t[4 * u + 3], acc[tt], 0, 0, 0);
+      for (int m = 0; m < 8; m++) {
+        const float x = t[8 * s2 + m];
+        const __bf16 hb = (__bf16)x;
+        ph[m] = hb;
+        pl[m] = (__bf16)(x - (float)hb);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; tt++) {
+        const float* vrow = &vt[b][32 * tt + j][4 * h + 16 * s2];
+        const float4 v0 = *reinterpret_cast<const float4*>(vrow);
+        const float4 v1 = *reinterpret_cast<const float4*>(vrow + 8);
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        v8bf vh, vl;
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+          const __bf16 hb = (__bf16)vv[m];
+          vh[m] = hb;
+          vl[m] = (__bf16)(vv[m] - (float)hb);
+        }
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, acc[tt], 0, 0, 0);
+        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, acc[tt], 0, 0, 0);
+        // keep each tile's V reads next to their MFMAs (hoisting them all
+        // would exceed the register budget of two waves per SIMD)
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // K(kb+2) into the buffer K(kb) left before the last barrier; V(kb+1)
