@@ -217,7 +217,7 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int kHd = 128;      // head dim
 constexpr int kKB = 32;       // keys per block
 constexpr int kKPad = 132;    // LDS row of K (floats): conflict-free 16-byte reads
-constexpr int kVPad = 36;     // LDS row of V^T
+constexpr int kVPd = 20;      // LDS row of V^T (dwords: 32 bf16 + pad; conflict-free stash)
 
 template <int NW>
 __global__ void __launch_bounds__(NW * 64)
@@ -225,7 +225,11 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
             const float* __restrict__ V, int64_t ldv, float* __restrict__ O, int64_t ldo,
             int64_t Lq, int64_t Lk, int qgroups, float scale_log2e) {
   __shared__ __attribute__((aligned(16))) float ks[2][kKB][kKPad];
-  __shared__ __attribute__((aligned(16))) float vt[2][kHd][kVPad];
+  // V^T as bf16 hi and lo parts, two keys per dword, keys of each 16-key
+  // group stored in the order 0-3, 8-11, 4-7, 12-15 (lane half h then reads
+  // its 8 keys of a PV step as one 16-byte run)
+  __shared__ __attribute__((aligned(16))) uint32_t vth[2][kHd][kVPd];
+  __shared__ __attribute__((aligned(16))) uint32_t vtl[2][kHd][kVPd];
   constexpr int NT = NW * 64;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int head = blockIdx.x / qgroups, qg = blockIdx.x - head * qgroups;
@@ -247,13 +251,20 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       qr[4 * c + 3] = v.w;
     }
   }
-  // Cooperative block loads, 32 keys x 32 float4 each of K and V. K: element
-  // f is (key f >> 5, float4 f & 31), whole rows per half-wave. V: (key
-  // (f >> 1) & 31, float4 (f & 1) + 2 (f >> 6)), so the transposed scalar LDS
-  // writes of a half-wave (16 keys x 2 float4s) fall in 32 distinct banks.
+  // Cooperative block loads. K: 32 keys x 32 float4, element f is (key
+  // f >> 5, float4 f & 31), whole rows per half-wave. V: 16 key pairs x 32
+  // float4s, item f is (pair f & 15, float4 2(f >> 5) + ((f >> 4) & 1)); a
+  // pair is the two keys that share a dword of the stored order, so the
+  // stash writes packed bf16x2 dwords, 32 distinct banks per half-wave.
   // Blocks past the end load zeros.
   constexpr int PER = (kKB * kHd / 4 + NT - 1) / NT;
-  float4 pk[PER], pv[PER];
+  constexpr int PERV = (kKB / 2 * kHd / 4 + NT - 1) / NT;
+  float4 pk[PER], pv0[PERV], pv1[PERV];
+  // stored position p (0..31) -> key: quads 1 and 2 of each 16 swapped
+  auto pos_key = [](int p) {
+    const int q = (p >> 2) & 3;
+    return (p & 16) + (q == 1 ? 8 : q == 2 ? 4 : 4 * q) + (p & 3);
+  };
   auto fetch_k = [&](int64_t kb) {
 #pragma unroll
     for (int c = 0; c < PER; c++) {
@@ -266,13 +277,15 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   };
   auto fetch_v = [&](int64_t kb) {
 #pragma unroll
-    for (int c = 0; c < PER; c++) {
+    for (int c = 0; c < PERV; c++) {
       const int f = tid + c * NT;
-      const int64_t kr = kb * kKB + ((f >> 1) & 31);
-      const int d4 = (f & 1) + 2 * (f >> 6);
-      pv[c] = f < kKB * kHd / 4 && kr < Lk
-                  ? *reinterpret_cast<const float4*>(V + kr * ldv + col + 4 * d4)
-                  : float4{0.f, 0.f, 0.f, 0.f};
+      const int kp = f & 15, d4 = 2 * (f >> 5) + ((f >> 4) & 1);
+      const int64_t k0 = kb * kKB + pos_key(2 * kp), k1 = kb * kKB + pos_key(2 * kp + 1);
+      const bool okf = f < kKB / 2 * kHd / 4;
+      pv0[c] = okf && k0 < Lk ? *reinterpret_cast<const float4*>(V + k0 * ldv + col + 4 * d4)
+                              : float4{0.f, 0.f, 0.f, 0.f};
+      pv1[c] = okf && k1 < Lk ? *reinterpret_cast<const float4*>(V + k1 * ldv + col + 4 * d4)
+                              : float4{0.f, 0.f, 0.f, 0.f};
     }
   };
   auto stash_k = [&](int b) {
@@ -282,16 +295,28 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       if (f < kKB * kHd / 4) *reinterpret_cast<float4*>(&ks[b][f >> 5][4 * (f & 31)]) = pk[c];
     }
   };
+  // x -> (bf16(x), bf16(x - bf16(x))) for the two keys of a dword
+  auto split2 = [](float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+    const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+  };
   auto stash_v = [&](int b) {
 #pragma unroll
-    for (int c = 0; c < PER; c++) {
+    for (int c = 0; c < PERV; c++) {
       const int f = tid + c * NT;
-      if (f < kKB * kHd / 4) {
-        const int key = (f >> 1) & 31, d = 4 * ((f & 1) + 2 * (f >> 6));
-        vt[b][d][key] = pv[c].x;
-        vt[b][d + 1][key] = pv[c].y;
-        vt[b][d + 2][key] = pv[c].z;
-        vt[b][d + 3][key] = pv[c].w;
+      if (f < kKB / 2 * kHd / 4) {
+        const int kp = f & 15, d = 4 * (2 * (f >> 5) + ((f >> 4) & 1));
+        const float a0[4] = {pv0[c].x, pv0[c].y, pv0[c].z, pv0[c].w};
+        const float a1[4] = {pv1[c].x, pv1[c].y, pv1[c].z, pv1[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          uint32_t hi, lo;
+          split2(a0[e], a1[e], hi, lo);
+          vth[b][d + e][kp] = hi;
+          vtl[b][d + e][kp] = lo;
+        }
       }
     }
   };
@@ -354,8 +379,12 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     }
     lsum = lsum * alpha + ps;
     m = mnew;
+    // alpha is exactly 1 where the max did not move: skip the rescale when
+    // that holds for the whole wave (bit-identical)
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++) acc[tt] *= alpha;
+      for (int tt = 0; tt < 4; tt++) acc[tt] *= alpha;
+    }
     // O^T += V^T . P^T on the bf16 MFMA (32x32x16), each product split as
     // V_hi.P_hi + V_hi.P_lo + V_lo.P_hi (x_hi = bf16(x), x_lo = bf16(x - x_hi):
     // ~2^-17 relative per product, fp32 accumulation; P is in [0, 1], so no
@@ -374,23 +403,12 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       }
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
-        const float* vrow = &vt[b][32 * tt + j][4 * h + 16 * s2];
-        const float4 v0 = *reinterpret_cast<const float4*>(vrow);
-        const float4 v1 = *reinterpret_cast<const float4*>(vrow + 8);
-        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        v8bf vh, vl;
-#pragma unroll
-        for (int m = 0; m < 8; m++) {
-          const __bf16 hb = (__bf16)vv[m];
-          vh[m] = hb;
-          vl[m] = (__bf16)(vv[m] - (float)hb);
-        }
+        const int dq = 8 * s2 + 4 * h;  // dword of stored position 16 s2 + 8h
+        const v8bf vh = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(&vth[b][32 * tt + j][dq]));
+        const v8bf vl = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(&vtl[b][32 * tt + j][dq]));
         acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, acc[tt], 0, 0, 0);
         acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, acc[tt], 0, 0, 0);
         acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, acc[tt], 0, 0, 0);
-        // keep each tile's V reads next to their MFMAs (hoisting them all
-        // would exceed the register budget of two waves per SIMD)
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // K(kb+2) into the buffer K(kb) left before the last barrier; V(kb+1)
