@@ -61,16 +61,25 @@ rms_stats_kernel(RmsSegs sg, int64_t C, float eps) {
 }
 
 // y = fl(fl(v*inv)*w) over the row, then the rotation of each head's first
-// nr pairs. One thread per pair; pairs never straddle heads (hd is even).
+// nr pairs. One thread per pair (pairs never straddle heads: hd is even);
+// grid.y is the segment, so its fields are wave-uniform. IDX32: the
+// segment's L*C/2 pairs fit 32-bit index math.
+template <bool IDX32>
 __global__ void __launch_bounds__(256)
 rms_rope_apply_kernel(RmsSegs sg, int64_t C, int hd) {
+  const RmsSeg& g = sg.s[blockIdx.y];
   const int64_t np = C / 2;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= sg.item0[sg.n]) return;
-  const int i = seg_of(sg.item0, sg.n, idx);
-  const RmsSeg& g = sg.s[i];
-  const int64_t it = idx - sg.item0[i];
-  const int64_t row = it / np, p = it - row * np;
+  if (idx >= g.L * np) return;
+  int64_t row, p;
+  if constexpr (IDX32) {
+    const uint32_t r32 = (uint32_t)idx / (uint32_t)np;
+    row = r32;
+    p = (int64_t)((uint32_t)idx - r32 * (uint32_t)np);
+  } else {
+    row = idx / np;
+    p = idx - row * np;
+  }
   const int64_t c0 = 2 * p;
   float* q = g.x + row * g.ld + c0;
   float y0 = q[0], y1 = q[1];
@@ -130,10 +139,14 @@ hipError_t launch_rmsnorm_rope_segs(const RmsSeg* segs, int nseg, int64_t C, int
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const int64_t items = st.item0[nseg];
-  if (items == 0) return hipSuccess;
-  hipLaunchKernelGGL(rms_rope_apply_kernel, dim3((unsigned)ceil_div(items, 256)), dim3(256), 0, s,
-                     st, C, (int)(C / heads));
+  int64_t most = 0;  // pairs of the largest segment
+  for (int i = 0; i < nseg; i++) most = most > segs[i].L * (C / 2) ? most : segs[i].L * (C / 2);
+  if (most == 0) return hipSuccess;
+  const dim3 ga((unsigned)ceil_div(most, 256), (unsigned)nseg);
+  if (most < (int64_t)1 << 31)
+    hipLaunchKernelGGL((rms_rope_apply_kernel<true>), ga, dim3(256), 0, s, st, C, (int)(C / heads));
+  else
+    hipLaunchKernelGGL((rms_rope_apply_kernel<false>), ga, dim3(256), 0, s, st, C, (int)(C / heads));
   return hipGetLastError();
 }
 
