@@ -573,8 +573,13 @@ def main():
         try:
             with open(os.path.join(ROOT, "profiles", "mfma_util.json")) as f:
                 mj = json.load(f)
+            sclk = mj["gui_active_cycles_per_xcd"] / (gemm_ms * 1e6)
+            cus = info.get("cu_count", 256) if isinstance(info, dict) else 256
+            # % of the int8 peak at that clock (SURVEY's CUs x sclk x 8192)
+            peak_eff = cus * sclk * 8192 / 1e3  # TOPS
             mfma = {"mfma_busy_frac_pmc": mj["mfma_busy_frac"],
-                    "sclk_ghz_effective": round(mj["gui_active_cycles_per_xcd"] / (gemm_ms * 1e6), 3)}
+                    "sclk_ghz_effective": round(sclk, 3),
+                    "gemm_pct_of_peak_at_effective_sclk": round(100 * achieved / peak_eff, 2)}
         except (OSError, ValueError, KeyError):
             mfma = {}
 

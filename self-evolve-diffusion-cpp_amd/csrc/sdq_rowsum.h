@@ -20,10 +20,10 @@ namespace rowsum {
 // waves per SIMD; bandwidth-bound there)
 constexpr int kLnDepthFew = 32, kLnDepthMany = 16;
 
-// 4 values of row r at columns c .. c+3, 0 past K; every lane issues its
-// load(s) (the address is clamped into the row), so the tile loop has no
-// branches and its loads stay in flight across iterations. VEC: K % 4 == 0
-// and 16-byte aligned rows (one 16-byte load).
+// 4 values of row r at columns c .. c+3 (values past K unspecified: see
+// mask4); every lane issues its load(s) (the address is clamped into the
+// row), so the tile loop has no branches and its loads stay in flight across
+// iterations. VEC: K % 4 == 0 and 16-byte aligned rows (one 16-byte load).
 template <bool VEC>
 __device__ __forceinline__ float4 load4(const float* __restrict__ r, int64_t c, int64_t K) {
   float4 v;
@@ -35,6 +35,13 @@ __device__ __forceinline__ float4 load4(const float* __restrict__ r, int64_t c, 
     v.z = r[c + 2 < K ? c + 2 : K - 1];
     v.w = r[c + 3 < K ? c + 3 : K - 1];
   }
+  return v;
+}
+
+// Zeroes the values of a load4 result past K. Applied when the tile is
+// consumed, not at the load: using the data right away would make every
+// prefetched load wait for its own completion.
+__device__ __forceinline__ float4 mask4(float4 v, int64_t c, int64_t K) {
   v.x = c < K ? v.x : 0.f;
   v.y = c + 1 < K ? v.y : 0.f;
   v.z = c + 2 < K ? v.z : 0.f;
@@ -103,6 +110,8 @@ __device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int 
   return acc;
 }
 
+// For one-wave workgroups only (64 threads: tb is the wave's own tile
+// buffer, and no barrier orders other waves).
 template <bool VEC, int PASS, int D>
 __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K, int l,
                                          float4 (&tb)[2][64], float mu) {
@@ -116,9 +125,13 @@ __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K,
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int64_t t = t0 + u;
-      tb[t & 1][l] = buf[u];
+      tb[t & 1][l] = mask4(buf[u], t * 32 + 4 * j, K);
       buf[u] = load4<VEC>(r, (t + D) * 32 + 4 * j, K);
-      __syncthreads();
+      // The workgroup is one wave (64 threads): its LDS operations execute
+      // in issue order, so waiting for the tile's LDS write is enough. A
+      // __syncthreads() would also wait for every global load in flight,
+      // draining the D-deep prefetch at each tile.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (l < 8 && t < nt) {
         const int n = (int)((K - t * 32) < 32 ? (K - t * 32) : 32);
         acc = ln_tile_sum<PASS>(tb[t & 1], l, acc, mu, n);
