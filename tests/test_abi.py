@@ -81,3 +81,22 @@ def test_host_mirror_headers_compile_standalone(tmp_path):
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
     assert subprocess.run([str(exe)]).returncode == 0
+
+
+def test_host_library_exports_its_c_shim():
+    """libsd_host.so exports every C function of the host mirror's headers
+    (the sd_dit_block_* shim, sd_rope_table_*), which the Python binding and
+    non-C++ callers use."""
+    import glob
+
+    import sdq
+
+    names = set()
+    for h in glob.glob(os.path.join(PKG, "host", "sd", "*.h")):
+        text = re.sub(r"/\*.*?\*/|//[^\n]*", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"^(?:int|double|size_t|const char\*|void)\s+(sd_[a-z0-9_]+)\s*\(",
+                                text, flags=re.M))
+    assert {"sd_dit_block_step_forward", "sd_rope_table_3d", "sd_dit_block_set_norms"} <= names
+    lib = sdq.load_host_library()
+    missing = sorted(n for n in names if not hasattr(lib, n))
+    assert not missing, missing
