@@ -23,6 +23,12 @@
 
 #pragma clang fp contract(off)
 
+// Row tiles per group of the persistent kernels' XCD-aware tile order (a
+// group's tiles share A panels in the XCD's L2).
+#ifndef SDQ_PERSIST_GROUP_M
+#define SDQ_PERSIST_GROUP_M 4
+#endif
+
 namespace sdq {
 
 namespace {
@@ -445,7 +451,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       ks = lin / T;
       lin -= ks * T;
     }
-    constexpr int GROUP_M = 4;
+    constexpr int GROUP_M = SDQ_PERSIST_GROUP_M;
     const int per_group = GROUP_M * tiles_n;
     const int g = lin / per_group;
     const int first_m = g * GROUP_M;
