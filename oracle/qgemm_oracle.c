@@ -42,6 +42,9 @@
  *                          tolerance; rows of p sum to 1.
  *   orc_rope_freqs_3d/1d - compiled reference rope_freqs_3d / rope_freqs_1d
  *                          bit-exact; float64 closed form within tolerance.
+ *   (layernorm, mod_rows, rmsnorm, rope, rope_freqs, sdpa are also pinned to
+ *   committed outputs of the reference build, tests/golden/ref_glue.npz, so
+ *   the pins hold where the reference sources are absent.)
  *   orc_quantize_rowwise - compiled reference sd::quantize_rowwise bit-exact,
  *                          reference golden replica (lround) bit-exact.
  *   orc_quant_rows       - closed form of the packer's numpy expression

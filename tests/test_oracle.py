@@ -414,3 +414,22 @@ def test_affine_layernorm_matches_reference_build(oracle, ref):
     t = oracle.layernorm(x, 1e-6)  # the no-affine output is t + 0 = fmaf(t, 1, 0)
     two = (t * w + b).astype(np.float32)  # planted: two roundings
     assert np.any(bits(two) != bits(got))
+
+
+def test_ref_glue_fixture_outputs(oracle):
+    """Committed outputs of the reference's own block glue (layernorm with and
+    without affine, mod_rows, rmsnorm, the 3-D / 1-D rope angles and
+    apply_rope, sdpa; tests/golden/make_golden_glue.py): the oracle's
+    restatements reproduce them bit for bit, without the reference sources."""
+    g = np.load(os.path.join(GOLDEN, "ref_glue.npz"))
+    x, w, b = g["x"], g["w"], g["b"]
+    assert_bitexact(oracle.layernorm(x, 1e-6), g["layernorm"], "layernorm")
+    assert_bitexact(oracle.layernorm(x, 1e-6, w, b), g["layernorm_affine"], "layernorm affine")
+    assert_bitexact(oracle.mod_rows(g["layernorm"], g["shift"], g["scale"]), g["mod_rows"],
+                    "mod_rows")
+    assert_bitexact(oracle.rmsnorm(x, w, 1e-6), g["rmsnorm"], "rmsnorm")
+    assert_bitexact(oracle.rope_freqs_3d(2, 3, 4, 128, 10000.0), g["ang3"], "rope_freqs_3d")
+    assert_bitexact(oracle.rope_freqs_1d(24, 128, 10000.0, 0.19676), g["ang1"], "rope_freqs_1d")
+    assert_bitexact(oracle.rope(x, oracle.rope_cs(g["ang3"]), 2), g["rope3"], "apply_rope 3-D")
+    assert_bitexact(oracle.rope(x, oracle.rope_cs(g["ang1"]), 2), g["rope1"], "apply_rope 1-D")
+    assert_bitexact(oracle.sdpa(g["q"], g["k"], g["v"], 2), g["sdpa"], "sdpa")
