@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the int8 qGEMM hot path on one MI355X.
 
-Workload (BASELINE.json metric, north star): one int8 Linear of the Ovi DiT
+Workload (the headline metric, the north star): one int8 Linear of the Ovi DiT
 FFN up-projection at 720p/121 frames, M=27280 tokens, K=3072, N=14336:
   Y[M,N] = qgemm(A, W) + bias  (sd::qgemm + mlin's bias pass, fused),
 including the per-row activation quantizer pre-pass, fp32 output.
@@ -403,7 +403,7 @@ def bench_twin(torch, sdq, args):
 
 
 def bench_load(torch, sdq, args):
-    """Weight upload from host memory (§8(f) rank 4): 8 DiT blocks at the real
+    """Weight upload from host memory (the streaming loader): 8 DiT blocks at the real
     widths (dim 3072, FFN 14336, fusion: 1.46 GB of int8 + scales, host arrays
     like load_sdcpp's views), one block at a time (per Linear: host concat,
     pageable copy, repack) vs one streamed upload (pinned ring, async copies,
@@ -575,7 +575,7 @@ def main():
                 mj = json.load(f)
             sclk = mj["gui_active_cycles_per_xcd"] / (gemm_ms * 1e6)
             cus = info.get("cu_count", 256) if isinstance(info, dict) else 256
-            # % of the int8 peak at that clock (SURVEY's CUs x sclk x 8192)
+            # % of the int8 peak at that clock (CUs x sclk x 8192 ops per clock)
             peak_eff = cus * sclk * 8192 / 1e3  # TOPS
             mfma = {"mfma_busy_frac_pmc": mj["mfma_busy_frac"],
                     "sclk_ghz_effective": round(sclk, 3),
