@@ -40,9 +40,18 @@ def parse():
     ap.add_argument("--K", type=int, default=K_NS)
     ap.add_argument("--N", type=int, default=N_NS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-rows", type=int, default=4096)
-    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
-                    help="rocprofv3 FETCH/WRITE_SIZE summary used for roofline.traffic")
+    ap.add_argument("--cpu-sample-rows", type=int, default=0,
+                    help="rows of the CPU baseline's sample (0: all M rows, the full workload)")
+    ap.add_argument("--settle-ms", type=float, default=600.0,
+                    help="after the W warmup steps, further untimed steps until this much wall "
+                         "time has passed since the first warmup step (the shader clock's "
+                         "power-limit transient; 0 = none)")
+    ap.add_argument("--counters-json", default=os.path.join(ROOT, "profiles", "ns_counters.json"),
+                    help="rocprofv3 counter summary (written by --summarize-counters); its "
+                         "figures are reported only when it was recorded on this library build")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="read rocprofv3 --pmc output directories (FETCH_SIZE, WRITE_SIZE, "
+                         "MFMA busy, L2 hit passes of --profile-pass) and write --counters-json")
     ap.add_argument("--config", default="ns",
                     choices=["ns", "block", "blockfull", "ffn", "cross", "twin", "load"],
                     help="ns: the north-star qGEMM (the driver's bench line); block: one DiT "
@@ -73,7 +82,9 @@ def profile_pass(torch, sdq, args):
     dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": True, "copy_bytes": src.numel() * 4, "M": args.M,
-                      "K": args.K, "N": args.N}), flush=True)
+                      "K": args.K, "N": args.N, "library": sdq.version(),
+                      "cu_count": sdq.device_info()["cu_count"],
+                      "plan": sdq.qlinear_plan(w, args.M)}), flush=True)
 
 
 def make_inputs(torch, dev, M, K, N, seed=1234):
@@ -451,7 +462,7 @@ def cpu_baseline(args, K, N):
     import numpy as np
     import pyoracle
 
-    rows = args.cpu_sample_rows
+    rows = args.cpu_sample_rows if args.cpu_sample_rows > 0 else args.M
     rng = np.random.default_rng(7)
     A = rng.standard_normal((rows, K), dtype=np.float32)
     W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
@@ -491,13 +502,17 @@ def cpu_baseline(args, K, N):
         pass
     return {"value": round(tops, 5), "unit": "TOPS", "cores": int(cores), "kind": kind,
             "value_8_threads": tops8,
-            "sample": f"M={rows} rows of the {args.M}x{K}x{N} qgemm (same K,N; M>=2048 keeps "
-                      f"the reference's widened-s16 path), best of 3 after 1 warmup, "
-                      f"{best * 1e3:.1f} ms/call, host CPU: {cpu}"}
+            "sample": (f"the full {args.M}x{K}x{N} qgemm" if rows == args.M else
+                       f"M={rows} rows of the {args.M}x{K}x{N} qgemm (same K,N; M>=2048 keeps "
+                       f"the reference's widened-s16 path)") +
+                      f", best of 3 after 1 warmup, {best * 1e3:.1f} ms/call, host CPU: {cpu}"}
 
 
 def main():
     args = parse()
+    if args.summarize_counters:
+        summarize_counters(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (every GPU box here has one); "
               "--gpus must be 1", file=sys.stderr)
@@ -534,8 +549,10 @@ def main():
     def step():
         sdq.qlinear(w, A, Y, kind="none", bias=bias)
 
+    t_warm = time.perf_counter()
     for _ in range(args.warmup):
         step()
+    settle = _settle(torch, step, args.settle_ms, t_warm)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -546,43 +563,31 @@ def main():
     ops = 2.0 * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
 
-    # per-kernel device time with HIP events on the launch stream
+    # per-kernel device time with HIP events on the launch stream, for the
+    # kernels the library's plan names (the 256x256 launch and, when the
+    # last round of tiles is split off, the 128x128 tail launch)
+    plan = sdq.qlinear_plan(w, M)
     sdq.profile_begin()
     for _ in range(args.steps):
         step()
     prof = sdq.profile_end()
-    gemm_name = next(k for k in prof if k.startswith("qgemm"))
-    g_launch, g_ms = prof[gemm_name]
-    gemm_ms = g_ms / g_launch
+    kern = {}
+    for name, r0, rows in plan:
+        n_launch, tot = prof[name]
+        kms = tot / n_launch
+        kops = 2.0 * rows * N * K
+        kern[name] = {"rows": rows, "ms": round(kms, 5), "tops": round(kops / kms / 1e9, 2),
+                      "ops": kops}
+    main_name = plan[0][0]
+    main = kern[main_name]
+    gemm_ms = sum(k["ms"] for k in kern.values())
     q_launch, q_ms = prof.get("act_quant", (1, 0.0))
-    achieved = ops / (gemm_ms * 1e-3) / 1e12
-    traffic = None
-    try:
-        with open(args.traffic_json) as f:
-            tj = json.load(f)
-        key = f"{M}x{K}x{N}"
-        if key in tj:
-            traffic = tj[key]["qgemm_hbm_bytes_per_launch"]
-    except (OSError, ValueError, KeyError):
-        traffic = None
-    # MFMA busy fraction of the GEMM's active cycles and its active cycles per
-    # XCD (rocprofv3 PMC, profiles/mfma_util.json): with this run's GEMM time
-    # they give the effective shader clock.
-    mfma = {}
-    if (M, K, N) == (M_NS, K_NS, N_NS):
-        try:
-            with open(os.path.join(ROOT, "profiles", "mfma_util.json")) as f:
-                mj = json.load(f)
-            sclk = mj["gui_active_cycles_per_xcd"] / (gemm_ms * 1e6)
-            cus = info.get("cu_count", 256) if isinstance(info, dict) else 256
-            # % of the int8 peak at that clock (CUs x sclk x 8192 ops per clock)
-            peak_eff = cus * sclk * 8192 / 1e3  # TOPS
-            mfma = {"mfma_busy_frac_pmc": mj["mfma_busy_frac"],
-                    "sclk_ghz_effective": round(sclk, 3),
-                    "gemm_pct_of_peak_at_effective_sclk": round(100 * achieved / peak_eff, 2)}
-        except (OSError, ValueError, KeyError):
-            mfma = {}
 
+    counters, stamp = _load_counters(args.counters_json, sdq.version(), f"{M}x{K}x{N}")
+    traffic = None
+    if counters:
+        kc = counters["kernels"].get(main_name, {})
+        traffic = kc.get("hbm_bytes_per_launch")
     line = {
         "metric": "int8 qGEMM TOPS + % of MI355X MFMA peak at M=27280,K=3072,N=14336",
         "value": round(tops, 2),
@@ -599,17 +604,152 @@ def main():
                 "resident in HBM",
         "config": {"workload": f"qgemm+bias M={M} K={K} N={N} (DiT FFN up, 720p/121f)",
                    "M": M, "K": K, "N": N, "output": "fp32", "epilogue": "bias",
-                   "gemm_kernel": gemm_name, "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
+                   "pct_of_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
+                   "settle": {"extra_untimed_steps": settle,
+                              "why": f"untimed steps after the {args.warmup} warmup steps until "
+                                     f"{args.settle_ms:.0f} ms had passed: the shader clock "
+                                     "overshoots and settles under the power limit over the "
+                                     "first ~25 calls"},
                    "act_quant_ms": round(q_ms / max(q_launch, 1), 5),
-                   "gemm_ms": round(gemm_ms, 5), "weight_repack_ms": round(repack_ms, 3),
-                   **mfma, "device": info},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                     "traffic": traffic},
+                   "gemm_kernels": kern, "gemm_ms": round(gemm_ms, 5),
+                   "weight_repack_ms": round(repack_ms, 3),
+                   "library": sdq.version(), "counters": stamp, "device": info},
+        "roofline": {"bound": "mfma", "kernel": main_name, "achieved": main["tops"],
+                     "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": round(main["tops"] / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "algorithmic_ops": main["ops"],
+                     "algorithmic_bytes": _gemm_bytes(main["rows"], K, N)},
     }
+    if counters:
+        kc = counters["kernels"].get(main_name, {})
+        if "mfma_busy_frac" in kc:
+            line["config"]["mfma_busy_frac_pmc"] = kc["mfma_busy_frac"]
+        if "l2_hit_frac" in kc:
+            line["config"]["l2_hit_frac_pmc"] = kc["l2_hit_frac"]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args, K, N)
     print(json.dumps(line), flush=True)
+
+
+def _settle(torch, step, settle_ms, t_start):
+    """Untimed steps until settle_ms of wall time have passed since t_start,
+    synchronizing every few steps so the host does not run ahead of the GPU;
+    returns the number of extra steps."""
+    n = 0
+    torch.cuda.synchronize()
+    while (time.perf_counter() - t_start) * 1e3 < settle_ms:
+        for _ in range(4):
+            step()
+        n += 4
+        torch.cuda.synchronize()
+    return n
+
+
+def _gemm_bytes(rows, K, N):
+    """Algorithmic HBM bytes of one GEMM launch over `rows` activation rows:
+    int8 activations (rows*K), int8 weights (N*K), weight scales + bias
+    (8N), fp32 output (4*rows*N)."""
+    return rows * K + N * K + 8 * N + 4 * rows * N
+
+
+def _load_counters(path, library, key):
+    """The counter summary for workload `key`, if it was recorded on this
+    library build (same source fingerprint); else (None, reason)."""
+    try:
+        with open(path) as f:
+            cj = json.load(f)
+    except (OSError, ValueError):
+        return None, "no counter summary"
+    if cj.get("workload") != key:
+        return None, f"counter summary is for {cj.get('workload')}, not {key}"
+    if cj.get("library") != library:
+        return None, (f"counter summary recorded on '{cj.get('library')}', this run loads "
+                      f"'{library}': not reported")
+    return cj, f"recorded on this build ({cj.get('commit', '?')}, {cj.get('source', '')})"
+
+
+def _short_kernel(name):
+    """rocprofv3 kernel name -> the library's record name (north-star pass)."""
+    if "qgemm_persist<256, 256" in name:
+        return "qgemm_tile256x256"
+    if "qgemm_persist<128, 128" in name:
+        return "qgemm_tail128"
+    if "act_quant_units_kernel" in name:
+        return "act_quant"
+    if "copyBuffer" in name or "copy" in name.lower():
+        return "copy"
+    return None
+
+
+def summarize_counters(args):
+    """Reads the counter_collection.csv files of rocprofv3 --pmc runs of
+    `bench.py --profile-pass` and writes the per-kernel summary bench.py
+    reports: HBM bytes per launch (FETCH_SIZE and WRITE_SIZE, each scaled by
+    what the counter reads for the pass's plain copy of known size), MFMA busy
+    fraction (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs) and L2
+    hit fraction (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum))."""
+    import csv
+    import glob
+    import subprocess
+
+    vals = {}  # (kernel, counter) -> [per-dispatch values]
+    meta = None
+    for d in args.summarize_counters:
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(fn, newline="") as f:
+                for row in csv.DictReader(f):
+                    k = _short_kernel(row["Kernel_Name"])
+                    if k:
+                        vals.setdefault((k, row["Counter_Name"]), []).append(
+                            float(row["Counter_Value"]))
+        for fn in glob.glob(os.path.join(d, "**", "*.log"), recursive=True) + \
+                glob.glob(os.path.join(d + ".log")):
+            with open(fn) as f:
+                for ln in f:
+                    if ln.startswith("{") and "profile_pass" in ln:
+                        meta = json.loads(ln)
+    if meta is None:
+        sys.exit("summarize: no --profile-pass output line found (pass the .log beside each dir)")
+    mean = lambda k, c: (sum(vals[(k, c)]) / len(vals[(k, c)])) if (k, c) in vals else None  # noqa
+    copy_bytes = meta["copy_bytes"]
+    cf, cw = mean("copy", "FETCH_SIZE"), mean("copy", "WRITE_SIZE")
+    fscale = copy_bytes / (cf * 1024) if cf else None
+    wscale = copy_bytes / (cw * 1024) if cw else None
+    info_cus = int(meta.get("cu_count", 256))
+    out = {"workload": f"{meta['M']}x{meta['K']}x{meta['N']}", "library": meta["library"],
+           "plan": meta["plan"], "calibration": {"copy_bytes": copy_bytes,
+                                                  "fetch_scale": fscale, "write_scale": wscale},
+           "kernels": {}}
+    try:
+        out["commit"] = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short=12", "HEAD"],
+                                       capture_output=True, text=True).stdout.strip()
+    except OSError:
+        out["commit"] = "?"
+    for k in ("qgemm_tile256x256", "qgemm_tail128", "act_quant"):
+        kc = {}
+        f, wr = mean(k, "FETCH_SIZE"), mean(k, "WRITE_SIZE")
+        if f is not None and fscale:
+            kc["fetch_bytes"] = round(f * 1024 * fscale)
+        if wr is not None and wscale:
+            kc["write_bytes"] = round(wr * 1024 * wscale)
+        if "fetch_bytes" in kc and "write_bytes" in kc:
+            kc["hbm_bytes_per_launch"] = kc["fetch_bytes"] + kc["write_bytes"]
+        busy, act = mean(k, "SQ_VALU_MFMA_BUSY_CYCLES"), mean(k, "GRBM_GUI_ACTIVE")
+        if busy is not None and act:
+            # GRBM_GUI_ACTIVE is summed over the 8 XCDs; 4 SIMDs per CU
+            kc["mfma_busy_frac"] = round(busy / ((act / 8) * info_cus * 4), 4)
+            kc["active_cycles_per_xcd"] = round(act / 8)
+        hit, miss = mean(k, "TCC_HIT_sum"), mean(k, "TCC_MISS_sum")
+        if hit is not None and miss is not None and hit + miss > 0:
+            kc["l2_hit_frac"] = round(hit / (hit + miss), 4)
+            kc["l2_requests"] = round(hit + miss)
+        if kc:
+            kc["dispatches"] = max(len(v) for (kk, c), v in vals.items() if kk == k)
+            out["kernels"][k] = kc
+    out["source"] = os.path.relpath(args.counters_json, ROOT).replace(".json", ".md")
+    with open(args.counters_json, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 if __name__ == "__main__":

@@ -79,7 +79,9 @@ typedef struct sdq_device_info {
 /* Thread-local text of the last error raised on this thread ("" if none). */
 const char* sdq_last_error(void);
 
-/* Library version string. */
+/* Library version string: "sdq <version> gfx950 src:<16 hex digits>", the
+ * last field a fingerprint of the device sources and build flags the library
+ * was compiled from. */
 const char* sdq_version(void);
 
 /* Select `device` for this thread and check it is gfx950. Idempotent.
@@ -255,6 +257,21 @@ typedef struct sdq_kernel_time {
 } sdq_kernel_time;
 int sdq_profile_begin(void);
 int sdq_profile_end(sdq_kernel_time* out, int max_records, int* n_records);
+
+/* The GEMM launches sdq_qlinear makes for M rows against w (16-byte aligned
+ * operands, N % 4 == 0): one, or two when a 256x256 launch hands its last
+ * rows to a 128x128 launch; for each, the record name sdq_profile_end uses
+ * and the activation rows [row0, row0 + rows) it covers, so a caller can
+ * price each kernel's own work. No GPU work is done.
+ * Replaces: nothing in the reference (measurement support). */
+typedef struct sdq_gemm_plan {
+  int nlaunch;
+  int splitk;        /* split-K factor (1 = none) */
+  char name[2][48];
+  int64_t row0[2];
+  int64_t rows[2];
+} sdq_gemm_plan;
+int sdq_qlinear_plan(const sdq_weight* w, int64_t M, int epi_kind, sdq_gemm_plan* out);
 
 /* Synchronize the current device (convenience for ctypes callers). */
 int sdq_sync(void);

@@ -350,21 +350,37 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (ea.bias) vec = vec && aligned16(ea.bias);
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
+  int tail = 0;
+  hipEvent_t pmid = nullptr;
+  if (t_prof && hipEventCreate(&pmid) != hipSuccess) pmid = nullptr;
   GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count, splitk,
-              splitk > 1 ? ws->part : nullptr, rmax_out ? &rmax_out->chunks : nullptr};
+              splitk > 1 ? ws->part : nullptr, rmax_out ? &rmax_out->chunks : nullptr, &tail,
+              pmid};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
-  if (e != hipSuccess) return hip_error(e, "qgemm launch");
+  if (e != hipSuccess) {
+    if (pmid) (void)hipEventDestroy(pmid);
+    return hip_error(e, "qgemm launch");
+  }
   if (t_prof) {
     hipEvent_t p2 = prof_mark(s);
-    if (p0 && p1 && p2) {
+    if (p0 && p1 && p2 && (!tail || pmid)) {
       t_recs.push_back({lnmod ? "ln_mod_quant" : premax ? "act_quant_premax" : "act_quant", p0, p1});
-      t_recs.push_back({std::string("qgemm_") + gemm_cfg_name(cfg) + (splitk > 1 ? "_splitk" : ""),
-                        p1, p2});
+      const std::string g = std::string("qgemm_") + gemm_cfg_name(cfg) + (splitk > 1 ? "_splitk" : "");
+      if (tail) {
+        // the 256x256 launch over the full rounds' rows, then the 128x128
+        // launch over the remaining rows: one record each
+        t_recs.push_back({g, p1, pmid});
+        t_recs.push_back({"qgemm_tail128", pmid, p2});
+        pmid = nullptr;
+      } else {
+        t_recs.push_back({g, p1, p2});
+      }
     } else {
       for (hipEvent_t ev : {p0, p1, p2})
         if (ev) (void)hipEventDestroy(ev);
     }
   }
+  if (pmid) (void)hipEventDestroy(pmid);
   return SDQ_OK;
 }
 
@@ -407,7 +423,10 @@ extern "C" {
 
 const char* sdq_last_error(void) { return t_err.c_str(); }
 
-const char* sdq_version(void) { return "sdq 0.1 gfx950"; }
+#ifndef SDQ_SRC_HASH
+#define SDQ_SRC_HASH "unknown"
+#endif
+const char* sdq_version(void) { return "sdq 0.2 gfx950 src:" SDQ_SRC_HASH; }
 
 int sdq_init(int device) {
   int n = 0;
@@ -914,6 +933,38 @@ int sdq_stream_sync(void* stream) {
 
 int sdq_profile_begin(void) {
   t_prof = true;
+  return SDQ_OK;
+}
+
+int sdq_qlinear_plan(const sdq_weight* w, int64_t M, int epi_kind, sdq_gemm_plan* out) {
+  if (!w || !out) return set_error(SDQ_ERR_INVALID, "null weight or out");
+  if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
+  int rc = ensure_device(w->device);
+  if (rc) return rc;
+  std::memset(out, 0, sizeof(*out));
+  out->splitk = 1;
+  if (M == 0 || w->N == 0) return SDQ_OK;
+  const int cu = g_dev[w->device].cu_count;
+  const int cfg = choose_gemm_cfg(M, w->N, w->KFp, epi_kind, cu);
+  auto put = [&](const std::string& name, int64_t r0, int64_t rows) {
+    const int i = out->nlaunch++;
+    std::snprintf(out->name[i], sizeof(out->name[i]), "%s", name.c_str());
+    out->row0[i] = r0;
+    out->rows[i] = rows;
+  };
+  if (cfg == kCfgSkinny && qin_fits(M, w->K, w->KFp) && !std::getenv("SDQ_NO_QIN")) {
+    put("qgemm_skinny_qin", 0, M);
+    return SDQ_OK;
+  }
+  out->splitk = choose_splitk(cfg, M, w->N, w->KFp, cu);
+  const std::string g = std::string("qgemm_") + gemm_cfg_name(cfg) + (out->splitk > 1 ? "_splitk" : "");
+  const int64_t Ma = (cfg == kCfg256x256 && w->K > 0) ? tail_split_rows(M, w->N, cu) : 0;
+  if (Ma > 0) {
+    put(g, 0, Ma);
+    put("qgemm_tail128", Ma, M - Ma);
+  } else {
+    put(g, 0, M);
+  }
   return SDQ_OK;
 }
 

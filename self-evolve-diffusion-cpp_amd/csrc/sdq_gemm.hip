@@ -1219,6 +1219,17 @@ int gemm_rmax_chunks(int cfg, int64_t N) {
   return 0;
 }
 
+int64_t tail_split_rows(int64_t M, int64_t N, int cu_count) {
+  // A last round of 256x256 tiles under half full: the rows of the full
+  // rounds (whole m-tiles) run as 256x256 tiles, the rest as 128x128 tiles.
+  if (std::getenv("SDQ_NO_TAIL")) return 0;
+  const int64_t tn = ceil_div(N, 256), T = ceil_div(M, 256) * tn;
+  const int64_t G = cu_count > 0 ? cu_count : 256;
+  const int64_t full = (T / G) * G, tail = T - full;
+  const int64_t Ma = (full / tn) * 256;
+  return (tail > 0 && 2 * tail < G && Ma > 0 && Ma < M) ? Ma : 0;
+}
+
 int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count) {
   // Long K on a grid that leaves CUs idle: split K so the 128x128 kernel's
   // (tile, k-range) items number at most one per CU (measured: more items
@@ -1251,6 +1262,7 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
   // Row maxima of a GELU output: written by the persistent kernels only
   // (not under split-K), one column chunk per wave column of each tile.
   if (aux.rmax_chunks) *aux.rmax_chunks = 0;
+  if (aux.tail) *aux.tail = 0;
   const bool rmax = epi.rmax && epi.kind == SDQ_EPI_GELU && persist && aux.splitk <= 1 &&
                     (cfg == kCfg128x128 || cfg == kCfg256x256) &&
                     gemm_rmax_chunks(cfg, N) <= epi.rmax_stride;
@@ -1281,15 +1293,13 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
         // full rounds (whole m-tiles) run here, the rest as 128x128 tiles (a
         // quarter of the work each, two per CU) right after. Not with row
         // maxima (the two tile widths write different column chunks).
-        const int64_t tn = ceil_div(N, 256), T = ceil_div(M, 256) * tn;
-        const int64_t G = aux.cu_count > 0 ? aux.cu_count : 256;
-        const int64_t full = (T / G) * G, tail = T - full;
-        const int64_t Ma = (full / tn) * 256;
-        if (!epi_r.rmax && tail > 0 && 2 * tail < G && Ma > 0 && Ma < M &&
-            !std::getenv("SDQ_NO_TAIL")) {
+        const int64_t Ma = epi_r.rmax ? 0 : tail_split_rows(M, N, aux.cu_count);
+        if (Ma > 0) {
           hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r,
                                                               Y, aux.cu_count, s);
           if (e != hipSuccess) return e;
+          if (aux.tail) *aux.tail = 1;
+          if (aux.mid && (e = hipEventRecord(aux.mid, s)) != hipSuccess) return e;
           EpiArgs et = epi_r;
           if (et.resid) et.resid += Ma * N;
           return run_persist<128, 128, 2, 2, 2, 4, 2>(

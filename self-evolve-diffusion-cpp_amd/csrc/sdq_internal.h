@@ -167,6 +167,9 @@ hipError_t launch_qgemm_qin(const int8_t* wt, const float* bs, const float* A, i
                             int vec, hipStream_t s);
 // Split-K factor for the 128x128 kernel at this shape (1 = no split).
 int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count);
+// Rows of a 256x256 persistent launch that run as 256x256 tiles when the
+// remaining rows go to a second, 128x128 launch; 0 = one launch.
+int64_t tail_split_rows(int64_t M, int64_t N, int cu_count);
 
 // Extra buffers of the persistent GEMM path: bias / gate copied into
 // zero-padded buffers (nullptr when absent) so they can be moved by LDS-DMA,
@@ -180,6 +183,9 @@ struct GemmAux {
   int splitk;  // choose_splitk's factor (1 = none)
   int* part;   // splitk x M x N int32 partial sums (splitk > 1)
   int* rmax_chunks;  // out (nullable): column chunks written to epi.rmax, 0 = none
+  int* tail;         // out (nullable): 1 when a 256x256 launch handed its last rows to a
+                     // second, 128x128 launch (two kernels ran), else 0
+  hipEvent_t mid;    // nullable: recorded between those two launches (per-kernel timing)
 };
 // Column chunks of the row maxima a GELU launch of this config writes.
 int gemm_rmax_chunks(int cfg, int64_t N);

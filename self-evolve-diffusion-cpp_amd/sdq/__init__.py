@@ -42,6 +42,12 @@ class DeviceInfo(ctypes.Structure):
                 ("total_mem", ctypes.c_int64), ("arch", ctypes.c_char * 64)]
 
 
+class GemmPlan(ctypes.Structure):
+    _fields_ = [("nlaunch", ctypes.c_int), ("splitk", ctypes.c_int),
+                ("name", (ctypes.c_char * 48) * 2), ("row0", ctypes.c_int64 * 2),
+                ("rows", ctypes.c_int64 * 2)]
+
+
 class KernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int),
                 ("total_ms", ctypes.c_double)]
@@ -87,6 +93,7 @@ SIGNATURES = {
     "sdq_profile_end": (ctypes.c_int, [ctypes.POINTER(KernelTime), ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_int)]),
     "sdq_sync": (ctypes.c_int, []),
+    "sdq_qlinear_plan": (ctypes.c_int, [_vp, _i64, ctypes.c_int, ctypes.POINTER(GemmPlan)]),
 }
 
 _lib = None
@@ -143,6 +150,69 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _bad(msg):
+    return SdqError(ERR_INVALID, msg)
+
+
+_DT = {"f32": "float32", "i32": "int32", "i8": "int8", "u8": "uint8"}
+
+
+class _Args:
+    """Checks the device-tensor arguments of one call before anything is
+    launched. The C ABI receives bare pointers and cannot see a host buffer,
+    a wrong element type, a strided view or a short buffer; any of those
+    would reach a kernel as an out-of-bounds address, so each raises
+    SdqError (ERR_INVALID) here. Calling the object checks one argument's
+    type, element type, shape and layout and returns its address; done()
+    then checks that every argument lives on the current GPU."""
+
+    def __init__(self):
+        self._seen = []
+
+    def __call__(self, t, name, dt="f32", shape=None, contig=True, optional=False):
+        """shape: the exact shape (None entries are free); contig=False accepts
+        2-D views whose rows are contiguous but strided (the caller passes
+        stride(0) as the row stride)."""
+        if t is None:
+            if optional:
+                return None
+            raise _bad(f"{name}: required")
+        import torch
+
+        if not isinstance(t, torch.Tensor):
+            raise _bad(f"{name}: expected a torch device tensor, got {type(t).__name__}")
+        want = getattr(torch, _DT[dt])
+        if t.dtype != want:
+            raise _bad(f"{name}: dtype {t.dtype}, expected {want}")
+        if shape is not None:
+            if t.dim() != len(shape) or any(w is not None and int(d) != int(w)
+                                            for d, w in zip(t.shape, shape)):
+                want_s = tuple("*" if w is None else int(w) for w in shape)
+                raise _bad(f"{name}: shape {tuple(t.shape)}, expected {want_s}")
+        if contig:
+            if not t.is_contiguous():
+                raise _bad(f"{name}: must be contiguous")
+        elif t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+            raise _bad(f"{name}: must be 2-D with contiguous rows")
+        self._seen.append((name, t))
+        return ctypes.c_void_p(t.data_ptr())
+
+    def done(self):
+        import torch
+
+        for name, t in self._seen:
+            if not t.is_cuda:
+                raise _bad(f"{name}: must be on the GPU (got device {t.device})")
+            cur = torch.cuda.current_device()
+            if t.device.index is not None and t.device.index != cur:
+                raise _bad(f"{name}: on {t.device}, current device is cuda:{cur}")
+
+
+def _ld(t):
+    """Row stride (elements) of a 2-D tensor with contiguous rows."""
+    return int(t.stride(0)) if t.shape[0] > 1 else int(t.shape[1])
+
+
 class Weight:
     """Device copy of an int8 [N,K] weight + f32 [N] scales (one-time upload
     and repack into the MFMA fragment layout)."""
@@ -172,11 +242,14 @@ class Weight:
 
     @classmethod
     def from_device(cls, q_dev, scale_dev, stream=None):
+        c = _Args()
         lib = load_library()
+        pq = c(q_dev, "q", "i8", (None, None))
         N, K = q_dev.shape
+        ps = c(scale_dev, "scale", "f32", (N,))
+        c.done()
         h = ctypes.c_void_p()
-        _check(lib.sdq_weight_upload_device(_ptr(q_dev), _ptr(scale_dev), N, K, _stream(stream),
-                                            ctypes.byref(h)))
+        _check(lib.sdq_weight_upload_device(pq, ps, N, K, _stream(stream), ctypes.byref(h)))
         return cls(h, N, K)
 
     def export(self):
@@ -204,6 +277,20 @@ def make_epilogue(kind="none", bias=None, gate=None, resid=None, gate_fma=True):
     e.bias = _ptr(bias)
     e.gate = _ptr(gate)
     e.resid = _ptr(resid)
+    return e
+
+
+def _epilogue_args(c, kind, M, N, out, bias, gate, resid, gate_fma):
+    """make_epilogue for device tensors, every operand checked against
+    [M, N] (out: int32 for the raw-accumulator kind, else float32)."""
+    k = EPI_NAMES[kind] if isinstance(kind, str) else int(kind)
+    c(out, "out", "i32" if k == EPI_ACC else "f32", (M, N))
+    e = Epilogue()
+    e.kind = k
+    e.gate_fma = 1 if gate_fma else 0
+    e.bias = c(bias, "bias", "f32", (N,), optional=True)
+    e.gate = c(gate, "gate", "f32", (N,), optional=True)
+    e.resid = c(resid, "resid", "f32", (M, N), optional=True)
     return e
 
 
@@ -241,81 +328,161 @@ def upload_batch(sources, stream=None):
                    arr[i].K) for i in range(n)]
 
 
+def _weight(w, name="w"):
+    if not isinstance(w, Weight) or w.h is None or not w.h.value:
+        raise _bad(f"{name}: not a live Weight")
+    return w.h
+
+
 def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, gate_fma=True,
             stream=None):
-    """out = epilogue(qgemm(A, W) + bias) on device tensors (stream-ordered)."""
-    M, K = A.shape
-    e = make_epilogue(kind, bias, gate, resid, gate_fma)
-    _check(_lib.sdq_qlinear(w.h, _ptr(A), M, K, ctypes.byref(e), _ptr(out), _stream(stream)))
+    """out = epilogue(qgemm(A, W) + bias) on device tensors (stream-ordered).
+    A [M, K] and out [M, N] (int32 for kind "acc"), bias / gate [N], resid
+    [M, N]; all checked before the launch (SdqError on a mismatch)."""
+    c = _Args()
+    h = _weight(w)
+    pa = c(A, "A", "f32", (None, w.K))
+    M = A.shape[0]
+    e = _epilogue_args(c, kind, M, w.N, out, bias, gate, resid, gate_fma)
+    c.done()
+    _check(_lib.sdq_qlinear(h, pa, M, w.K, ctypes.byref(e), _ptr(out), _stream(stream)))
     return out
 
 
 def qgemm(w: Weight, A, out, stream=None):
-    M, K = A.shape
-    _check(_lib.sdq_qgemm(w.h, _ptr(A), M, K, _ptr(out), _stream(stream)))
+    c = _Args()
+    h = _weight(w)
+    pa = c(A, "A", "f32", (None, w.K))
+    M = A.shape[0]
+    po = c(out, "out", "f32", (M, w.N))
+    c.done()
+    _check(_lib.sdq_qgemm(h, pa, M, w.K, po, _stream(stream)))
     return out
+
+
+def _ffn_args(c, fc1, b1, fc2, b2, M, gate, hid):
+    if fc2.K != fc1.N or fc2.N != fc1.K:
+        raise _bad(f"ffn: fc1 [{fc1.N},{fc1.K}] and fc2 [{fc2.N},{fc2.K}] do not chain")
+    D, F = fc1.K, fc1.N
+    return (c(b1, "b1", "f32", (F,), optional=True), c(b2, "b2", "f32", (D,), optional=True),
+            c(gate, "gate", "f32", (D,)), c(hid, "hid", "f32", (M, F)))
 
 
 def ffn(fc1: Weight, b1, fc2: Weight, b2, h, gate, hid, x, gate_fma=True, stream=None):
     """hid = gelu_tanh(mlin(h, fc1)); x = fma(mlin(hid, fc2), gate, x), in place
     (ovi_dit.cpp:218-221), device tensors, stream-ordered."""
+    c = _Args()
+    h1, h2 = _weight(fc1, "fc1"), _weight(fc2, "fc2")
+    ph = c(h, "h", "f32", (None, fc1.K))
     M = h.shape[0]
-    _check(_lib.sdq_ffn(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(h), M, _ptr(gate),
-                        1 if gate_fma else 0, _ptr(hid), _ptr(x), _stream(stream)))
+    pb1, pb2, pg, phid = _ffn_args(c, fc1, b1, fc2, b2, M, gate, hid)
+    px = c(x, "x", "f32", (M, fc1.K))
+    c.done()
+    _check(_lib.sdq_ffn(h1, pb1, h2, pb2, ph, M, pg, 1 if gate_fma else 0, phid, px,
+                        _stream(stream)))
     return x
 
 
 def qlinear_lnmod(w: Weight, x, out, shift, scale, eps=1e-6, kind="none", bias=None, gate=None,
                   resid=None, gate_fma=True, stream=None):
     """out = epilogue(qgemm(mod_rows(layernorm(x), shift, scale), W) + bias)."""
+    c = _Args()
+    hw = _weight(w)
+    px = c(x, "x", "f32", (None, w.K))
     M, K = x.shape
-    e = make_epilogue(kind, bias, gate, resid, gate_fma)
-    _check(_lib.sdq_qlinear_lnmod(w.h, _ptr(x), M, K, _ptr(shift), _ptr(scale), eps,
-                                  ctypes.byref(e), _ptr(out), _stream(stream)))
+    psh, psc = c(shift, "shift", "f32", (K,)), c(scale, "scale", "f32", (K,))
+    e = _epilogue_args(c, kind, M, w.N, out, bias, gate, resid, gate_fma)
+    c.done()
+    _check(_lib.sdq_qlinear_lnmod(hw, px, M, K, psh, psc, eps, ctypes.byref(e), _ptr(out),
+                                  _stream(stream)))
     return out
 
 
 def ffn_lnmod(fc1: Weight, b1, fc2: Weight, b2, x, shift, scale, gate, hid, eps=1e-6,
               gate_fma=True, stream=None):
     """ffn_fwd (ovi_dit.cpp:214-222) with x the norm input and the residual."""
-    M = x.shape[0]
-    _check(_lib.sdq_ffn_lnmod(fc1.h, _ptr(b1), fc2.h, _ptr(b2), _ptr(x), M, _ptr(shift),
-                              _ptr(scale), eps, _ptr(gate), 1 if gate_fma else 0, _ptr(hid),
-                              _stream(stream)))
+    c = _Args()
+    h1, h2 = _weight(fc1, "fc1"), _weight(fc2, "fc2")
+    px = c(x, "x", "f32", (None, fc1.K))
+    M, D = x.shape
+    pb1, pb2, pg, phid = _ffn_args(c, fc1, b1, fc2, b2, M, gate, hid)
+    psh, psc = c(shift, "shift", "f32", (D,)), c(scale, "scale", "f32", (D,))
+    c.done()
+    _check(_lib.sdq_ffn_lnmod(h1, pb1, h2, pb2, px, M, psh, psc, eps, pg, 1 if gate_fma else 0,
+                              phid, _stream(stream)))
     return x
 
 
 def layernorm(x, y, w=None, b=None, eps=1e-6, stream=None):
+    c = _Args()
+    px = c(x, "x", "f32", (None, None))
     M, K = x.shape
-    _check(_lib.sdq_layernorm(_ptr(x), M, K, _ptr(w), _ptr(b), eps, _ptr(y), _stream(stream)))
+    py = c(y, "y", "f32", (M, K))
+    pw, pb = c(w, "w", "f32", (K,), optional=True), c(b, "b", "f32", (K,), optional=True)
+    load_library()
+    c.done()
+    _check(_lib.sdq_layernorm(px, M, K, pw, pb, eps, py, _stream(stream)))
     return y
 
 
 def add_(x, y, stream=None):
-    _check(_lib.sdq_add(_ptr(x), _ptr(y), x.numel(), _stream(stream)))
+    c = _Args()
+    px = c(x, "x", "f32")
+    py = c(y, "y", "f32", tuple(x.shape))
+    load_library()
+    c.done()
+    _check(_lib.sdq_add(px, py, x.numel(), _stream(stream)))
     return x
+
+
+def _cols(c, t, name, col, C):
+    """Address of column `col` of a 2-D row-strided device tensor whose rows
+    hold at least col + C floats."""
+    c(t, name, "f32", contig=False)
+    if col < 0 or col + C > t.shape[1]:
+        raise _bad(f"{name}: columns [{col}, {col + C}) outside its {t.shape[1]} columns")
+    return ctypes.c_void_p(t.data_ptr() + 4 * col)
 
 
 def sdpa(q, k, v, out, heads, qcol=0, kcol=0, vcol=0, stream=None):
     """out = attention(q, k, v) over `heads` heads of 128 columns, taken from
     column offsets qcol / kcol / vcol of the device tensors q, k, v (e.g. one
-    q|k|v tensor passed three times)."""
+    q|k|v tensor passed three times); rows may be strided (stride(0))."""
+    c = _Args()
+    C = heads * 128
+    pq, pk, pv = _cols(c, q, "q", qcol, C), _cols(c, k, "k", kcol, C), _cols(c, v, "v", vcol, C)
+    po = _cols(c, out, "out", 0, C)
     Lq, Lk = q.shape[0], k.shape[0]
-    P = lambda t, c: ctypes.c_void_p(t.data_ptr() + 4 * c)  # noqa: E731
-    _check(_lib.sdq_sdpa(P(q, qcol), q.shape[1], P(k, kcol), k.shape[1], P(v, vcol), v.shape[1],
-                         _ptr(out), out.shape[1], Lq, Lk, heads, 128, _stream(stream)))
+    if v.shape[0] != Lk or out.shape[0] != Lq:
+        raise _bad(f"sdpa: {Lq} queries, {Lk} keys, {v.shape[0]} values, {out.shape[0]} out rows")
+    load_library()
+    c.done()
+    _check(_lib.sdq_sdpa(pq, _ld(q), pk, _ld(k), pv, _ld(v), po, _ld(out), Lq, Lk, heads, 128,
+                         _stream(stream)))
     return out
+
+
+def _rope_table(c, cs, L, name="cs"):
+    if cs is None:
+        return None, 0
+    p = c(cs, name, "f32", (None, None, 2))
+    if cs.shape[0] < L:
+        raise _bad(f"{name}: {cs.shape[0]} rows of (cos, sin) pairs for {L} tokens")
+    return p, int(cs.shape[1])
 
 
 def rmsnorm_rope(x, C, w, heads, cs=None, eps=1e-6, col0=0, stream=None):
     """In place: columns [col0, col0+C) of every row of the device tensor x
-    (rows of x.shape[1] floats) get rmsnorm(w, eps) then RoPE with the
-    (cos, sin) table cs [L, nr, 2] (None: no rotation)."""
-    L, ld = x.shape
-    nr = 0 if cs is None else cs.shape[1]
-    p = ctypes.c_void_p(x.data_ptr() + 4 * col0)
-    _check(_lib.sdq_rmsnorm_rope(p, L, C, ld, _ptr(w), eps, heads, _ptr(cs), nr,
-                                 _stream(stream)))
+    (rows may be strided) get rmsnorm(w, eps) then RoPE with the (cos, sin)
+    table cs [>= L, nr, 2] (None: no rotation)."""
+    c = _Args()
+    p = _cols(c, x, "x", col0, C)
+    L = x.shape[0]
+    pw = c(w, "w", "f32", (C,), optional=True)
+    pcs, nr = _rope_table(c, cs, L)
+    load_library()
+    c.done()
+    _check(_lib.sdq_rmsnorm_rope(p, L, C, _ld(x), pw, eps, heads, pcs, nr, _stream(stream)))
     return x
 
 
@@ -327,12 +494,15 @@ class RmsSeg(ctypes.Structure):
 def rmsnorm_rope_batch(segs, C, heads, eps=1e-6, stream=None):
     """sdq_rmsnorm_rope_batch: segs = [(x, col0, w, cs)], each as in
     rmsnorm_rope (x a device tensor whose rows hold the block at col0)."""
+    c = _Args()
     arr = (RmsSeg * max(len(segs), 1))()
     for i, (x, col0, w, cs) in enumerate(segs):
-        arr[i].x = x.data_ptr() + 4 * col0
-        arr[i].L, arr[i].ld = x.shape[0], x.shape[1]
-        arr[i].w, arr[i].cs = _ptr(w), _ptr(cs)
-        arr[i].nr = 0 if cs is None else cs.shape[1]
+        arr[i].x = _cols(c, x, f"segs[{i}].x", col0, C).value
+        arr[i].L, arr[i].ld = x.shape[0], _ld(x)
+        arr[i].w = c(w, f"segs[{i}].w", "f32", (C,), optional=True)
+        arr[i].cs, arr[i].nr = _rope_table(c, cs, x.shape[0], f"segs[{i}].cs")
+    load_library()
+    c.done()
     _check(_lib.sdq_rmsnorm_rope_batch(arr, len(segs), C, heads, eps, _stream(stream)))
 
 
@@ -351,8 +521,26 @@ def qlinear_host(w: Weight, A: np.ndarray, kind="none", bias=None, gate=None, re
 
 
 def act_quant(A, aq, asc, stream=None):
+    c = _Args()
+    pa = c(A, "A", "f32", (None, None))
     M, K = A.shape
-    _check(_lib.sdq_act_quant(_ptr(A), M, K, _ptr(aq), _ptr(asc), _stream(stream)))
+    pq, ps = c(aq, "aq", "i8", (M, K)), c(asc, "as", "f32", (M,))
+    load_library()
+    c.done()
+    _check(_lib.sdq_act_quant(pa, M, K, pq, ps, _stream(stream)))
+
+
+def qlinear_plan(w: Weight, M: int, kind="none") -> list:
+    """[(record name, first row, rows)] of the GEMM launches sdq_qlinear makes
+    for M rows (sdq_qlinear_plan)."""
+    p = GemmPlan()
+    k = EPI_NAMES[kind] if isinstance(kind, str) else int(kind)
+    _check(load_library().sdq_qlinear_plan(_weight(w), M, k, ctypes.byref(p)))
+    return [(p.name[i].value.decode(), int(p.row0[i]), int(p.rows[i])) for i in range(p.nlaunch)]
+
+
+def version() -> str:
+    return load_library().sdq_version().decode()
 
 
 def profile_begin():
@@ -519,6 +707,7 @@ class DitBlock:
         _hcheck(h.sd_dit_block_create(arr, 1 if fusion else 0, 1 if on_device else 0,
                                       ctypes.byref(self.h)))
         self.fusion = fusion
+        self.dim, self.ffn_dim = int(arr[0].in_), int(arr[10].out)
 
     @classmethod
     def create_many(cls, lins, fusion: bool):
@@ -546,16 +735,32 @@ class DitBlock:
             blk = cls.__new__(cls)
             blk.h = ctypes.c_void_p(handles[b])
             blk.fusion = fusion
+            blk.dim, blk.ffn_dim = int(arr[0].in_), int(arr[10].out)
             out.append(blk)
         return out
 
+    def _io_shapes(self, M, Mc, Mt):
+        d, f = self.dim, self.ffn_dim
+        return {"h_sa": (M, d), "att": (M, d), "gate_sa": (d,), "xq": (M, d), "ctx": (Mc, d),
+                "tn": (Mt, d), "xt": (M, d), "h_ffn": (M, d), "gate_ffn": (d,),
+                "qkv": (M, 3 * d), "cq": (M, d), "ckv": (Mc, 2 * d), "kvt": (Mt, 2 * d),
+                "hid": (M, f), "x": (M, d), "shift_sa": (d,), "scale_sa": (d,),
+                "shift_ffn": (d,), "scale_ffn": (d,)}
+
     def forward(self, stream=None, **io):
-        """io: M, Mc, Mt and the device tensors named in BlockIO."""
+        """io: M, Mc, Mt and the device tensors named in BlockIO; each tensor
+        given is checked against its [rows, cols] before the launch."""
+        c = _Args()
         b = BlockIO()
         b.M, b.Mc, b.Mt = int(io.get("M", 0)), int(io.get("Mc", 0)), int(io.get("Mt", 0))
+        shapes = self._io_shapes(b.M, b.Mc, b.Mt)
         for name in _BLOCK_PTRS:
-            setattr(b, name, _ptr(io.get(name)))
+            t = io.get(name)
+            if t is not None and shapes[name][0] == 0:
+                t = None  # a fusion input of a call without target rows is not read
+            setattr(b, name, c(t, name, "f32", shapes[name], optional=True))
         b.eps = float(io.get("eps", 1e-6))
+        c.done()
         _hcheck(_host.sd_dit_block_forward(self.h, ctypes.byref(b), _stream(stream)))
 
     def ops(self, M, Mc=0, Mt=0) -> float:
@@ -585,15 +790,20 @@ class DitBlock:
         [M,dim] in place, ctx [Mc,dim], e [6,dim], cs [M,nr,2] (RoPE table on
         the device), target [Mt,dim] and cs_tgt for fusion blocks; ws a device
         byte tensor of workspace_bytes (allocated here when None)."""
+        c = _Args()
         import torch
 
+        d = self.dim
         st = BlockStep()
+        st.x = c(x, "x", "f32", (None, d))
+        st.ctx = c(ctx, "ctx", "f32", (None, d))
         st.M, st.Mc = x.shape[0], ctx.shape[0]
+        st.target = c(target, "target", "f32", (None, d), optional=True)
         st.Mt = 0 if target is None else target.shape[0]
         st.heads, st.eps = heads, eps
-        st.x, st.ctx, st.target, st.e = _ptr(x), _ptr(ctx), _ptr(target), _ptr(e)
-        st.cs, st.nr = _ptr(cs), (0 if cs is None else cs.shape[1])
-        st.cs_tgt, st.nr_tgt = _ptr(cs_tgt), (0 if cs_tgt is None else cs_tgt.shape[1])
+        st.e = c(e, "e", "f32", (6, d))
+        st.cs, st.nr = _rope_table(c, cs, st.M)
+        st.cs_tgt, st.nr_tgt = _rope_table(c, cs_tgt, st.Mt, "cs_tgt")
         if ws is None:
             if stream is not None:
                 # a workspace allocated here would be freed on return while
@@ -601,7 +811,12 @@ class DitBlock:
                 raise ValueError("DitBlock.step: pass ws when running on a given stream")
             ws = torch.empty(self.workspace_bytes(st.M, st.Mc, st.Mt), dtype=torch.uint8,
                              device=x.device)
-        st.ws, st.ws_bytes = _ptr(ws), ws.numel() * ws.element_size()
+        st.ws = c(ws, "ws", "u8")
+        st.ws_bytes = ws.numel()
+        need = self.workspace_bytes(st.M, st.Mc, st.Mt)
+        if st.ws_bytes < need:
+            raise _bad(f"ws: workspace too small ({st.ws_bytes} bytes, the block needs {need})")
+        c.done()
         _hcheck(_host.sd_dit_block_step_forward(self.h, ctypes.byref(st), phases, _stream(stream)))
         return x
 

@@ -86,6 +86,24 @@ def test_block_stack_bitexact(sdq_dev, oracle, fusion):
     blk.free()
 
 
+@pytest.mark.parametrize("M,Mt", [(768, 157), (157, 768)])
+def test_block_stack_cfg5_real_width(sdq_dev, oracle, M, Mt):
+    """Config 5's fusion-layer linear stack at the real widths (dim 3072, FFN
+    14336, text context 512): the video branch (M=768 tokens, the 157 audio
+    tokens as fusion target) and the audio branch (M=157, target 768), every
+    output against the oracle."""
+    import sdq
+
+    dim, ffn, Mc = 3072, 14336, 512
+    print(f"[block-cfg5] M={M} Mc={Mc} Mt={Mt}", flush=True)
+    lin = _weights(oracle, dim, ffn, 600, True)
+    inp = _inputs(oracle, M, Mc, Mt, dim, 700 + M)
+    blk = sdq.DitBlock(lin, True)
+    got = _run_block(blk, sdq_dev, inp, M, Mc, Mt, dim, ffn, True)
+    _check_small(oracle, got, lin, inp, True, Mt)
+    blk.free()
+
+
 def test_block_device_weights_match_host_weights(sdq_dev, oracle):
     """The on-device construction path (concatenation + repack on the GPU)
     gives the same block as the host path, bit for bit."""

@@ -122,6 +122,13 @@ def _case(sdq_dev, oracle, dim, ffn, heads, M, Mc, Mt, fusion, rope, seed, phase
     if rope == "3d":
         cs = sdq.rope_table_3d(1, M // 4, 4)[:M] if M % 4 == 0 else sdq.rope_table_1d(M)
         cs_t = sdq.rope_table_1d(Mt, 128, 10000.0, 0.19676) if fusion else None
+    elif rope in ("video", "audio"):
+        # the 256x256/9-frame grids: video latents 3x16x16 = 768 tokens (RoPE-3D),
+        # audio 157 tokens (RoPE-1D with the audio backbone's scaling,
+        # ovi_dit.cpp:330, 656-658)
+        vid = lambda n: sdq.rope_table_3d(3, 16, 16)[:n]  # noqa: E731
+        aud = lambda n: sdq.rope_table_1d(n, 128, 10000.0, 0.19676)  # noqa: E731
+        cs, cs_t = (vid(M), aud(Mt)) if rope == "video" else (aud(M), vid(Mt))
     else:
         cs, cs_t = None, None
     want = _ref_block(oracle, x, ctx, e, lin, nm, heads, cs, fusion, target, cs_t, phases)
@@ -163,6 +170,15 @@ def test_block_real_width(sdq_dev, oracle):
     """dim 3072, ffn 14336, 24 heads (the Wan2.2 5B width), audio-sized rows
     against video-sized fusion target."""
     _case(sdq_dev, oracle, 3072, 14336, 24, 157, 64, 300, True, "3d", 71, tol=5e-2)
+
+
+@pytest.mark.parametrize("M,Mt,rope", [(768, 157, "video"), (157, 768, "audio")])
+def test_block_cfg5_real_width(sdq_dev, oracle, M, Mt, rope):
+    """Config 5's fusion block whole at the real widths: the video branch
+    (768 tokens, RoPE-3D on the 3x16x16 grid) against the 157 audio tokens,
+    and the audio branch (157 tokens, RoPE-1D) against the 768 video tokens;
+    text context 512 rows, 24 heads."""
+    _case(sdq_dev, oracle, 3072, 14336, 24, M, 512, Mt, True, rope, 91 + M, tol=5e-2)
 
 
 def test_block_fusion_no_rope(sdq_dev, oracle):

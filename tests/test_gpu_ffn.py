@@ -8,6 +8,8 @@ M <= 64 (fc1 on the skinny kernel, which writes no maxima: fc2 quantizes
 from scratch). The results must equal the two separate sdq_qlinear calls
 bit for bit (hid and x), and x must equal the oracle's gated fc2 applied to
 the GPU's own hidden state."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -80,8 +82,13 @@ def test_ffn_errors(sdq_dev, oracle):
     hid = torch.empty((8, 256), device=sdq_dev)
     x = torch.zeros((8, 64), device=sdq_dev)
     g = torch.ones(64, device=sdq_dev)
-    with pytest.raises(sdq.SdqError, match="need fc1"):
+    with pytest.raises(sdq.SdqError, match="do not chain"):
         sdq.ffn(w1, None, w2, None, h, g, hid, x)
-    with pytest.raises(sdq.SdqError, match="null gate"):
-        sdq.ffn(w1, None, sdq.Weight.from_host(*_lin(oracle, 64, 256, 3)[:2]), None, h, None,
-                hid, x)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    rc = sdq._lib.sdq_ffn(w1.h, None, w2.h, None, P(h), 8, P(g), 1, P(hid), P(x), None)
+    assert rc == sdq.ERR_INVALID and b"need fc1" in sdq._lib.sdq_last_error()
+    w3 = sdq.Weight.from_host(*_lin(oracle, 64, 256, 3)[:2])
+    with pytest.raises(sdq.SdqError, match="gate: required"):
+        sdq.ffn(w1, None, w3, None, h, None, hid, x)
+    rc = sdq._lib.sdq_ffn(w1.h, None, w3.h, None, P(h), 8, None, 1, P(hid), P(x), None)
+    assert rc == sdq.ERR_INVALID and b"null gate" in sdq._lib.sdq_last_error()

@@ -2,6 +2,8 @@
 sdq_rmsnorm_rope = rmsnorm (tensor.cpp:112-123) then apply_rope
 (blocks.cpp:86-100) on the q / k columns of a q|k|v row, bit-exact, with the
 (cosf, sinf) table of the reference's rope angles."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -122,8 +124,12 @@ def test_sdpa_errors(sdq_dev):
     import sdq
 
     q = torch.zeros((4, 96), device=sdq_dev)
-    with pytest.raises(sdq.SdqError, match="row strides"):
+    # the binding sees the short rows; the C ABI rejects them too
+    with pytest.raises(sdq.SdqError, match="outside its 96 columns"):
         sdq.sdpa(q, q, q, q, 1)  # 96 columns < one head of 128
+    p = ctypes.c_void_p(q.data_ptr())
+    rc = sdq._lib.sdq_sdpa(p, 96, p, 96, p, 96, p, 96, 4, 4, 1, 128, None)
+    assert rc == sdq.ERR_INVALID and b"row strides" in sdq._lib.sdq_last_error()
 
 
 @pytest.mark.parametrize("M,K,affine", [(1, 3072, True), (157, 3072, True), (300, 3072, False),

@@ -4,6 +4,8 @@ shift, scale), W)) against the oracle's layernorm (blocks.cpp:18-43) and
 mod_rows (ovi_dit.cpp:161-172), both pinned bit-exactly to the reference
 build, then its linear. Bit-exact, including zero, constant, tiny, huge
 and NaN rows."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -122,5 +124,11 @@ def test_lnmod_errors(sdq_dev, oracle):
     w = sdq.Weight.from_host(q, s)
     x = torch.zeros((4, 128), device=sdq_dev)
     Y = torch.empty((4, 64), device=sdq_dev)
-    with pytest.raises(sdq.SdqError, match="shift or scale"):
-        sdq.qlinear_lnmod(w, x, Y, None, torch.zeros(128, device=sdq_dev))
+    sc = torch.zeros(128, device=sdq_dev)
+    with pytest.raises(sdq.SdqError, match="shift: required"):
+        sdq.qlinear_lnmod(w, x, Y, None, sc)
+    e = sdq.make_epilogue()
+    rc = sdq._lib.sdq_qlinear_lnmod(w.h, ctypes.c_void_p(x.data_ptr()), 4, 128, None,
+                                    ctypes.c_void_p(sc.data_ptr()), 1e-6, ctypes.byref(e),
+                                    ctypes.c_void_p(Y.data_ptr()), None)
+    assert rc == sdq.ERR_INVALID and b"shift or scale" in sdq._lib.sdq_last_error()

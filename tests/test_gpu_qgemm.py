@@ -2,6 +2,8 @@
 bit-exact quantized activations, int32 accumulators and fp32 outputs."""
 import os
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -105,6 +107,7 @@ SHAPES = [
     (256, 3072, 3072),   # BASELINE cfg1
     (300, 257, 129),     # ragged everything
     (512, 3072, 3072),   # cross-attn K/V on ctx[512]
+    (512, 4096, 3072),   # cfg4 text_embedding.0 on the whole [512, 4096] UMT5 context
     (768, 14336, 3072),  # cfg2 FFN down
     (70, 4200, 300),     # long rows, last 32-fragment group of the quantizer partial
     (33, 16384, 64),     # the longest row the single-pass quantizer keeps in registers
@@ -282,8 +285,13 @@ def test_errors_are_reported(sdq_dev):
     w = sdq.Weight.from_host(np.ones((8, 16), np.int8), np.ones(8, np.float32))
     A = torch.zeros((4, 15), device=sdq_dev)
     Y = torch.zeros((4, 8), device=sdq_dev)
-    with pytest.raises(sdq.SdqError, match="K mismatch"):
+    with pytest.raises(sdq.SdqError, match=r"A: shape \(4, 15\)"):
         sdq.qlinear(w, A, Y)
+    # the C ABI's own check, without the binding in front of it
+    e = sdq.make_epilogue()
+    rc = sdq._lib.sdq_qlinear(w.h, ctypes.c_void_p(A.data_ptr()), 4, 15, ctypes.byref(e),
+                              ctypes.c_void_p(Y.data_ptr()), None)
+    assert rc == sdq.ERR_INVALID and b"K mismatch" in sdq._lib.sdq_last_error()
     with pytest.raises(sdq.SdqError, match="GATED"):
         sdq.qlinear(w, torch.zeros((4, 16), device=sdq_dev), Y, kind="gated")
 

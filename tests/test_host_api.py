@@ -210,3 +210,63 @@ def test_rope_table_1d_matches_oracle(oracle, L, scaling):
     assert np.array_equal(cs.view(np.uint32), want.reshape(cs.shape).view(np.uint32))
     with pytest.raises(ValueError):
         sdq.rope_table_1d(L, 127)
+
+
+REF_CALLER = os.path.join(os.path.dirname(PKG), "oracle", "_ref", "ref_caller")
+
+
+def _read_ref_caller(path):
+    raw = open(path, "rb").read()
+    M, K, N = struct.unpack_from("<3q", raw, 0)
+    o = 24
+    A = np.frombuffer(raw, np.float32, M * K, o).reshape(M, K)
+    o += 4 * M * K
+    Wq = np.frombuffer(raw, np.int8, N * K, o).reshape(N, K)
+    o += N * K
+    sc = np.frombuffer(raw, np.float32, N, o)
+    o += 4 * N
+    out = np.frombuffer(raw, np.float32, M * N, o).reshape(M, N)
+    assert o + 4 * M * N == len(raw)
+    return A, Wq, sc, out
+
+
+def test_ref_caller_links_without_a_second_tensor():
+    """The drop-in link (CPU): libsd_qgemm.so defines sd::qgemm and leaves
+    every sd::Tensor member undefined, and the reference-shaped caller built
+    with the reference's tensor.cpp loads it and not libsd_host.so."""
+    lib = os.path.join(PKG, "lib", "libsd_qgemm.so")
+    syms = subprocess.run(["nm", "-DC", lib], capture_output=True, text=True, check=True).stdout
+    defined = [ln for ln in syms.splitlines() if " T " in ln or " W " in ln]
+    assert any("sd::qgemm(sd::Tensor const&" in ln for ln in defined)
+    assert not any("sd::Tensor::" in ln for ln in defined), "libsd_qgemm defines Tensor members"
+    assert any(" U sd::Tensor::Tensor(" in ln for ln in syms.splitlines())
+    if not os.path.exists(REF_CALLER):
+        pytest.skip("oracle/_ref/ref_caller not built (reference sources absent)")
+    ldd = subprocess.run(["ldd", REF_CALLER], capture_output=True, text=True, check=True).stdout
+    assert "libsd_qgemm.so" in ldd and "libsdq.so" in ldd and "libsd_host" not in ldd
+    own = subprocess.run(["nm", "-C", REF_CALLER], capture_output=True, text=True,
+                         check=True).stdout
+    # the Tensor members are the reference's own (tensor.cpp), defined once, in the
+    # program (the destructor's complete and base-object symbols share one address)
+    addrs = {ln.split()[0] for ln in own.splitlines() if " T sd::Tensor::~Tensor()" in ln}
+    assert len(addrs) == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(17, 31, 13), (64, 1024, 512), (300, 3072, 1000),
+                                   (2100, 640, 384)])
+def test_ref_caller_bitexact(tmp_path, oracle, M, K, N):
+    """A program written against the reference's src/core/tensor.h, linked with
+    the reference's tensor.cpp and libsd_qgemm.so, gets the reference's qgemm
+    output bit for bit (test_core.cpp's seeds: randu 7+M for A, 13+N for W)."""
+    if not os.path.exists(REF_CALLER):
+        pytest.skip("oracle/_ref/ref_caller not built (reference sources absent)")
+    out = tmp_path / "o.bin"
+    r = subprocess.run([REF_CALLER] + [str(v) for v in (M, K, N, 7 + M, 13 + N, out)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    A, Wq, sc, got = _read_ref_caller(out)
+    assert_bitexact(got, oracle.qgemm(A, Wq, sc), f"ref_caller {M}x{K}x{N}")
+    import pyoracle
+    if pyoracle.Ref.available():
+        assert_bitexact(got, pyoracle.Ref().qgemm(A, Wq, sc), "reference build")
