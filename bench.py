@@ -46,7 +46,7 @@ def parse():
                     help="after the W warmup steps, further untimed steps until this much wall "
                          "time has passed since the first warmup step (the shader clock's "
                          "power-limit transient; 0 = none)")
-    ap.add_argument("--counters-json", default=os.path.join(ROOT, "profiles", "ns_counters.json"),
+    ap.add_argument("--counters-json", default=os.path.join(ROOT, "profiles", "qgemm_ns_counters.json"),
                     help="rocprofv3 counter summary (written by --summarize-counters); its "
                          "figures are reported only when it was recorded on this library build")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
@@ -59,6 +59,9 @@ def parse():
                          "cross: text/cross-attention and AdaLN projections; twin: the "
                          "full twin-backbone linear stack (28 and 30 layers); load: weight "
                          "upload of 8 blocks from host memory")
+    ap.add_argument("--pack-dir", default=None,
+                    help="--config load: directory for the temporary .sdcpp file (default: the "
+                         "system temp directory)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run a few steps plus a 1 GiB torch copy (the counter calibration "
                          "kernel) and exit; used under rocprofv3 --pmc")
@@ -340,75 +343,85 @@ def bench_twin(torch, sdq, args):
     # the other's snapshot (two streams). 30 layers.
     import numpy as np
 
-    layers = 30
+    layers, slg = 30, 9  # gen.cpp:258: skip-layer guidance at layer 9
     heads = dim // 128
     ones = {n: np.ones(dim, np.float32) for n in sdq.NORM_NAMES}
     for b in blocks[:2 * layers]:
         b.set_norms(ones)
-    cs_v = torch.from_numpy(sdq.rope_table_3d(3, 16, 16)).to(dev)  # 768 video tokens
-    cs_a = torch.from_numpy(sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)).to(dev)
-    xv, xa = torch.randn((Mv, dim), device=dev), torch.randn((Ma, dim), device=dev)
-    og_v, og_a = torch.empty_like(xv), torch.empty_like(xa)
-    ctx_v, ctx_a = torch.randn((Mc, dim), device=dev), torch.randn((Mc, dim), device=dev)
+    tab_v = sdq.rope_table_3d(3, 16, 16)  # 768 video tokens
+    tab_a = sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)
     e_v = [torch.randn((6, dim), device=dev) * 0.1 for _ in range(layers)]
     e_a = [torch.randn((6, dim), device=dev) * 0.1 for _ in range(layers)]
-    ws_v = torch.empty(blocks[0].workspace_bytes(Mv, Mc, Ma), dtype=torch.uint8, device=dev)
-    ws_a = torch.empty(blocks[1].workspace_bytes(Ma, Mc, Mv), dtype=torch.uint8, device=dev)
 
-    def fn_full():
-        cur = torch.cuda.current_stream()
-        sv.wait_stream(cur)
-        sa.wait_stream(cur)
-        for i in range(layers):
-            bv, ba = blocks[2 * i], blocks[2 * i + 1]
-            ba.step(xa, ctx_a, e_a[i], heads, cs=cs_a, ws=ws_a, phases=sdq.SELF,
-                    stream=sa.cuda_stream)
-            bv.step(xv, ctx_v, e_v[i], heads, cs=cs_v, ws=ws_v, phases=sdq.SELF,
-                    stream=sv.cuda_stream)
-            with torch.cuda.stream(sa):
-                og_a.copy_(xa)
-            with torch.cuda.stream(sv):
-                og_v.copy_(xv)
-            sv.wait_stream(sa)
-            sa.wait_stream(sv)
-            ba.step(xa, ctx_a, e_a[i], heads, cs=cs_a, target=og_v, cs_tgt=cs_v, ws=ws_a,
-                    phases=sdq.CROSS_FFN, stream=sa.cuda_stream)
-            bv.step(xv, ctx_v, e_v[i], heads, cs=cs_v, target=og_a, cs_tgt=cs_a, ws=ws_v,
-                    phases=sdq.CROSS_FFN, stream=sv.cuda_stream)
-            sv.wait_stream(sa)
-            sa.wait_stream(sv)
-        cur.wait_stream(sv)
-        cur.wait_stream(sa)
-    ms_full = _timed(torch, fn_full, 2, max(args.steps // 10, 3))
-    assert bool(torch.isfinite(xv).all()) and bool(torch.isfinite(xa).all())
+    def whole(batch, skip):
+        """The 30-layer forward over `batch` stacked passes (batch 2: the
+        conditional and unconditional forwards of one guidance step, each with
+        its own text context; the unconditional half skips layer `skip`,
+        which then runs on the conditional half alone)."""
+        cs_v = torch.from_numpy(np.concatenate([tab_v] * batch)).to(dev)
+        cs_a = torch.from_numpy(np.concatenate([tab_a] * batch)).to(dev)
+        xv = torch.randn((batch * Mv, dim), device=dev)
+        xa = torch.randn((batch * Ma, dim), device=dev)
+        og_v, og_a = torch.empty_like(xv), torch.empty_like(xa)
+        ctx_v = torch.randn((batch * Mc, dim), device=dev)
+        ctx_a = torch.randn((batch * Mc, dim), device=dev)
+        ws_v = torch.empty(blocks[0].workspace_bytes(batch * Mv, batch * Mc, batch * Ma),
+                           dtype=torch.uint8, device=dev)
+        ws_a = torch.empty(blocks[1].workspace_bytes(batch * Ma, batch * Mc, batch * Mv),
+                           dtype=torch.uint8, device=dev)
+
+        def fn():
+            cur = torch.cuda.current_stream()
+            sv.wait_stream(cur)
+            sa.wait_stream(cur)
+            for i in range(layers):
+                n = batch
+                if i == skip:
+                    if batch == 1:
+                        continue  # the reference's `continue` (ovi_dit.cpp:713)
+                    n = 1
+                bv, ba = blocks[2 * i], blocks[2 * i + 1]
+                xv_, xa_, ov, oa = xv[:n * Mv], xa[:n * Ma], og_v[:n * Mv], og_a[:n * Ma]
+                cv, ca = ctx_v[:n * Mc], ctx_a[:n * Mc]
+                tv, ta = cs_v[:n * Mv], cs_a[:n * Ma]
+                ba.step(xa_, ca, e_a[i], heads, cs=ta, ws=ws_a, phases=sdq.SELF,
+                        stream=sa.cuda_stream, batch=n)
+                bv.step(xv_, cv, e_v[i], heads, cs=tv, ws=ws_v, phases=sdq.SELF,
+                        stream=sv.cuda_stream, batch=n)
+                with torch.cuda.stream(sa):
+                    oa.copy_(xa_)
+                with torch.cuda.stream(sv):
+                    ov.copy_(xv_)
+                sv.wait_stream(sa)
+                sa.wait_stream(sv)
+                ba.step(xa_, ca, e_a[i], heads, cs=ta, target=ov, cs_tgt=tv, ws=ws_a,
+                        phases=sdq.CROSS_FFN, stream=sa.cuda_stream, batch=n)
+                bv.step(xv_, cv, e_v[i], heads, cs=tv, target=oa, cs_tgt=ta, ws=ws_v,
+                        phases=sdq.CROSS_FFN, stream=sv.cuda_stream, batch=n)
+                sv.wait_stream(sa)
+                sa.wait_stream(sv)
+            cur.wait_stream(sv)
+            cur.wait_stream(sa)
+        ms = _timed(torch, fn, 2, max(args.steps // 10, 3))
+        assert bool(torch.isfinite(xv).all()) and bool(torch.isfinite(xa).all())
+        return ms, fn
+
+    ms_full, fn_full = whole(1, -1)
     ops_full = sum(blocks[2 * i].step_ops(Mv, Mc, Ma) + blocks[2 * i + 1].step_ops(Ma, Mc, Mv)
                    for i in range(layers))
     res["whole_blocks_30"] = {"ms_per_pass": round(ms_full, 4),
                               "TFLOPs": round(ops_full / ms_full / 1e9, 2),
                               "kernel_ms_per_pass": _kernel_split(sdq, fn_full, 1)}
-    # CFG batching (denoise.cpp:95-98 runs the conditional and unconditional
-    # forwards one after the other): both forwards' rows stacked, 2M tokens
-    # and 2 text contexts per Linear, one weight stream for the pair
-    # (bit-identical per row; the attention between the Linears keeps the
-    # two halves apart). 28 layers, two streams as above.
-    layers = 28
-    iov2 = _block_io(torch, dev, 2 * Mv, 2 * Mc, 2 * Ma, dim, ffn)
-    ioa2 = _block_io(torch, dev, 2 * Ma, 2 * Mc, 2 * Mv, dim, ffn)
-
-    def fn_cfg():
-        cur = torch.cuda.current_stream()
-        sv.wait_stream(cur)
-        sa.wait_stream(cur)
-        for i in range(layers):
-            blocks[2 * i].forward(stream=sv.cuda_stream, **iov2)
-            blocks[2 * i + 1].forward(stream=sa.cuda_stream, **ioa2)
-            sv.wait_stream(sa)
-            sa.wait_stream(sv)
-        cur.wait_stream(sv)
-        cur.wait_stream(sa)
-    ms_cfg = _timed(torch, fn_cfg, 2, max(args.steps // 10, 3))
-    res["cfg_batched_28"] = {"ms_per_cond_uncond_pair": round(ms_cfg, 4),
-                             "two_separate_passes_ms": round(2 * res["layers"]["28"]["ms_per_pass"], 4)}
+    # Classifier-free guidance (denoise.cpp:95-98 runs the conditional pass,
+    # then the unconditional one with SLG): both passes' rows stacked through
+    # the whole forward (sd_dit_block_step_forward_batched; bit-identical to
+    # the two passes), against the two passes one after the other.
+    ms_uncond, _ = whole(1, slg)
+    ms_pair, fn_pair = whole(2, slg)
+    res["cfg_pair_whole_30"] = {"ms_per_cond_uncond_pair": round(ms_pair, 4),
+                                "two_separate_passes_ms": round(ms_full + ms_uncond, 4),
+                                "slg_layer": slg,
+                                "kernel_ms_per_pair": _kernel_split(sdq, fn_pair, 1)}
     res["value"] = res["layers"]["28"]["ms_per_pass"]
     return res
 
@@ -448,11 +461,109 @@ def bench_load(torch, sdq, args):
     t_many = time.perf_counter() - t0
     for blk in many:
         blk.free()
+    files = _bench_pack_file(torch, sdq, args, lins, dim, ffn, nbytes)
     return {"metric": "DiT block weight upload from host memory", "unit": "GB/s",
             "value": round(nbytes / t_many / 1e9, 2), "dtype": "int8",
             "config": {"workload": f"{nb} blocks dim={dim} ffn={ffn} fusion, {nbytes / 1e9:.2f} GB",
                        "streamed_s": round(t_many, 3), "block_by_block_s": round(t_one, 3),
-                       "block_by_block_GBps": round(nbytes / t_one / 1e9, 2)}}
+                       "block_by_block_GBps": round(nbytes / t_one / 1e9, 2),
+                       "from_pack_file": files}}
+
+
+_PACK_NAMES = {"q": "self_attn.q", "k": "self_attn.k", "v": "self_attn.v", "o": "self_attn.o",
+               "cq": "cross_attn.q", "ck": "cross_attn.k", "cv": "cross_attn.v",
+               "co": "cross_attn.o", "kf": "cross_attn.k_fusion", "vf": "cross_attn.v_fusion",
+               "fc1": "ffn.0", "fc2": "ffn.2"}
+_PACK_VECS = ("self_attn.norm_q.weight", "self_attn.norm_k.weight", "cross_attn.norm_q.weight",
+              "cross_attn.norm_k.weight", "norm3.weight", "norm3.bias",
+              "cross_attn.norm_k_fusion.weight", "cross_attn.pre_attn_norm_fusion.weight",
+              "cross_attn.pre_attn_norm_fusion.bias")
+
+
+def _write_int8_pack(path, lins, dim):
+    """A .sdcpp v1 file (src/serde/sdcpp.cpp:1-8) of already-quantized blocks
+    under load_impl's names: each Linear's int8 rows then its f32 scales
+    (code 0), biases / norms / modulation raw f32 (code 1), back to back."""
+    import struct
+
+    import numpy as np
+
+    ents = []
+    for b, lin in enumerate(lins):
+        B = f"video_model.blocks.{b}."
+        for k, (q, s, bias) in lin.items():
+            ents.append((B + _PACK_NAMES[k] + ".weight", 0, q.shape, [q, s]))
+            ents.append((B + _PACK_NAMES[k] + ".bias", 1, bias.shape, [bias]))
+        for n in _PACK_VECS:
+            ents.append((B + n, 1, (dim,), [np.ones(dim, np.float32)]))
+        ents.append((B + "modulation.modulation", 1, (1, 6, dim), [np.zeros(6 * dim, np.float32)]))
+    with open(path, "wb") as f:
+        f.write(b"SDCP" + struct.pack("<II", 1, len(ents)))
+        off = 0
+        for name, code, dims, parts in ents:
+            nb = name.encode()
+            f.write(struct.pack("<I", len(nb)) + nb + struct.pack("<BI", code, len(dims)))
+            f.write(struct.pack(f"<{len(dims)}q", *dims) + struct.pack("<Q", off))
+            off += sum(p.nbytes for p in parts)
+        for _, _, _, parts in ents:
+            for p in parts:
+                f.write(np.ascontiguousarray(p).tobytes())
+        f.flush()
+        os.fsync(f.fileno())
+
+
+def _drop_cache(path):
+    """Evicts the file's clean pages from the page cache (no privileges
+    needed for a file of one's own); False when the filesystem keeps them."""
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+    finally:
+        os.close(fd)
+
+
+def _fs_type(path):
+    best, fs = "", "?"
+    try:
+        with open("/proc/mounts") as f:
+            for ln in f:
+                dev, mnt, typ = ln.split()[:3]
+                if path.startswith(mnt) and len(mnt) > len(best):
+                    best, fs = mnt, typ
+    except OSError:
+        pass
+    return fs
+
+
+def _bench_pack_file(torch, sdq, args, lins, dim, ffn, nbytes):
+    """The same blocks loaded whole from a .sdcpp file (sd_dit_blocks_from_pack):
+    sequential file reads into the pinned ring vs load_sdcpp's mapping, each
+    from a cold page cache (the file's pages evicted first) and warm."""
+    import tempfile
+
+    d = args.pack_dir or tempfile.gettempdir()
+    path = os.path.join(d, f"sdq_bench_{os.getpid()}.sdcpp")
+    _write_int8_pack(path, lins, dim)
+    try:
+        out = {"file_bytes": os.path.getsize(path), "filesystem": _fs_type(os.path.abspath(path))}
+        layers = list(range(len(lins)))
+        for mode, file_reads in (("file_reads", True), ("mapped", False)):
+            for temp in ("cold", "warm"):
+                if temp == "cold":
+                    _drop_cache(path)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                blocks = sdq.DitBlock.from_pack(path, "video_model.", layers, dim, ffn, True,
+                                                file_reads)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                for b in blocks:
+                    b.free()
+                out[f"{mode}_{temp}_s"] = round(dt, 3)
+                out[f"{mode}_{temp}_GBps"] = round(nbytes / dt / 1e9, 2)
+        return out
+    finally:
+        os.unlink(path)
 
 
 def cpu_baseline(args, K, N):
@@ -676,7 +787,7 @@ def _short_kernel(name):
         return "qgemm_tail128"
     if "act_quant_units_kernel" in name:
         return "act_quant"
-    if "copyBuffer" in name or "copy" in name.lower():
+    if "copyBuffer" in name:  # the runtime's device-to-device copy (the 1 GiB calibration)
         return "copy"
     return None
 

@@ -119,6 +119,26 @@ typedef struct sdq_weight_src {
   int64_t K;
 } sdq_weight_src;
 int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out);
+/* The same from a .sdcpp file, by file offsets instead of memory views: the
+ * parts' int8 rows and scales are read with large sequential reads (several
+ * threads) straight into the pinned staging ring, so a cold pack is read
+ * from disk once, in order, with no page faults through a mapping.
+ * q_off / scale_off: absolute file offsets (the pack index's data and scale
+ * offsets; scales right after the int8 rows in .sdcpp v1, any alignment).
+ * Same device contents as sdq_weight_upload_batch on the mapped views.
+ * Errors: SDQ_ERR_NOTFOUND (cannot open), SDQ_ERR_FORMAT (a part outside the
+ * file, a short read).
+ * Replaces: the page-in of load_sdcpp's mapped views (src/serde/sdcpp.cpp:
+ * 57-60) followed by the per-tensor upload, for a whole pack. */
+typedef struct sdq_weight_fsrc {
+  int nparts;              /* 1..4 */
+  uint64_t q_off[4];       /* [rows[i], K] int8 */
+  uint64_t scale_off[4];   /* [rows[i]] f32 */
+  int64_t rows[4];
+  int64_t K;
+} sdq_weight_fsrc;
+int sdq_weight_upload_file(const char* path, const sdq_weight_fsrc* src, int n, void* stream,
+                           sdq_weight** out);
 int sdq_weight_free(sdq_weight* w);
 int sdq_weight_dims(const sdq_weight* w, int64_t* N, int64_t* K);
 /* Unpack the device copy back to row-major int8 [N,K] + f32 [N] in host
@@ -220,6 +240,19 @@ int sdq_add(float* x, const float* y, int64_t n, void* stream);
 int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
              float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
              void* stream);
+
+/* sdq_sdpa over `batch` sequences stacked along the rows: sequence b's
+ * queries are rows [b*Lq, (b+1)*Lq) of q (and of out), its keys and values
+ * rows [b*Lk, (b+1)*Lk) of k and v; each sequence attends only to its own
+ * keys, as `batch` separate sdq_sdpa calls would (same results, bit for
+ * bit), in one launch. For the conditional and unconditional forwards of a
+ * classifier-free-guidance step run as one stacked forward (the two passes
+ * of denoise.cpp:95-98, each with its own text context).
+ * Replaces: the sdpa calls of two OviDit::forward passes (ovi_dit.cpp:186,
+ * 200, 241, 249). */
+int sdq_sdpa_batched(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                     int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
+                     int head_dim, int batch, void* stream);
 
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);

@@ -6,9 +6,13 @@
 // failures as a status code plus a thread-local message and never throws
 // (the reference's loader throws std::runtime_error, src/serde/sdcpp.cpp:27;
 // its qgemm has no error path at all, src/core/qgemm.cpp:73-142).
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -519,35 +523,27 @@ void par_memcpy(char* dst, const char* src, size_t bytes, int threads) {
 
 }  // namespace
 
-int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out) {
-  if (!out || (n > 0 && !src)) return set_error(SDQ_ERR_INVALID, "null src or out");
-  if (n < 0) return set_error(SDQ_ERR_INVALID, "negative count");
-  for (int i = 0; i < n; i++) out[i] = nullptr;
-  if (n == 0) return SDQ_OK;
-  int dev = -1;
-  int rc = current_device(&dev);
-  if (rc) return rc;
-  if ((rc = ensure_device(dev))) return rc;
-  // layout of one staged weight: int8 rows, then the scales at soff
-  std::vector<int64_t> Ns(n);
+}  // extern "C"
+
+namespace {
+
+// Streams n weights (weight i: N[i] x K[i] int8 rows + N[i] scales) to the
+// device through a ring of pinned staging slots: fill(i, slot, soff) writes
+// weight i's int8 rows at slot[0..) and its scales at slot[soff..) on the
+// host (several threads), the H2D copy runs on a copy stream, and the GPU
+// repack of the previous weight runs on `s` meanwhile. On error no handle is
+// returned.
+template <class Fill>
+int upload_ring(int dev, const std::vector<int64_t>& Ns, const std::vector<int64_t>& Ks, Fill fill,
+                hipStream_t s, sdq_weight** out) {
+  const int n = (int)Ns.size();
   size_t slot = 0;
-  for (int i = 0; i < n; i++) {
-    const sdq_weight_src& w = src[i];
-    if (w.nparts < 1 || w.nparts > 4 || w.K < 0)
-      return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": bad parts or K");
-    int64_t N = 0;
-    for (int p = 0; p < w.nparts; p++) {
-      if (w.rows[p] < 0 || (w.rows[p] * w.K > 0 && !w.q[p]) || (w.rows[p] > 0 && !w.scale[p]))
-        return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": null part");
-      N += w.rows[p];
-    }
-    Ns[i] = N;
-    slot = std::max(slot, (size_t)round_up(N * w.K, 256) + (size_t)N * 4 + 16);
-  }
+  for (int i = 0; i < n; i++)
+    slot = std::max(slot, (size_t)round_up(Ns[i] * Ks[i], 256) + (size_t)Ns[i] * 4 + 16);
   constexpr int kSlots = 3;
   const int nslots = std::min(n, kSlots);
-  const int threads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
-  hipStream_t s = static_cast<hipStream_t>(stream), cs = nullptr;
+  int rc = SDQ_OK;
+  hipStream_t cs = nullptr;
   std::vector<char*> pin(nslots, nullptr), dst(nslots, nullptr);
   std::vector<hipEvent_t> copied(nslots, nullptr), repacked(nslots, nullptr);
   hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
@@ -558,20 +554,13 @@ int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_
     if (e == hipSuccess) e = hipEventCreateWithFlags(&repacked[k], hipEventDisableTiming);
   }
   for (int i = 0; i < n && e == hipSuccess && rc == SDQ_OK; i++) {
-    const sdq_weight_src& w = src[i];
     const int k = i % nslots;
-    const int64_t N = Ns[i], K = w.K;
+    const int64_t N = Ns[i], K = Ks[i];
     const size_t soff = (size_t)round_up(N * K, 256);
     if ((rc = alloc_weight(dev, N, K, &out[i]))) break;
     // the pinned slot is free once its previous H2D copy has finished
     if (i >= nslots && (e = hipEventSynchronize(copied[k])) != hipSuccess) break;
-    size_t r = 0;
-    for (int p = 0; p < w.nparts; p++) {
-      par_memcpy(pin[k] + r * (size_t)K, reinterpret_cast<const char*>(w.q[p]),
-                 (size_t)(w.rows[p] * K), threads);
-      std::memcpy(pin[k] + soff + r * 4, w.scale[p], (size_t)w.rows[p] * 4);
-      r += (size_t)w.rows[p];
-    }
+    if ((rc = fill(i, pin[k], soff))) break;
     // the device slot is free once the repack that read it has run
     if (i >= nslots && (e = hipStreamWaitEvent(cs, repacked[k], 0)) != hipSuccess) break;
     if ((e = hipMemcpyAsync(dst[k], pin[k], soff + (size_t)N * 4, hipMemcpyHostToDevice, cs)) !=
@@ -602,6 +591,140 @@ int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_
     }
     t_err = msg;
   }
+  return rc;
+}
+
+int upload_threads() {
+  return (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+}
+
+// pread of [off, off + bytes) into dst, split over up to `threads` threads
+// (large sequential reads; a page-cache or NVMe read runs faster in
+// parallel). Returns false on a short read or an I/O error.
+bool par_pread(int fd, char* dst, uint64_t off, size_t bytes, int threads) {
+  constexpr size_t kMinPerThread = size_t(8) << 20;
+  auto span = [fd](char* d, uint64_t o, size_t b) {
+    while (b) {
+      const ssize_t got = ::pread(fd, d, b, (off_t)o);
+      if (got < 0 && errno == EINTR) continue;
+      if (got <= 0) return false;
+      d += got;
+      o += (uint64_t)got;
+      b -= (size_t)got;
+    }
+    return true;
+  };
+  const int t = (int)std::min<size_t>((size_t)threads, std::max<size_t>(1, bytes / kMinPerThread));
+  if (t <= 1) return span(dst, off, bytes);
+  std::vector<std::thread> pool;
+  std::vector<char> ok(t, 0);
+  const size_t chunk = round_up((int64_t)((bytes + t - 1) / t), 4096);
+  for (int i = 0; i < t; i++) {
+    const size_t a = std::min(bytes, (size_t)i * chunk), b = std::min(bytes, a + chunk);
+    pool.emplace_back([&, i, a, b] { ok[i] = span(dst + a, off + a, b - a); });
+  }
+  for (auto& th : pool) th.join();
+  return std::all_of(ok.begin(), ok.end(), [](char v) { return v != 0; });
+}
+
+}  // namespace
+
+extern "C" {
+
+int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out) {
+  if (!out || (n > 0 && !src)) return set_error(SDQ_ERR_INVALID, "null src or out");
+  if (n < 0) return set_error(SDQ_ERR_INVALID, "negative count");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  if (n == 0) return SDQ_OK;
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  std::vector<int64_t> Ns(n), Ks(n);
+  for (int i = 0; i < n; i++) {
+    const sdq_weight_src& w = src[i];
+    if (w.nparts < 1 || w.nparts > 4 || w.K < 0)
+      return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": bad parts or K");
+    int64_t N = 0;
+    for (int p = 0; p < w.nparts; p++) {
+      if (w.rows[p] < 0 || (w.rows[p] * w.K > 0 && !w.q[p]) || (w.rows[p] > 0 && !w.scale[p]))
+        return set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": null part");
+      N += w.rows[p];
+    }
+    Ns[i] = N;
+    Ks[i] = w.K;
+  }
+  const int threads = upload_threads();
+  auto fill = [&](int i, char* pin, size_t soff) {
+    const sdq_weight_src& w = src[i];
+    size_t r = 0;
+    for (int p = 0; p < w.nparts; p++) {
+      par_memcpy(pin + r * (size_t)w.K, reinterpret_cast<const char*>(w.q[p]),
+                 (size_t)(w.rows[p] * w.K), threads);
+      std::memcpy(pin + soff + r * 4, w.scale[p], (size_t)w.rows[p] * 4);
+      r += (size_t)w.rows[p];
+    }
+    return SDQ_OK;
+  };
+  return upload_ring(dev, Ns, Ks, fill, static_cast<hipStream_t>(stream), out);
+}
+
+int sdq_weight_upload_file(const char* path, const sdq_weight_fsrc* src, int n, void* stream,
+                           sdq_weight** out) {
+  if (!path || !out || (n > 0 && !src)) return set_error(SDQ_ERR_INVALID, "null path, src or out");
+  if (n < 0) return set_error(SDQ_ERR_INVALID, "negative count");
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  if (n == 0) return SDQ_OK;
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const int fd = ::open(path, O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return set_error(SDQ_ERR_NOTFOUND, std::string("cannot open ") + path);
+  struct stat st;
+  if (::fstat(fd, &st) != 0) {
+    ::close(fd);
+    return set_error(SDQ_ERR_FORMAT, std::string("cannot stat ") + path);
+  }
+  const uint64_t size = (uint64_t)st.st_size;
+  std::vector<int64_t> Ns(n), Ks(n);
+  for (int i = 0; i < n && rc == SDQ_OK; i++) {
+    const sdq_weight_fsrc& w = src[i];
+    if (w.nparts < 1 || w.nparts > 4 || w.K < 0) {
+      rc = set_error(SDQ_ERR_INVALID, "weight source " + std::to_string(i) + ": bad parts or K");
+      break;
+    }
+    int64_t N = 0;
+    for (int p = 0; p < w.nparts; p++) {
+      const uint64_t qb = (uint64_t)(w.rows[p] * w.K), sb = (uint64_t)w.rows[p] * 4;
+      if (w.rows[p] < 0 || w.q_off[p] > size || qb > size - w.q_off[p] ||
+          w.scale_off[p] > size || sb > size - w.scale_off[p]) {
+        rc = set_error(SDQ_ERR_FORMAT, "weight source " + std::to_string(i) + ": part " +
+                                           std::to_string(p) + " lies outside " + path);
+        break;
+      }
+      N += w.rows[p];
+    }
+    Ns[i] = N;
+    Ks[i] = w.K;
+  }
+  if (rc == SDQ_OK) {
+    (void)::posix_fadvise(fd, 0, 0, POSIX_FADV_SEQUENTIAL);
+    const int threads = upload_threads();
+    auto fill = [&](int i, char* pin, size_t soff) {
+      const sdq_weight_fsrc& w = src[i];
+      size_t r = 0;
+      for (int p = 0; p < w.nparts; p++) {
+        if (!par_pread(fd, pin + r * (size_t)w.K, w.q_off[p], (size_t)(w.rows[p] * w.K), threads) ||
+            !par_pread(fd, pin + soff + r * 4, w.scale_off[p], (size_t)w.rows[p] * 4, 1))
+          return set_error(SDQ_ERR_FORMAT, std::string("short read from ") + path);
+        r += (size_t)w.rows[p];
+      }
+      return SDQ_OK;
+    };
+    rc = upload_ring(dev, Ns, Ks, fill, static_cast<hipStream_t>(stream), out);
+  }
+  ::close(fd);
   return rc;
 }
 
@@ -797,7 +920,14 @@ int sdq_add(float* x, const float* y, int64_t n, void* stream) {
 int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
              float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
              void* stream) {
+  return sdq_sdpa_batched(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, head_dim, 1, stream);
+}
+
+int sdq_sdpa_batched(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                     int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
+                     int head_dim, int batch, void* stream) {
   if (Lq < 0 || Lk < 0) return set_error(SDQ_ERR_INVALID, "negative Lq or Lk");
+  if (batch < 1 || batch > 65535) return set_error(SDQ_ERR_INVALID, "sdpa: batch must be 1..65535");
   if (Lq == 0) return SDQ_OK;
   if (Lk == 0) return set_error(SDQ_ERR_INVALID, "sdpa: no keys");
   if (head_dim != 128) return set_error(SDQ_ERR_INVALID, "sdpa: head_dim must be 128");
@@ -815,7 +945,7 @@ int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const flo
   if ((rc = ensure_device(dev))) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s);
+  hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s, batch);
   if (e != hipSuccess) return hip_error(e, "sdpa launch");
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);

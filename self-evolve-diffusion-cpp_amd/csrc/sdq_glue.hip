@@ -237,6 +237,12 @@ __global__ void __launch_bounds__(NW * 64)
 sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
             const float* __restrict__ V, int64_t ldv, float* __restrict__ O, int64_t ldo,
             int64_t Lq, int64_t Lk, int qgroups, float scale_log2e) {
+  // Sequence blockIdx.y of a batch: its Lq query rows and Lk key rows follow
+  // the previous sequence's (stacked rows, attention stays inside each).
+  Q += (int64_t)blockIdx.y * Lq * ldq;
+  O += (int64_t)blockIdx.y * Lq * ldo;
+  K += (int64_t)blockIdx.y * Lk * ldk;
+  V += (int64_t)blockIdx.y * Lk * ldv;
   __shared__ __attribute__((aligned(16))) float ks[2][kKB][kKPad];
   // V^T as bf16 hi and lo parts, two keys per dword, keys of each 16-key
   // group stored in the order 0-3, 8-11, 4-7, 12-15 (lane half h then reads
@@ -451,9 +457,9 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
 
 hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                        int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
-                       hipStream_t s) {
-  if (Lq <= 0) return hipSuccess;
-  if (Lk <= 0 || heads <= 0) return hipErrorInvalidValue;
+                       hipStream_t s, int batch) {
+  if (Lq <= 0 || batch == 0) return hipSuccess;
+  if (Lk <= 0 || heads <= 0 || batch < 0 || batch > 65535) return hipErrorInvalidValue;
   const float scale_log2e = (1.f / sqrtf((float)kHd)) * 1.4426950408889634f;
   // waves per workgroup (32 queries each); SDQ_SDPA_NW = 2, 4 or 8 overrides
   static const int forced = [] {
@@ -465,8 +471,9 @@ hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk,
   auto go = [&](auto nwc) {
     constexpr int NW = decltype(nwc)::value;
     const int qgroups = (int)ceil_div(Lq, 32 * NW);
-    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads)), dim3(NW * 64), 0, s, q,
-                       ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups, scale_log2e);
+    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads), (unsigned)batch),
+                       dim3(NW * 64), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups,
+                       scale_log2e);
   };
   if (nw == 8)
     go(std::integral_constant<int, 8>{});

@@ -124,9 +124,12 @@ hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* s
 hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s);
 // Attention, head_dim 128 (launch_sdpa rejects nothing else; the API checks):
 // out[i, head cols] = softmax(q_i . k_j / sqrt(128)) v_j over j < Lk.
+// batch > 1: `batch` sequences stacked along the rows (sequence b: query rows
+// [b*Lq, (b+1)*Lq), key / value rows [b*Lk, (b+1)*Lk)), each attending only
+// to its own keys.
 hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                        int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
-                       hipStream_t s);
+                       hipStream_t s, int batch = 1);
 // Same output, with the row maxima already known: max_c rmax[row*rstride + c]
 // over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
 // read once.

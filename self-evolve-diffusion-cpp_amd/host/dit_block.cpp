@@ -2,6 +2,7 @@
 #include "sd/dit_block.h"
 
 #include <algorithm>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -143,6 +144,25 @@ void DitBlock::set_norms(const sd_dit_norms& n) {
   norms_ = std::move(d);
 }
 
+void DitBlock::set_modulation(const float* mod) {
+  need(mod != nullptr, "modulation bias is required");
+  DeviceFloats d((size_t)6 * dim_);
+  check(sdq_memcpy(d.get(), mod, (size_t)6 * dim_ * sizeof(float), SDQ_H2D, nullptr),
+        "modulation upload");
+  check(sdq_stream_sync(nullptr), "modulation upload");
+  mod_ = std::move(d);
+}
+
+// e = t6 + mod, value by value (the reference adds the block's bias into a
+// copy of the time rows, ovi_dit.cpp:716-723): a copy, then x += y.
+void DitBlock::modulation_rows(const float* t6, float* e, void* s) const {
+  need(static_cast<bool>(mod_), "modulation bias not set (set_modulation)");
+  need(t6 && e, "t6 and e are required");
+  const size_t n = (size_t)6 * dim_;
+  if (e != t6) check(sdq_memcpy(e, t6, n * sizeof(float), SDQ_D2D, s), "modulation rows");
+  check(sdq_add(e, mod_.get(), (int64_t)n, s), "modulation rows");
+}
+
 namespace {
 
 // Workspace carve-up (floats, each region 256-byte aligned): a [M,3dim]
@@ -177,23 +197,25 @@ size_t DitBlock::workspace_bytes(int64_t M, int64_t Mc, int64_t Mt) const {
 // block_self_fwd (ovi_dit.cpp:205-212) with self_attn_fwd (176-188):
 // q|k|v = mlin(mod_rows(layernorm(x), e0, e1)); rmsnorm + RoPE on q and k;
 // x += o(sdpa(q, k, v)) * e2.
-void DitBlock::self_phase(const sd_dit_block_step& st, float* ws, void* s) const {
-  const int64_t C = dim_, M = st.M;
-  const Carve c = carve(M, st.Mc, st.Mt, C, ffn_, fusion_);
+void DitBlock::self_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const {
+  // `batch` sequences stacked along the rows: every step is per row except
+  // the attention, which stays inside each sequence
+  const int64_t C = dim_, M = st.M, BM = batch * M;
+  const Carve c = carve(BM, batch * st.Mc, batch * st.Mt, C, ffn_, fusion_);
   float* qkv = ws + c.a;
   float* att = ws + c.att;
   sdq_epilogue epi{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
-  check(sdq_qlinear_lnmod(qkv_.handle(), st.x, M, C, st.e, st.e + C, st.eps, &epi, qkv, s),
+  check(sdq_qlinear_lnmod(qkv_.handle(), st.x, BM, C, st.e, st.e + C, st.eps, &epi, qkv, s),
         "self q|k|v");
   // q and k norms (+ RoPE) in one launch: two independent serial row-sum sets
   const int nr = st.cs ? st.nr : 0;
-  const sdq_rms_seg qk[2] = {{qkv, M, 3 * C, norm(SA_NQ), st.cs, nr},
-                             {qkv + C, M, 3 * C, norm(SA_NK), st.cs, nr}};
+  const sdq_rms_seg qk[2] = {{qkv, BM, 3 * C, norm(SA_NQ), st.cs, nr},
+                             {qkv + C, BM, 3 * C, norm(SA_NK), st.cs, nr}};
   check(sdq_rmsnorm_rope_batch(qk, 2, C, st.heads, st.eps, s), "self rmsnorm+rope q, k");
-  check(sdq_sdpa(qkv, 3 * C, qkv + C, 3 * C, qkv + 2 * C, 3 * C, att, C, M, M, st.heads,
-                 (int)(C / st.heads), s),
+  check(sdq_sdpa_batched(qkv, 3 * C, qkv + C, 3 * C, qkv + 2 * C, 3 * C, att, C, M, M, st.heads,
+                         (int)(C / st.heads), batch, s),
         "self sdpa");
-  o_.forward_device(att, M, SDQ_EPI_GATED, st.e + 2 * C, st.x, st.x, s);
+  o_.forward_device(att, BM, SDQ_EPI_GATED, st.e + 2 * C, st.x, st.x, s);
 }
 
 // Non-fusion blocks (block_vanilla_fwd, ovi_dit.cpp:259-268 with
@@ -203,68 +225,73 @@ void DitBlock::self_phase(const sd_dit_block_step& st, float* ws, void* s) const
 // table for the attention on the target's k_fusion (rmsnorm + the target's
 // table) and v_fusion of layernorm(target; pre_attn_norm_fusion); x +=
 // o(text + target attention). Then ffn_fwd (214-222).
-void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) const {
+void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const {
   const int64_t C = dim_, M = st.M, Mc = st.Mc, Mt = st.Mt;
+  const int64_t BM = batch * M, BMc = batch * Mc, BMt = batch * Mt;
   const int hd = (int)(C / st.heads);
-  const Carve c = carve(M, Mc, Mt, C, ffn_, fusion_);
+  const Carve c = carve(BM, BMc, BMt, C, ffn_, fusion_);
   float* cq = ws + c.a;
-  float* xt = ws + c.a + M * C;
-  float* aux = ws + c.a + 2 * M * C;  // norm3 output, then the target attention
+  float* xt = ws + c.a + BM * C;
+  float* aux = ws + c.a + 2 * BM * C;  // norm3 output, then the target attention
   float* ckv = ws + c.ckv;
   const float* qin = st.x;
   if (!fusion_) {
-    check(sdq_layernorm(st.x, M, C, norm(LN3_W), norm(LN3_B), st.eps, aux, s), "norm3");
+    check(sdq_layernorm(st.x, BM, C, norm(LN3_W), norm(LN3_B), st.eps, aux, s), "norm3");
     qin = aux;
   }
-  cq_.forward_device(qin, M, SDQ_EPI_NONE, nullptr, nullptr, cq, s);
-  ckv_.forward_device(st.ctx, Mc, SDQ_EPI_NONE, nullptr, nullptr, ckv, s);
+  cq_.forward_device(qin, BM, SDQ_EPI_NONE, nullptr, nullptr, cq, s);
+  ckv_.forward_device(st.ctx, BMc, SDQ_EPI_NONE, nullptr, nullptr, ckv, s);
   float* kvt = ws + c.kvt;
   if (fusion_) {  // the target's k|v first, so the three norms share one launch
     float* tn = ws + c.tn;
-    check(sdq_layernorm(st.target, Mt, C, norm(PNF_W), norm(PNF_B), st.eps, tn, s),
+    check(sdq_layernorm(st.target, BMt, C, norm(PNF_W), norm(PNF_B), st.eps, tn, s),
           "pre_attn_norm_fusion");
-    kvf_.forward_device(tn, Mt, SDQ_EPI_NONE, nullptr, nullptr, kvt, s);
+    kvf_.forward_device(tn, BMt, SDQ_EPI_NONE, nullptr, nullptr, kvt, s);
   }
   // rmsnorm of cross q and context k (no rotation); fusion: rmsnorm_k_fusion
   // + the target's rotation of k_fusion. Independent row sets, one launch.
-  const sdq_rms_seg nk[3] = {{cq, M, C, norm(CA_NQ), nullptr, 0},
-                             {ckv, Mc, 2 * C, norm(CA_NK), nullptr, 0},
-                             {kvt, Mt, 2 * C, norm(NK_F), st.cs_tgt, st.cs_tgt ? st.nr_tgt : 0}};
+  const sdq_rms_seg nk[3] = {{cq, BM, C, norm(CA_NQ), nullptr, 0},
+                             {ckv, BMc, 2 * C, norm(CA_NK), nullptr, 0},
+                             {kvt, BMt, 2 * C, norm(NK_F), st.cs_tgt, st.cs_tgt ? st.nr_tgt : 0}};
   check(sdq_rmsnorm_rope_batch(nk, fusion_ ? 3 : 2, C, st.heads, st.eps, s), "cross norms");
-  check(sdq_sdpa(cq, C, ckv, 2 * C, ckv + C, 2 * C, xt, C, M, Mc, st.heads, hd, s), "text sdpa");
+  check(sdq_sdpa_batched(cq, C, ckv, 2 * C, ckv + C, 2 * C, xt, C, M, Mc, st.heads, hd, batch, s),
+        "text sdpa");
   if (fusion_) {
     if (st.cs)
-      check(sdq_rmsnorm_rope(cq, M, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
-    check(sdq_sdpa(cq, C, kvt, 2 * C, kvt + C, 2 * C, aux, C, M, Mt, st.heads, hd, s),
+      check(sdq_rmsnorm_rope(cq, BM, C, C, nullptr, st.eps, st.heads, st.cs, st.nr, s), "rope q");
+    check(sdq_sdpa_batched(cq, C, kvt, 2 * C, kvt + C, 2 * C, aux, C, M, Mt, st.heads, hd, batch,
+                           s),
           "target sdpa");
-    check(sdq_add(xt, aux, M * C, s), "text + target");
+    check(sdq_add(xt, aux, BM * C, s), "text + target");
   }
-  co_.forward_device(xt, M, SDQ_EPI_RESID, nullptr, st.x, st.x, s);
+  co_.forward_device(xt, BM, SDQ_EPI_RESID, nullptr, st.x, st.x, s);
   const float* e = st.e;
   check(sdq_ffn_lnmod(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), st.x,
-                      M, e + 3 * C, e + 4 * C, st.eps, e + 5 * C, 1, ws + c.hid, s),
+                      BM, e + 3 * C, e + 4 * C, st.eps, e + 5 * C, 1, ws + c.hid, s),
         "ffn");
 }
 
-void DitBlock::forward_step(const sd_dit_block_step& st, int phases, void* s) const {
+void DitBlock::forward_step(const sd_dit_block_step& st, int phases, void* s, int batch) const {
   need(norms_.get() != nullptr, "norm weights not set (set_norms)");
   need(phases >= 1 && phases <= 3, "phases must be SD_DIT_SELF, SD_DIT_CROSS_FFN or both");
+  need(batch >= 1 && batch <= 64, "batch must be 1..64");
   need(st.M >= 0 && st.Mc > 0 && st.Mt >= 0, "row counts (M >= 0, Mc > 0)");
   need(st.heads > 0 && dim_ % st.heads == 0 && dim_ / st.heads == 128, "head_dim must be 128");
   need(st.x && st.e, "x and e are required");
-  need(st.ws && st.ws_bytes >= workspace_bytes(st.M, st.Mc, st.Mt), "workspace too small");
+  need(st.ws && st.ws_bytes >= workspace_bytes(batch * st.M, batch * st.Mc, batch * st.Mt),
+       "workspace too small");
   if (st.M == 0) return;
   const int64_t hd = dim_ / st.heads;
   need(!st.cs || (st.nr > 0 && st.nr <= hd / 2), "rope table pairs out of range");
   float* ws = static_cast<float*>(st.ws);
-  if (phases & SD_DIT_SELF) self_phase(st, ws, s);
+  if (phases & SD_DIT_SELF) self_phase(st, batch, ws, s);
   if (phases & SD_DIT_CROSS_FFN) {
     need(st.ctx, "ctx is required");
     if (fusion_) {
       need(st.target && st.Mt > 0, "fusion blocks need the target tokens");
       need(!st.cs_tgt || (st.nr_tgt > 0 && st.nr_tgt <= hd / 2), "target rope pairs out of range");
     }
-    cross_ffn_phase(st, ws, s);
+    cross_ffn_phase(st, batch, ws, s);
   }
 }
 
@@ -308,12 +335,79 @@ void block_parts(const std::unordered_map<std::string, Tensor>& pack, const std:
 
 }  // namespace
 
+namespace {
+
+// The block's small F32 tensors (vec() and the modulation check of
+// load_impl, ovi_dit.cpp:417-422, 509-537), from any source of F32 values:
+// get(name, &dims) returns the values and shape, or throws "missing tensor".
+struct BlockVectors {
+  std::vector<float> v[9];  // sd_dit_norms order
+  std::vector<float> mod;   // [6, dim]
+};
+
+template <class Get>
+BlockVectors block_vectors(Get get, const std::string& prefix, int layer, int64_t dim,
+                           bool fusion) {
+  const std::string B = prefix + "blocks." + std::to_string(layer) + ".";
+  BlockVectors out;
+  auto vec = [&](int slot, const std::string& n) {
+    std::vector<int64_t> dims;
+    std::vector<float> v = get(n, dims);
+    if (dims.size() != 1 || dims[0] != dim) throw std::runtime_error("ovi_dit: bad shape for " + n);
+    out.v[slot] = std::move(v);
+  };
+  vec(0, B + "self_attn.norm_q.weight");
+  vec(1, B + "self_attn.norm_k.weight");
+  vec(2, B + "cross_attn.norm_q.weight");
+  vec(3, B + "cross_attn.norm_k.weight");
+  vec(4, B + "norm3.weight");
+  vec(5, B + "norm3.bias");
+  std::vector<int64_t> md;
+  out.mod = get(B + "modulation.modulation", md);
+  if (md.size() != 3 || md[0] != 1 || md[1] != 6 || md[2] != dim)
+    throw std::runtime_error("ovi_dit: bad modulation " + B);
+  if (fusion) {
+    vec(6, B + "cross_attn.norm_k_fusion.weight");
+    vec(7, B + "cross_attn.pre_attn_norm_fusion.weight");
+    vec(8, B + "cross_attn.pre_attn_norm_fusion.bias");
+  }
+  return out;
+}
+
+void apply_vectors(DitBlock& b, const BlockVectors& bv) {
+  auto p = [&](int i) { return bv.v[i].empty() ? nullptr : bv.v[i].data(); };
+  const sd_dit_norms n{p(0), p(1), p(2), p(3), p(4), p(5), p(6), p(7), p(8)};
+  b.set_norms(n);
+  b.set_modulation(bv.mod.data());
+}
+
+// F32 values of a load_sdcpp view (the reference's vec() would dequantize an
+// int8 entry; packs never quantize these small tensors).
+std::vector<float> view_values(const std::unordered_map<std::string, Tensor>& pack,
+                               const std::string& name, std::vector<int64_t>& dims) {
+  auto it = pack.find(name);
+  if (it == pack.end() || !it->second.data) throw std::runtime_error("ovi_dit: missing tensor " + name);
+  const Tensor& t = it->second;
+  if (t.dtype != DType::F32)
+    throw std::runtime_error("ovi_dit: " + name + " is not an F32 pack entry");
+  dims = t.shape;
+  const float* f = t.ptr<float>();
+  return std::vector<float>(f, f + t.numel());
+}
+
+}  // namespace
+
 DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                              const std::string& prefix, int layer, int64_t dim, int64_t ffn_dim,
                              bool fusion) {
   LinearPart l[DitBlock::kCount];
   block_parts(pack, prefix, layer, dim, ffn_dim, fusion, l);
-  return DitBlock(l, fusion, false);
+  const BlockVectors bv = block_vectors(
+      [&](const std::string& n, std::vector<int64_t>& d) { return view_values(pack, n, d); },
+      prefix, layer, dim, fusion);
+  DitBlock b(l, fusion, false);
+  apply_vectors(b, bv);
+  return b;
 }
 
 std::vector<DitBlock> dit_blocks_from_pack(const std::unordered_map<std::string, Tensor>& pack,
@@ -321,9 +415,111 @@ std::vector<DitBlock> dit_blocks_from_pack(const std::unordered_map<std::string,
                                            const std::vector<int>& layers, int64_t dim,
                                            int64_t ffn_dim, bool fusion) {
   std::vector<std::array<LinearPart, DitBlock::kCount>> parts(layers.size());
-  for (size_t i = 0; i < layers.size(); i++)
+  std::vector<BlockVectors> vecs;
+  for (size_t i = 0; i < layers.size(); i++) {
     block_parts(pack, prefix, layers[i], dim, ffn_dim, fusion, parts[i].data());
-  return DitBlock::create_many(parts, fusion);
+    vecs.push_back(block_vectors(
+        [&](const std::string& n, std::vector<int64_t>& d) { return view_values(pack, n, d); },
+        prefix, layers[i], dim, fusion));
+  }
+  std::vector<DitBlock> blocks = DitBlock::create_many(parts, fusion);
+  for (size_t i = 0; i < blocks.size(); i++) apply_vectors(blocks[i], vecs[i]);
+  return blocks;
+}
+
+namespace {
+
+// lin() on the pack index (ovi_dit.cpp:397-415): the same names, checks and
+// messages as linear_part_from_pack on load_sdcpp's views.
+FilePart file_part(const PackIndex& ix, const std::string& base, int64_t in, int64_t out) {
+  const std::string wn = base + ".weight";
+  const PackEntry* w = ix.find(wn);
+  if (!w) throw std::runtime_error("ovi_dit: missing tensor " + wn);
+  if (w->dims.size() != 2 || w->dims[0] != out || w->dims[1] != in)
+    throw std::runtime_error("ovi_dit: bad shape for " + wn);
+  if (w->kind != PackEntry::kInt8Rows)
+    throw std::runtime_error("ovi_dit: " + wn + " is not an int8 pack entry");
+  bool from_int8 = false;
+  const PackEntry* sc = ix.f32_view(wn + ".scale", &from_int8);
+  if (!sc) throw std::runtime_error("ovi_dit: missing tensor " + wn + ".scale");
+  if (!from_int8 || sc != w) throw std::runtime_error("ovi_dit: scale not packed after i8 for " + base);
+  bool bias_scale = false;
+  const PackEntry* b = ix.f32_view(base + ".bias", &bias_scale);
+  if (!b) throw std::runtime_error("ovi_dit: missing tensor " + base + ".bias");
+  const int64_t bn = bias_scale ? b->rows : b->numel;
+  if ((!bias_scale && b->dims.size() != 1) || bn != out)
+    throw std::runtime_error("ovi_dit: bad shape for " + base + ".bias");
+  FilePart p;
+  p.q_off = w->data;
+  p.scale_off = w->scale;
+  p.bias = ix.read_f32(*b, bias_scale);
+  p.out = out;
+  p.in = in;
+  return p;
+}
+
+std::vector<float> index_values(const PackIndex& ix, const std::string& name,
+                                std::vector<int64_t>& dims) {
+  bool is_scale = false;
+  const PackEntry* e = ix.f32_view(name, &is_scale);
+  if (!e) {
+    if (ix.find(name)) throw std::runtime_error("ovi_dit: " + name + " is not an F32 pack entry");
+    throw std::runtime_error("ovi_dit: missing tensor " + name);
+  }
+  dims = is_scale ? std::vector<int64_t>{e->rows} : e->dims;
+  return ix.read_f32(*e, is_scale);
+}
+
+}  // namespace
+
+std::vector<DitBlock> dit_blocks_from_pack_file(const std::string& path, const std::string& prefix,
+                                                const std::vector<int>& layers, int64_t dim,
+                                                int64_t ffn_dim, bool fusion) {
+  const PackIndex ix = PackIndex::read(path);
+  std::vector<std::vector<FilePart>> sets;
+  std::vector<BlockVectors> vecs;
+  for (int layer : layers) {
+    const std::string B = prefix + "blocks." + std::to_string(layer) + ".";
+    auto fp = [&](const char* n, int64_t in, int64_t out) { return file_part(ix, B + n, in, out); };
+    FilePart q = fp("self_attn.q", dim, dim), k = fp("self_attn.k", dim, dim),
+             v = fp("self_attn.v", dim, dim), o = fp("self_attn.o", dim, dim);
+    FilePart cq = fp("cross_attn.q", dim, dim), ck = fp("cross_attn.k", dim, dim),
+             cv = fp("cross_attn.v", dim, dim), co = fp("cross_attn.o", dim, dim);
+    FilePart fc1 = fp("ffn.0", dim, ffn_dim), fc2 = fp("ffn.2", ffn_dim, dim);
+    sets.push_back({std::move(q), std::move(k), std::move(v)});
+    sets.push_back({std::move(o)});
+    sets.push_back({std::move(cq)});
+    sets.push_back({std::move(ck), std::move(cv)});
+    if (fusion)
+      sets.push_back({fp("cross_attn.k_fusion", dim, dim), fp("cross_attn.v_fusion", dim, dim)});
+    sets.push_back({std::move(co)});
+    sets.push_back({std::move(fc1)});
+    sets.push_back({std::move(fc2)});
+    vecs.push_back(block_vectors(
+        [&](const std::string& n, std::vector<int64_t>& d) { return index_values(ix, n, d); },
+        prefix, layer, dim, fusion));
+  }
+  std::vector<QLinear> q = QLinear::upload_many_file(path, sets);
+  std::vector<DitBlock> out;
+  out.reserve(layers.size());
+  size_t j = 0;
+  for (size_t b = 0; b < layers.size(); b++) {
+    DitBlock d;
+    d.fusion_ = fusion;
+    d.dim_ = dim;
+    d.ffn_ = ffn_dim;
+    d.qkv_ = std::move(q[j++]);
+    d.o_ = std::move(q[j++]);
+    d.cq_ = std::move(q[j++]);
+    d.ckv_ = std::move(q[j++]);
+    if (fusion) d.kvf_ = std::move(q[j++]);
+    d.co_ = std::move(q[j++]);
+    d.fc1_ = std::move(q[j++]);
+    d.fc2_ = std::move(q[j++]);
+    apply_vectors(d, vecs[b]);
+    out.push_back(std::move(d));
+  }
+  return out;
 }
 
 }  // namespace gpu
@@ -418,17 +614,60 @@ int sd_dit_block_set_norms(sd_dit_block* b, const sd_dit_norms* n) {
   return guarded([&] { b->blk.set_norms(*n); });
 }
 
+int sd_dit_block_set_modulation(sd_dit_block* b, const float* mod) {
+  if (!b || !mod) {
+    t_dit_err = "sd_dit_block_set_modulation: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { b->blk.set_modulation(mod); });
+}
+
+int sd_dit_block_modulation(const sd_dit_block* b, const float* t6, float* e, void* stream) {
+  if (!b) {
+    t_dit_err = "sd_dit_block_modulation: null block";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { b->blk.modulation_rows(t6, e, stream); });
+}
+
+int sd_dit_blocks_from_pack(const char* path, const char* prefix, const int* layers, int n,
+                            int64_t dim, int64_t ffn_dim, int fusion, int file_reads,
+                            sd_dit_block** out) {
+  if (!path || !prefix || !out || n < 0 || (n > 0 && !layers)) {
+    t_dit_err = "sd_dit_blocks_from_pack: null argument or negative count";
+    return SDQ_ERR_INVALID;
+  }
+  for (int i = 0; i < n; i++) out[i] = nullptr;
+  return guarded([&] {
+    const std::vector<int> ls(layers, layers + n);
+    std::vector<sd::gpu::DitBlock> blocks;
+    if (file_reads) {
+      blocks = sd::gpu::dit_blocks_from_pack_file(path, prefix, ls, dim, ffn_dim, fusion != 0);
+    } else {
+      std::shared_ptr<void> owner;
+      const auto pack = sd::load_sdcpp(path, owner);
+      blocks = sd::gpu::dit_blocks_from_pack(pack, prefix, ls, dim, ffn_dim, fusion != 0);
+    }
+    for (int i = 0; i < n; i++) out[i] = new sd_dit_block{std::move(blocks[i])};
+  });
+}
+
 size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {
   return b && M >= 0 && Mc >= 0 && Mt >= 0 ? b->blk.workspace_bytes(M, Mc, Mt) : 0;
 }
 
 int sd_dit_block_step_forward(const sd_dit_block* b, const sd_dit_block_step* st, int phases,
                               void* stream) {
+  return sd_dit_block_step_forward_batched(b, st, 1, phases, stream);
+}
+
+int sd_dit_block_step_forward_batched(const sd_dit_block* b, const sd_dit_block_step* st,
+                                      int batch, int phases, void* stream) {
   if (!b || !st) {
     t_dit_err = "sd_dit_block_step_forward: null argument";
     return SDQ_ERR_INVALID;
   }
-  return guarded([&] { b->blk.forward_step(*st, phases, stream); });
+  return guarded([&] { b->blk.forward_step(*st, phases, stream, batch); });
 }
 
 double sd_dit_block_step_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt) {

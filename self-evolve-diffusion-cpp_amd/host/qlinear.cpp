@@ -94,6 +94,46 @@ std::vector<QLinear> QLinear::upload_many(const std::vector<std::vector<LinearPa
   return out;
 }
 
+std::vector<QLinear> QLinear::upload_many_file(const std::string& path,
+                                               const std::vector<std::vector<FilePart>>& linears) {
+  std::vector<sdq_weight_fsrc> src(linears.size());
+  for (size_t i = 0; i < linears.size(); i++) {
+    const std::vector<FilePart>& parts = linears[i];
+    if (parts.empty() || parts.size() > 4)
+      throw std::runtime_error("QLinear::upload_many_file: 1-4 parts per Linear");
+    sdq_weight_fsrc& w = src[i];
+    w = sdq_weight_fsrc{};
+    w.nparts = (int)parts.size();
+    w.K = parts[0].in;
+    for (size_t p = 0; p < parts.size(); p++) {
+      if (parts[p].out <= 0 || parts[p].in != w.K)
+        throw std::runtime_error("QLinear: parts must share in_features");
+      if (parts[p].bias.empty() != parts[0].bias.empty())
+        throw std::runtime_error("QLinear: bias on some parts only");
+      w.q_off[p] = parts[p].q_off;
+      w.scale_off[p] = parts[p].scale_off;
+      w.rows[p] = parts[p].out;
+    }
+  }
+  std::vector<sdq_weight*> handles(linears.size(), nullptr);
+  check(sdq_weight_upload_file(path.c_str(), src.data(), (int)src.size(), nullptr, handles.data()),
+        "QLinear::upload_many_file");
+  std::vector<QLinear> out(linears.size());
+  for (size_t i = 0; i < linears.size(); i++) {  // each takes its handle first (freed on throw)
+    out[i].w_ = handles[i];
+    out[i].K_ = src[i].K;
+    for (const FilePart& p : linears[i]) out[i].N_ += p.out;
+  }
+  for (size_t i = 0; i < linears.size(); i++) {
+    if (linears[i][0].bias.empty()) continue;
+    std::vector<float> b;
+    b.reserve((size_t)out[i].N_);
+    for (const FilePart& p : linears[i]) b.insert(b.end(), p.bias.begin(), p.bias.end());
+    out[i].upload_bias(b.data(), false);
+  }
+  return out;
+}
+
 QLinear::QLinear(const std::vector<LinearPart>& parts, bool on_device) {
   if (parts.empty()) throw std::runtime_error("QLinear: no parts");
   K_ = parts[0].in;

@@ -26,6 +26,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "sd/pack.h"
 #include "sd/qlinear.h"
 #include "sd/tensor.h"
 
@@ -123,6 +124,23 @@ int sd_dit_block_free(sd_dit_block* b);
 // Copies the block's norm vectors to the device (required before
 // sd_dit_block_step_forward; the fusion ones for fusion blocks, ln3 for others).
 int sd_dit_block_set_norms(sd_dit_block* b, const sd_dit_norms* n);
+// The block's own modulation bias (modulation.modulation, [6,dim] F32 host
+// array, copied), and e = t6 + that bias on the device: the per-layer
+// ModulationAdd of OviDit::forward (ovi_dit.cpp:716-723, one fp32 add per
+// value, bit-exact). t6 [6,dim] are the time rows (time_projection output),
+// e [6,dim] receives the block's modulation rows for sd_dit_block_step_forward.
+int sd_dit_block_set_modulation(sd_dit_block* b, const float* mod);
+int sd_dit_block_modulation(const sd_dit_block* b, const float* t6, float* e, void* stream);
+// Blocks `layers[0..n)` of backbone `prefix` ("video_model." or
+// "audio_model.") of a .sdcpp file, whole: the 12 int8 Linears, the norm
+// vectors and modulation.modulation, with OviDit::load_impl's names, checks
+// and messages (ovi_dit.cpp:397-415, 505-537). file_reads = 1 reads the
+// weights with large sequential reads into the pinned staging ring
+// (sdq_weight_upload_file); 0 goes through load_sdcpp's mapping. out[i]
+// receives block layers[i]; on error none is returned.
+int sd_dit_blocks_from_pack(const char* path, const char* prefix, const int* layers, int n,
+                            int64_t dim, int64_t ffn_dim, int fusion, int file_reads,
+                            sd_dit_block** out);
 // Device workspace bytes that sd_dit_block_step_forward needs for these rows.
 size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
 // The whole block on the GPU, stream-ordered, bit-exact with the reference
@@ -133,6 +151,17 @@ size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc
 // a copy of the audio x taken before the audio CROSS_FFN.
 int sd_dit_block_step_forward(const sd_dit_block* b, const sd_dit_block_step* st, int phases,
                               void* stream);
+// The same block on `batch` sequences stacked along the rows, sharing the
+// weights and the modulation rows e: the conditional and unconditional
+// forwards of a guidance step (denoise.cpp:95-98) as one pass, each with its
+// own text context. st.M, st.Mc, st.Mt are per sequence; x holds batch*M
+// rows, ctx batch*Mc, target batch*Mt (sequence b at row b*M, b*Mc, b*Mt);
+// cs covers batch*M rows and cs_tgt batch*Mt (each sequence's table
+// repeated); ws is sd_dit_block_workspace_bytes(batch*M, batch*Mc,
+// batch*Mt). Every step is per row except the attention, which stays inside
+// each sequence (sdq_sdpa_batched): bit-identical to `batch` separate calls.
+int sd_dit_block_step_forward_batched(const sd_dit_block* b, const sd_dit_block_step* st,
+                                      int batch, int phases, void* stream);
 // 2*M*N*K of the Linears plus the attention products (4*Lq*Lk*dim per sdpa).
 double sd_dit_block_step_ops(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
 // 2*M*N*K summed over the block's Linears for these row counts.
@@ -180,8 +209,14 @@ class DitBlock {
   double ops(int64_t M, int64_t Mc, int64_t Mt) const;
   // The whole block (norms, RoPE, attention and Linears) on device arrays.
   void set_norms(const sd_dit_norms& n);
+  // modulation.modulation ([6,dim], host) and e = t6 + it on the device.
+  void set_modulation(const float* mod);
+  bool has_modulation() const { return static_cast<bool>(mod_); }
+  void modulation_rows(const float* t6, float* e, void* stream) const;
   size_t workspace_bytes(int64_t M, int64_t Mc, int64_t Mt) const;
-  void forward_step(const sd_dit_block_step& st, int phases, void* stream) const;
+  // batch > 1: that many sequences stacked along the rows (see
+  // sd_dit_block_step_forward_batched).
+  void forward_step(const sd_dit_block_step& st, int phases, void* stream, int batch = 1) const;
   double step_ops(int64_t M, int64_t Mc, int64_t Mt) const;
 
  private:
@@ -189,10 +224,13 @@ class DitBlock {
   static void check_shapes(const LinearPart* l, bool fusion);
   enum Norm { SA_NQ, SA_NK, CA_NQ, CA_NK, LN3_W, LN3_B, NK_F, PNF_W, PNF_B, kNorms };
   const float* norm(Norm n) const { return norms_.get() + n * dim_; }
-  void self_phase(const sd_dit_block_step& st, float* ws, void* s) const;
-  void cross_ffn_phase(const sd_dit_block_step& st, float* ws, void* s) const;
+  void self_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const;
+  void cross_ffn_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const;
+  friend std::vector<DitBlock> dit_blocks_from_pack_file(const std::string&, const std::string&,
+                                                         const std::vector<int>&, int64_t,
+                                                         int64_t, bool);
   QLinear qkv_, o_, cq_, ckv_, kvf_, co_, fc1_, fc2_;
-  DeviceFloats norms_;
+  DeviceFloats norms_, mod_;
   int64_t dim_ = 0, ffn_ = 0;
   bool fusion_ = false;
 };
@@ -207,10 +245,22 @@ DitBlock dit_block_from_pack(const std::unordered_map<std::string, Tensor>& pack
                              bool fusion);
 // Blocks `layers` of a backbone, all uploaded in one stream (the pack's
 // int8 views are copied through pinned buffers while the GPU repacks).
+// Both also load the block's norm vectors (self_attn.norm_q/k, cross_attn.
+// norm_q/k, norm3.weight/bias; fusion: cross_attn.norm_k_fusion,
+// pre_attn_norm_fusion.weight/bias) and modulation.modulation [1,6,dim]
+// (ovi_dit.cpp:509-537), so the blocks are ready for forward_step; packs keep
+// these small tensors F32 (pack_sdcpp.py:23, numel < 65536), and an int8
+// one is rejected.
 std::vector<DitBlock> dit_blocks_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                                            const std::string& prefix,
                                            const std::vector<int>& layers, int64_t dim,
                                            int64_t ffn_dim, bool fusion);
+// The same from the file itself: the tensor table is indexed (sd::PackIndex)
+// and the weights are read with large sequential reads straight into the
+// pinned staging ring (QLinear::upload_many_file), no mapping.
+std::vector<DitBlock> dit_blocks_from_pack_file(const std::string& path, const std::string& prefix,
+                                                const std::vector<int>& layers, int64_t dim,
+                                                int64_t ffn_dim, bool fusion);
 
 }  // namespace gpu
 }  // namespace sd

@@ -27,6 +27,14 @@ struct LinearPart {
   int64_t out = 0, in = 0;
 };
 
+// One [out,in] int8 Linear inside a .sdcpp file: absolute offsets of its
+// int8 rows and scales (sd::PackEntry), and its bias already read (host).
+struct FilePart {
+  uint64_t q_off = 0, scale_off = 0;
+  std::vector<float> bias;  // [out] or empty
+  int64_t out = 0, in = 0;
+};
+
 class QLinear {
  public:
   QLinear() = default;
@@ -41,6 +49,10 @@ class QLinear {
   // Many Linears (each one or more parts, host arrays) in one streamed upload
   // (sdq_weight_upload_batch: pinned staging, async copies, repack overlap).
   static std::vector<QLinear> upload_many(const std::vector<std::vector<LinearPart>>& linears);
+  // The same straight from a pack file with sequential reads
+  // (sdq_weight_upload_file): no page faults through a mapping.
+  static std::vector<QLinear> upload_many_file(const std::string& path,
+                                               const std::vector<std::vector<FilePart>>& linears);
   QLinear(const QLinear&) = delete;
   QLinear& operator=(const QLinear&) = delete;
   QLinear(QLinear&& o) noexcept;

@@ -66,6 +66,8 @@ SIGNATURES = {
     "sdq_weight_upload_device": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, ctypes.POINTER(_vp)]),
     "sdq_weight_free": (ctypes.c_int, [_vp]),
     "sdq_weight_upload_batch": (ctypes.c_int, [_vp, ctypes.c_int, _vp, ctypes.POINTER(_vp)]),
+    "sdq_weight_upload_file": (ctypes.c_int, [ctypes.c_char_p, _vp, ctypes.c_int, _vp,
+                                              ctypes.POINTER(_vp)]),
     "sdq_weight_dims": (ctypes.c_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
@@ -76,6 +78,8 @@ SIGNATURES = {
     "sdq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "sdq_sdpa": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
                                 ctypes.c_int, ctypes.c_int, _vp]),
+    "sdq_sdpa_batched": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]),
     "sdq_rmsnorm_rope": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, ctypes.c_float, ctypes.c_int,
                                         _vp, ctypes.c_int, _vp]),
     "sdq_ffn": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _vp, _vp]),
@@ -334,6 +338,30 @@ def _weight(w, name="w"):
     return w.h
 
 
+class WeightFileSrc(ctypes.Structure):
+    _fields_ = [("nparts", ctypes.c_int), ("q_off", ctypes.c_uint64 * 4),
+                ("scale_off", ctypes.c_uint64 * 4), ("rows", ctypes.c_int64 * 4),
+                ("K", ctypes.c_int64)]
+
+
+def upload_file(path, sources, stream=None):
+    """sources: list of lists of (q_offset, scale_offset, rows, K) parts inside the
+    .sdcpp file `path` (absolute file offsets); one Weight per source, read with
+    sequential file reads (sdq_weight_upload_file)."""
+    load_library()
+    n = len(sources)
+    arr = (WeightFileSrc * max(n, 1))()
+    for i, parts in enumerate(sources):
+        arr[i].nparts = len(parts)
+        arr[i].K = parts[0][3]
+        for p, (qo, so, rows, _k) in enumerate(parts):
+            arr[i].q_off[p], arr[i].scale_off[p], arr[i].rows[p] = qo, so, rows
+    handles = (ctypes.c_void_p * max(n, 1))()
+    _check(_lib.sdq_weight_upload_file(os.fsencode(path), arr, n, _stream(stream), handles))
+    return [Weight(ctypes.c_void_p(handles[i]), sum(arr[i].rows[p] for p in range(arr[i].nparts)),
+                   arr[i].K) for i in range(n)]
+
+
 def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, gate_fma=True,
             stream=None):
     """out = epilogue(qgemm(A, W) + bias) on device tensors (stream-ordered).
@@ -444,21 +472,27 @@ def _cols(c, t, name, col, C):
     return ctypes.c_void_p(t.data_ptr() + 4 * col)
 
 
-def sdpa(q, k, v, out, heads, qcol=0, kcol=0, vcol=0, stream=None):
+def sdpa(q, k, v, out, heads, qcol=0, kcol=0, vcol=0, batch=1, stream=None):
     """out = attention(q, k, v) over `heads` heads of 128 columns, taken from
     column offsets qcol / kcol / vcol of the device tensors q, k, v (e.g. one
-    q|k|v tensor passed three times); rows may be strided (stride(0))."""
+    q|k|v tensor passed three times); rows may be strided (stride(0)).
+    batch > 1: that many sequences stacked along the rows, each attending to
+    its own keys only (sdq_sdpa_batched)."""
     c = _Args()
     C = heads * 128
     pq, pk, pv = _cols(c, q, "q", qcol, C), _cols(c, k, "k", kcol, C), _cols(c, v, "v", vcol, C)
     po = _cols(c, out, "out", 0, C)
-    Lq, Lk = q.shape[0], k.shape[0]
-    if v.shape[0] != Lk or out.shape[0] != Lq:
-        raise _bad(f"sdpa: {Lq} queries, {Lk} keys, {v.shape[0]} values, {out.shape[0]} out rows")
+    if batch < 1 or q.shape[0] % batch or k.shape[0] % batch:
+        raise _bad(f"sdpa: {q.shape[0]} query and {k.shape[0]} key rows do not split into "
+                   f"{batch} sequences")
+    Lq, Lk = q.shape[0] // batch, k.shape[0] // batch
+    if v.shape[0] != k.shape[0] or out.shape[0] != q.shape[0]:
+        raise _bad(f"sdpa: {q.shape[0]} queries, {k.shape[0]} keys, {v.shape[0]} values, "
+                   f"{out.shape[0]} out rows")
     load_library()
     c.done()
-    _check(_lib.sdq_sdpa(pq, _ld(q), pk, _ld(k), pv, _ld(v), po, _ld(out), Lq, Lk, heads, 128,
-                         _stream(stream)))
+    _check(_lib.sdq_sdpa_batched(pq, _ld(q), pk, _ld(k), pv, _ld(v), po, _ld(out), Lq, Lk, heads,
+                                 128, batch, _stream(stream)))
     return out
 
 
@@ -652,6 +686,9 @@ def load_host_library(path: str = HOST_LIB_PATH):
     h.sd_dit_block_step_forward.restype = ctypes.c_int
     h.sd_dit_block_step_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockStep),
                                             ctypes.c_int, ctypes.c_void_p]
+    h.sd_dit_block_step_forward_batched.restype = ctypes.c_int
+    h.sd_dit_block_step_forward_batched.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockStep),
+                                                    ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     h.sd_dit_block_step_ops.restype = ctypes.c_double
     h.sd_dit_block_step_ops.argtypes = [ctypes.c_void_p, _i64, _i64, _i64]
     for f in (h.sd_rope_table_3d, h.sd_rope_table_1d):
@@ -659,6 +696,16 @@ def load_host_library(path: str = HOST_LIB_PATH):
     h.sd_rope_table_3d.argtypes = [ctypes.c_int] * 4 + [ctypes.c_float, ctypes.c_void_p]
     h.sd_rope_table_1d.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float,
                                    ctypes.c_void_p]
+    h.sd_dit_block_set_modulation.restype = ctypes.c_int
+    h.sd_dit_block_set_modulation.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    h.sd_dit_block_modulation.restype = ctypes.c_int
+    h.sd_dit_block_modulation.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_void_p]
+    h.sd_dit_blocks_from_pack.restype = ctypes.c_int
+    h.sd_dit_blocks_from_pack.argtypes = [ctypes.c_char_p, ctypes.c_char_p,
+                                          ctypes.POINTER(ctypes.c_int), ctypes.c_int, _i64, _i64,
+                                          ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_void_p)]
     h.sd_dit_block_free.restype = ctypes.c_int
     h.sd_dit_block_free.argtypes = [ctypes.c_void_p]
     h.sd_dit_block_ops.restype = ctypes.c_double
@@ -747,6 +794,41 @@ class DitBlock:
                 "hid": (M, f), "x": (M, d), "shift_sa": (d,), "scale_sa": (d,),
                 "shift_ffn": (d,), "scale_ffn": (d,)}
 
+    @classmethod
+    def from_pack(cls, path, prefix, layers, dim, ffn_dim, fusion, file_reads=True):
+        """Blocks `layers` of backbone `prefix` ("video_model." / "audio_model.")
+        of a .sdcpp file, whole: Linears, norms and modulation bias, with
+        OviDit::load_impl's names and checks (sd_dit_blocks_from_pack);
+        file_reads: sequential file reads (else load_sdcpp's mapping)."""
+        h = load_host_library()
+        n = len(layers)
+        arr = (ctypes.c_int * max(n, 1))(*layers)
+        handles = (ctypes.c_void_p * max(n, 1))()
+        _hcheck(h.sd_dit_blocks_from_pack(os.fsencode(path), prefix.encode(), arr, n, dim,
+                                          ffn_dim, 1 if fusion else 0, 1 if file_reads else 0,
+                                          handles))
+        out = []
+        for b in range(n):
+            blk = cls.__new__(cls)
+            blk.h = ctypes.c_void_p(handles[b])
+            blk.fusion, blk.dim, blk.ffn_dim = fusion, int(dim), int(ffn_dim)
+            out.append(blk)
+        return out
+
+    def set_modulation(self, mod):
+        """mod: host float32 [6, dim] (or [1, 6, dim]), modulation.modulation."""
+        m = np.ascontiguousarray(mod, np.float32).reshape(6, self.dim)
+        _hcheck(_host.sd_dit_block_set_modulation(self.h, _ptr(m)))
+
+    def modulation(self, t6, e, stream=None):
+        """e = t6 + the block's modulation bias (device [6, dim] tensors)."""
+        c = _Args()
+        pt = c(t6, "t6", "f32", (6, self.dim))
+        pe = c(e, "e", "f32", (6, self.dim))
+        c.done()
+        _hcheck(_host.sd_dit_block_modulation(self.h, pt, pe, _stream(stream)))
+        return e
+
     def forward(self, stream=None, **io):
         """io: M, Mc, Mt and the device tensors named in BlockIO; each tensor
         given is checked against its [rows, cols] before the launch."""
@@ -785,11 +867,13 @@ class DitBlock:
         return _host.sd_dit_block_step_ops(self.h, M, Mc, Mt)
 
     def step(self, x, ctx, e, heads, cs=None, target=None, cs_tgt=None, ws=None, phases=ALL,
-             eps=1e-6, stream=None):
+             eps=1e-6, stream=None, batch=1):
         """The whole block on device tensors (sd_dit_block_step_forward): x
         [M,dim] in place, ctx [Mc,dim], e [6,dim], cs [M,nr,2] (RoPE table on
         the device), target [Mt,dim] and cs_tgt for fusion blocks; ws a device
-        byte tensor of workspace_bytes (allocated here when None)."""
+        byte tensor of workspace_bytes (allocated here when None). batch > 1:
+        that many sequences stacked along the rows of x, ctx, target, cs and
+        cs_tgt (sd_dit_block_step_forward_batched)."""
         c = _Args()
         import torch
 
@@ -797,27 +881,29 @@ class DitBlock:
         st = BlockStep()
         st.x = c(x, "x", "f32", (None, d))
         st.ctx = c(ctx, "ctx", "f32", (None, d))
-        st.M, st.Mc = x.shape[0], ctx.shape[0]
         st.target = c(target, "target", "f32", (None, d), optional=True)
-        st.Mt = 0 if target is None else target.shape[0]
+        rows = (x.shape[0], ctx.shape[0], 0 if target is None else target.shape[0])
+        if batch < 1 or any(r % batch for r in rows):
+            raise _bad(f"step: rows {rows} of x, ctx, target do not split into {batch} sequences")
+        st.M, st.Mc, st.Mt = (r // batch for r in rows)
         st.heads, st.eps = heads, eps
         st.e = c(e, "e", "f32", (6, d))
-        st.cs, st.nr = _rope_table(c, cs, st.M)
-        st.cs_tgt, st.nr_tgt = _rope_table(c, cs_tgt, st.Mt, "cs_tgt")
+        st.cs, st.nr = _rope_table(c, cs, batch * st.M)
+        st.cs_tgt, st.nr_tgt = _rope_table(c, cs_tgt, batch * st.Mt, "cs_tgt")
+        need = self.workspace_bytes(batch * st.M, batch * st.Mc, batch * st.Mt)
         if ws is None:
             if stream is not None:
                 # a workspace allocated here would be freed on return while
                 # the side stream still uses it
                 raise ValueError("DitBlock.step: pass ws when running on a given stream")
-            ws = torch.empty(self.workspace_bytes(st.M, st.Mc, st.Mt), dtype=torch.uint8,
-                             device=x.device)
+            ws = torch.empty(need, dtype=torch.uint8, device=x.device)
         st.ws = c(ws, "ws", "u8")
         st.ws_bytes = ws.numel()
-        need = self.workspace_bytes(st.M, st.Mc, st.Mt)
         if st.ws_bytes < need:
             raise _bad(f"ws: workspace too small ({st.ws_bytes} bytes, the block needs {need})")
         c.done()
-        _hcheck(_host.sd_dit_block_step_forward(self.h, ctypes.byref(st), phases, _stream(stream)))
+        _hcheck(_host.sd_dit_block_step_forward_batched(self.h, ctypes.byref(st), batch, phases,
+                                                        _stream(stream)))
         return x
 
     def free(self):

@@ -1,0 +1,139 @@
+"""Drift of the whole twin backbone over several fusion layers at the real
+widths (dim 3072, FFN 14336, 24 heads; video 768 tokens on the 3x16x16 grid,
+audio 157 tokens, text contexts of 512 rows), the layer loop of
+OviDit::forward (ovi_dit.cpp:712-739).
+
+Two chains run beside the GPU's, layer by layer:
+  * the reference chain: every step of the reference block, computed by the
+    reference's own compiled functions (oracle/_ref: sd::qgemm, sdpa,
+    layernorm, mod_rows, rmsnorm; bit-identical to the oracle's restatement,
+    which the CPU suite pins) plus the oracle's elementwise steps;
+  * the same chain with its sdpa and fc1 + GELU steps replaced by the GPU's
+    own kernels (the two steps that are not bit-exact by construction): the
+    GPU must match it bit for bit after every layer, which pins the order
+    and wiring of every other step across layers.
+Against the reference chain the GPU is gated like the reference's own int8
+DiT test (tests/test_ovit8.cpp:113-122: cosine > 0.99); the per-layer cosine
+and max relative error are printed and bounded, so their growth over the
+layers is measured."""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact
+from test_gpu_block_full import _gpu_fc1_gelu, _gpu_sdpa, _norms, _ref_block, _weights
+
+pytestmark = pytest.mark.gpu
+
+
+class _RefOps:
+    """The oracle interface _ref_block uses, on the reference build where it
+    has the function (same results, bit for bit; much faster at these sizes)."""
+
+    def __init__(self, oracle, ref):
+        self.o, self.r = oracle, ref
+
+    def linear(self, A, q, s, bias=None, epilogue="none", gate=None, resid=None, use_fma=True):
+        y = self.r.qgemm(A, q, s)
+        if bias is not None:
+            y = self.o.bias_add(y, bias)
+        if epilogue == "none":
+            return y
+        if epilogue == "gelu":
+            return self.o.gelu_tanh(y)
+        if epilogue == "gated":
+            return self.o.gated_add(resid, y, gate, use_fma)
+        if epilogue == "resid":
+            return self.o.add(resid, y)
+        raise ValueError(epilogue)
+
+    def sdpa(self, q, k, v, heads):
+        return self.r.sdpa(q, k, v, heads)
+
+    def layernorm(self, x, eps=1e-6, w=None, b=None):
+        return self.r.layernorm(x, eps, w, b)
+
+    def mod_rows(self, x, shift, scale):
+        return self.r.mod_rows(x, shift, scale)
+
+    def rmsnorm(self, x, w, eps=1e-6):
+        return self.r.rmsnorm(x, w, eps)
+
+    def __getattr__(self, name):  # rope, gelu_tanh, add: the oracle's
+        return getattr(self.o, name)
+
+
+def _cos(a, b):
+    a, b = a.astype(np.float64).ravel(), b.astype(np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def test_twin_backbone_drift_real_width(sdq_dev, oracle, ref):
+    import torch
+
+    import sdq
+
+    dim, ffn, heads, L = 3072, 14336, 24, 4
+    Mv, Ma, Mc = 768, 157, 512
+    print(f"[drift] {L} fusion layers, video {Mv} / audio {Ma} tokens, dim {dim}", flush=True)
+    ops = _RefOps(oracle, ref)
+    cs_v = sdq.rope_table_3d(3, 16, 16)
+    cs_a = sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)
+    xv0 = oracle.randn(Mv * dim, 1).reshape(Mv, dim)
+    xa0 = oracle.randn(Ma * dim, 2).reshape(Ma, dim)
+    ctx_v = oracle.randn(Mc * dim, 3).reshape(Mc, dim)
+    ctx_a = oracle.randn(Mc * dim, 4).reshape(Mc, dim)
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(sdq_dev)  # noqa
+    gxv, gxa = dv(xv0), dv(xa0)
+    g_ctx_v, g_ctx_a, g_cs_v, g_cs_a = dv(ctx_v), dv(ctx_a), dv(cs_v), dv(cs_a)
+    want_v, want_a, ex_v, ex_a = xv0, xa0, xv0, xa0
+    gsd = _gpu_sdpa(sdq_dev)
+    report = []
+    for i in range(L):
+        ev = (oracle.randn(6 * dim, 100 + i) * np.float32(0.3)).reshape(6, dim)
+        ea = (oracle.randn(6 * dim, 200 + i) * np.float32(0.3)).reshape(6, dim)
+        lv = _weights(oracle, dim, ffn, 1000 + 100 * i, True)
+        la = _weights(oracle, dim, ffn, 5000 + 100 * i, True)
+        nv, na = _norms(oracle, dim, 300 + i), _norms(oracle, dim, 400 + i)
+        bv, ba = sdq.DitBlock(lv, True), sdq.DitBlock(la, True)
+        bv.set_norms(nv)
+        ba.set_norms(na)
+        # the GPU: fusion layer order (ovi_dit.cpp:726-734)
+        ba.step(gxa, g_ctx_a, dv(ea), heads, cs=g_cs_a, phases=sdq.SELF)
+        bv.step(gxv, g_ctx_v, dv(ev), heads, cs=g_cs_v, phases=sdq.SELF)
+        og_a = gxa.clone()
+        ba.step(gxa, g_ctx_a, dv(ea), heads, cs=g_cs_a, target=gxv, cs_tgt=g_cs_v,
+                phases=sdq.CROSS_FFN)
+        bv.step(gxv, g_ctx_v, dv(ev), heads, cs=g_cs_v, target=og_a, cs_tgt=g_cs_a,
+                phases=sdq.CROSS_FFN)
+        torch.cuda.synchronize()
+        bv.free()
+        ba.free()
+        # the two CPU chains, same order
+        for kind in ("want", "exact"):
+            xv, xa = (want_v, want_a) if kind == "want" else (ex_v, ex_a)
+            kw_a = kw_v = {}
+            if kind == "exact":
+                kw_a = dict(sdpa=gsd, fc1_gelu=_gpu_fc1_gelu(la))
+                kw_v = dict(sdpa=gsd, fc1_gelu=_gpu_fc1_gelu(lv))
+            xa1 = _ref_block(ops, xa, ctx_a, ea, la, na, heads, cs_a, True, phases=1, **kw_a)
+            xv1 = _ref_block(ops, xv, ctx_v, ev, lv, nv, heads, cs_v, True, phases=1, **kw_v)
+            xa2 = _ref_block(ops, xa1, ctx_a, ea, la, na, heads, cs_a, True, xv1, cs_v, 2, **kw_a)
+            xv2 = _ref_block(ops, xv1, ctx_v, ev, lv, nv, heads, cs_v, True, xa1, cs_a, 2, **kw_v)
+            if kind == "want":
+                want_v, want_a = xv2, xa2
+            else:
+                ex_v, ex_a = xv2, xa2
+        got_v, got_a = gxv.cpu().numpy(), gxa.cpu().numpy()
+        assert_bitexact(got_v, ex_v, f"layer {i} video vs the chain with the GPU's sdpa and GELU")
+        assert_bitexact(got_a, ex_a, f"layer {i} audio vs the chain with the GPU's sdpa and GELU")
+        row = {"layer": i}
+        for name, g, w in (("video", got_v, want_v), ("audio", got_a, want_a)):
+            err = np.abs(g.astype(np.float64) - w) / (np.abs(w).max() + 1e-30)
+            row[name] = (round(_cos(g, w), 8), float(f"{err.max():.3e}"))
+        report.append(row)
+        print(f"  layer {i}: cosine / max rel err vs the reference chain: "
+              f"video {row['video']}, audio {row['audio']}", flush=True)
+        for name in ("video", "audio"):
+            cos, err = row[name]
+            assert cos > 0.99, (i, name, cos)  # the reference's own int8 DiT gate
+            assert err < 0.1, (i, name, err)

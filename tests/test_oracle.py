@@ -433,3 +433,35 @@ def test_ref_glue_fixture_outputs(oracle):
     assert_bitexact(oracle.rope(x, oracle.rope_cs(g["ang3"]), 2), g["rope3"], "apply_rope 3-D")
     assert_bitexact(oracle.rope(x, oracle.rope_cs(g["ang1"]), 2), g["rope1"], "apply_rope 1-D")
     assert_bitexact(oracle.sdpa(g["q"], g["k"], g["v"], 2), g["sdpa"], "sdpa")
+
+
+def test_reference_build_block_chain_equals_oracle_chain(oracle, ref):
+    """The block chain the GPU drift test runs on the reference build's own
+    functions (qgemm, sdpa, layernorm, mod_rows, rmsnorm) gives the oracle
+    chain's bits: two fusion layers of a twin backbone at small widths."""
+    from test_gpu_block_full import _norms, _ref_block, _weights
+    from test_gpu_drift import _RefOps
+
+    dim, heads, Mv, Ma, Mc = 256, 2, 48, 20, 16
+    ops = _RefOps(oracle, ref)
+    xv = oracle.randn(Mv * dim, 1).reshape(Mv, dim)
+    xa = oracle.randn(Ma * dim, 2).reshape(Ma, dim)
+    cv = oracle.randn(Mc * dim, 3).reshape(Mc, dim)
+    ca = oracle.randn(Mc * dim, 4).reshape(Mc, dim)
+    cs_v = oracle.rope_cs(oracle.rope_freqs_3d(1, 12, 4, 128))
+    cs_a = oracle.rope_cs(oracle.rope_freqs_1d(Ma, 128, 10000.0, 0.19676))
+    chains = []
+    for o in (oracle, ops):
+        a, v = xa, xv
+        for i in range(2):
+            lv, la = _weights(oracle, dim, 512, 10 + i, True), _weights(oracle, dim, 512, 50 + i, True)
+            nv, na = _norms(oracle, dim, 20 + i), _norms(oracle, dim, 30 + i)
+            ev = (oracle.randn(6 * dim, 40 + i) * np.float32(0.3)).reshape(6, dim)
+            ea = (oracle.randn(6 * dim, 60 + i) * np.float32(0.3)).reshape(6, dim)
+            a1 = _ref_block(o, a, ca, ea, la, na, heads, cs_a, True, phases=1)
+            v1 = _ref_block(o, v, cv, ev, lv, nv, heads, cs_v, True, phases=1)
+            a = _ref_block(o, a1, ca, ea, la, na, heads, cs_a, True, v1, cs_v, 2)
+            v = _ref_block(o, v1, cv, ev, lv, nv, heads, cs_v, True, a1, cs_a, 2)
+        chains.append((v, a))
+    assert_bitexact(chains[1][0], chains[0][0], "video chain")
+    assert_bitexact(chains[1][1], chains[0][1], "audio chain")
