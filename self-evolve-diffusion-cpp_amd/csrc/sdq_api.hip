@@ -12,6 +12,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <cstdio>
 #include <cstdlib>
@@ -270,6 +271,7 @@ struct LnMod {
 int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                    const sdq_epilogue* epi, void* Y, hipStream_t s, const RowMax* pre = nullptr,
                    RowMax* rmax_out = nullptr, const LnMod* lnmod = nullptr) {
+  const bool prof = t_prof;
   int rc = check_weight(w, K);
   if (rc) return rc;
   if ((rc = validate_epi(epi))) return rc;
@@ -294,10 +296,10 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
     if (ea.gate) vec = vec && aligned16(ea.gate);
     if (ea.resid) vec = vec && aligned16(ea.resid);
     if (rmax_out) rmax_out->chunks = 0;
-    hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+    hipEvent_t p0 = prof ? prof_mark(s) : nullptr;
     hipError_t e = launch_qgemm_qin(w->frags, w->scale, A, M, K, N, w->KFp, ea, Y, vec, s);
     if (e != hipSuccess) return hip_error(e, "qgemm launch");
-    if (t_prof) {
+    if (prof) {
       hipEvent_t p1 = prof_mark(s);
       if (p0 && p1) {
         t_recs.push_back({"qgemm_skinny_qin", p0, p1});
@@ -340,7 +342,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   cc.N = N;
   cc.CP = (int64_t)col_cap;
 
-  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  hipEvent_t p0 = prof ? prof_mark(s) : nullptr;
   hipError_t e =
       lnmod ? launch_act_quant_frags_lnmod(A, M, K, Mp, w->KFp, ws->at, ws->as, cc, lnmod->shift,
                                            lnmod->scale, lnmod->eps, ws->st, s)
@@ -349,14 +351,14 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                : launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
                                         pmax_bytes ? ws->pmax : nullptr, cu_count, s);
   if (e != hipSuccess) return hip_error(e, "act_quant launch");
-  hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
+  hipEvent_t p1 = prof ? prof_mark(s) : nullptr;
   int vec = (N % 4 == 0) && aligned16(Y);
   if (ea.bias) vec = vec && aligned16(ea.bias);
   if (ea.gate) vec = vec && aligned16(ea.gate);
   if (ea.resid) vec = vec && aligned16(ea.resid);
   int tail = 0;
   hipEvent_t pmid = nullptr;
-  if (t_prof && hipEventCreate(&pmid) != hipSuccess) pmid = nullptr;
+  if (prof && hipEventCreate(&pmid) != hipSuccess) pmid = nullptr;
   GemmAux aux{cc.bias_pad, cc.gate_pad, ws->sink, g_dev[w->device].cu_count, splitk,
               splitk > 1 ? ws->part : nullptr, rmax_out ? &rmax_out->chunks : nullptr, &tail,
               pmid};
@@ -365,7 +367,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
     if (pmid) (void)hipEventDestroy(pmid);
     return hip_error(e, "qgemm launch");
   }
-  if (t_prof) {
+  if (prof) {
     hipEvent_t p2 = prof_mark(s);
     if (p0 && p1 && p2 && (!tail || pmid)) {
       t_recs.push_back({lnmod ? "ln_mod_quant" : premax ? "act_quant_premax" : "act_quant", p0, p1});
@@ -598,12 +600,27 @@ int upload_threads() {
   return (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
 }
 
-// pread of [off, off + bytes) into dst, split over up to `threads` threads
-// (large sequential reads; a page-cache or NVMe read runs faster in
-// parallel). Returns false on a short read or an I/O error.
-bool par_pread(int fd, char* dst, uint64_t off, size_t bytes, int threads) {
-  constexpr size_t kMinPerThread = size_t(8) << 20;
-  auto span = [fd](char* d, uint64_t o, size_t b) {
+// One file range to read into host memory.
+struct ReadSpan {
+  char* dst;
+  uint64_t off;
+  size_t bytes;
+};
+
+// Reads every span, cut into chunks of at most kChunk bytes spread over up to
+// `threads` threads: large sequential reads with enough of them in flight for
+// a page cache or an NVMe queue. Returns false on a short read or an I/O
+// error.
+bool read_spans(int fd, const std::vector<ReadSpan>& spans, int threads) {
+  constexpr size_t kChunk = size_t(4) << 20;
+  std::vector<ReadSpan> chunks;
+  for (const ReadSpan& s : spans)
+    for (size_t a = 0; a < s.bytes; a += kChunk)
+      chunks.push_back({s.dst + a, s.off + a, std::min(kChunk, s.bytes - a)});
+  auto one = [fd](const ReadSpan& c) {
+    char* d = c.dst;
+    uint64_t o = c.off;
+    size_t b = c.bytes;
     while (b) {
       const ssize_t got = ::pread(fd, d, b, (off_t)o);
       if (got < 0 && errno == EINTR) continue;
@@ -614,17 +631,22 @@ bool par_pread(int fd, char* dst, uint64_t off, size_t bytes, int threads) {
     }
     return true;
   };
-  const int t = (int)std::min<size_t>((size_t)threads, std::max<size_t>(1, bytes / kMinPerThread));
-  if (t <= 1) return span(dst, off, bytes);
-  std::vector<std::thread> pool;
-  std::vector<char> ok(t, 0);
-  const size_t chunk = round_up((int64_t)((bytes + t - 1) / t), 4096);
-  for (int i = 0; i < t; i++) {
-    const size_t a = std::min(bytes, (size_t)i * chunk), b = std::min(bytes, a + chunk);
-    pool.emplace_back([&, i, a, b] { ok[i] = span(dst + a, off + a, b - a); });
+  const int t = (int)std::min<size_t>((size_t)std::max(threads, 1), chunks.size());
+  if (t <= 1) {
+    for (const ReadSpan& c : chunks)
+      if (!one(c)) return false;
+    return true;
   }
+  std::atomic<size_t> next{0};
+  std::atomic<bool> ok{true};
+  std::vector<std::thread> pool;
+  for (int i = 0; i < t; i++)
+    pool.emplace_back([&] {
+      for (size_t j; ok && (j = next.fetch_add(1)) < chunks.size();)
+        if (!one(chunks[j])) ok = false;
+    });
   for (auto& th : pool) th.join();
-  return std::all_of(ok.begin(), ok.end(), [](char v) { return v != 0; });
+  return ok;
 }
 
 }  // namespace
@@ -710,16 +732,29 @@ int sdq_weight_upload_file(const char* path, const sdq_weight_fsrc* src, int n, 
   }
   if (rc == SDQ_OK) {
     (void)::posix_fadvise(fd, 0, 0, POSIX_FADV_SEQUENTIAL);
-    const int threads = upload_threads();
-    auto fill = [&](int i, char* pin, size_t soff) {
+    const int threads = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    // the kernel's read-ahead of a weight's ranges (no wait)
+    auto prefetch = [&](int i) {
+      if (i >= n) return;
       const sdq_weight_fsrc& w = src[i];
+      for (int p = 0; p < w.nparts; p++) {
+        (void)::posix_fadvise(fd, (off_t)w.q_off[p], (off_t)(w.rows[p] * w.K), POSIX_FADV_WILLNEED);
+        (void)::posix_fadvise(fd, (off_t)w.scale_off[p], (off_t)(w.rows[p] * 4), POSIX_FADV_WILLNEED);
+      }
+    };
+    prefetch(0);
+    auto fill = [&](int i, char* pin, size_t soff) {
+      prefetch(i + 1);
+      const sdq_weight_fsrc& w = src[i];
+      std::vector<ReadSpan> spans;
       size_t r = 0;
       for (int p = 0; p < w.nparts; p++) {
-        if (!par_pread(fd, pin + r * (size_t)w.K, w.q_off[p], (size_t)(w.rows[p] * w.K), threads) ||
-            !par_pread(fd, pin + soff + r * 4, w.scale_off[p], (size_t)w.rows[p] * 4, 1))
-          return set_error(SDQ_ERR_FORMAT, std::string("short read from ") + path);
+        spans.push_back({pin + r * (size_t)w.K, w.q_off[p], (size_t)(w.rows[p] * w.K)});
+        spans.push_back({pin + soff + r * 4, w.scale_off[p], (size_t)w.rows[p] * 4});
         r += (size_t)w.rows[p];
       }
+      if (!read_spans(fd, spans, threads))
+        return set_error(SDQ_ERR_FORMAT, std::string("short read from ") + path);
       return SDQ_OK;
     };
     rc = upload_ring(dev, Ns, Ks, fill, static_cast<hipStream_t>(stream), out);
