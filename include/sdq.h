@@ -155,6 +155,22 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale);
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
                 void* Y, void* stream);
 
+/* sdq_qlinear for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. The same results as sdq_qlinear, bit for
+ * bit, with no hipMalloc / hipFree or other allocation on any call: the
+ * quantized activations and the GEMM's other scratch live in a static device
+ * array of SDQ_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).
+ * Limit: the call's scratch (about M*K bytes of quantized activations, plus
+ * 8*N bytes and, for split-K shapes, up to 32*M*N bytes) must fit that array, e.g.
+ * up to 4096 rows at K = 14336 or 20480 rows at K = 3072; larger calls fail
+ * with SDQ_ERR_INVALID before anything is launched. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams,
+ * threads) race; serialize them. No profiling records are made. */
+#define SDQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int sdq_qlinear_noalloc(const sdq_weight* w, const float* A, int64_t M, int64_t K,
+                        const sdq_epilogue* epi, void* Y, void* stream);
+
 /* The FFN of a DiT block after its norm (src/model/ovi_dit.cpp:218-221,
  * ffn_fwd):  hid = gelu_tanh(mlin(h, fc1));  x = fma(mlin(hid, fc2), gate, x)
  * (gate_fma = 0: x + fl(y*gate)). fc1 is [F,D], fc2 [D,F]; h and x are

@@ -28,6 +28,13 @@
 
 #include "sdq_internal.h"
 
+// Scratch memory of sdq_qlinear_noalloc: a file-scope device array, one copy
+// per GPU (each holds it until the process ends). In host code this name is
+// only a stand-in for the symbol: host code uses the address that
+// hipGetSymbolAddress returns for the current device (DevState::scratch),
+// never the name itself.
+static __device__ __align__(256) char scratch[SDQ_NOALLOC_SCRATCH_BYTES];
+
 struct sdq_weight {
   int device;
   int64_t N, K, Np, KFp;
@@ -45,6 +52,8 @@ struct DevState {
   bool ready = false;
   int cu_count = 0;
   hipDeviceProp_t prop{};
+  char* scratch = nullptr;    // this device's copy of `scratch` (hipGetSymbolAddress)
+  std::string scratch_err;    // why scratch is null, if it is
 };
 
 constexpr int kMaxDev = 64;
@@ -109,6 +118,16 @@ int ensure_device(int dev) {
     return set_error(SDQ_ERR_NODEV, std::string("sdq kernels are built for gfx950, device is ") +
                                         d.prop.gcnArchName);
   d.cu_count = d.prop.multiProcessorCount;
+  // The no-alloc entry point's scratch on this device (current here): looked
+  // up once; a failure only disables that entry point.
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e == hipSuccess && p) {
+    d.scratch = static_cast<char*>(p);
+  } else {
+    (void)hipGetLastError();
+    d.scratch_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+  }
   d.ready = true;
   return SDQ_OK;
 }
@@ -268,10 +287,16 @@ struct LnMod {
 // Core device-pointer path shared by the entry points. `pre` (nullable):
 // A's row maxima are known; `rmax_out` (nullable, GELU): write Y's; `lnmod`
 // (nullable): quantize mod_rows(layernorm(A)) instead of A.
+// `fixed` (nullable): the no-alloc mode, all scratch carved from this
+// device's static scratch array instead of the grown workspace (nothing is
+// allocated; no profiling events are made).
 int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                    const sdq_epilogue* epi, void* Y, hipStream_t s, const RowMax* pre = nullptr,
-                   RowMax* rmax_out = nullptr, const LnMod* lnmod = nullptr) {
-  const bool prof = t_prof;
+                   RowMax* rmax_out = nullptr, const LnMod* lnmod = nullptr,
+                   char* fixed = nullptr) {
+  if (fixed && (pre || rmax_out || lnmod))
+    return set_error(SDQ_ERR_INVALID, "no-alloc mode covers the plain qlinear only");
+  const bool prof = t_prof && !fixed;
   int rc = check_weight(w, K);
   if (rc) return rc;
   if ((rc = validate_epi(epi))) return rc;
@@ -318,9 +343,36 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   const size_t part_bytes = splitk > 1 ? (size_t)splitk * (size_t)M * (size_t)N * 4 : 0;
   const int cu_count = g_dev[w->device].cu_count;
   const size_t pmax_bytes = (size_t)act_quant_pmax_floats(Mp, w->KFp, cu_count) * sizeof(float);
-  if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap, part_bytes,
-                      pmax_bytes, &ws)))
+  Workspace fixed_ws;
+  if (fixed) {
+    // Every region is rewritten by this call's kernels before it is read
+    // (the quantizer writes all Mp rows of fragments and the padded column
+    // copies; split-K items write their whole slices; the pmax kernel every
+    // chunk it hands on), so nothing needs clearing between calls.
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      char* p = fixed + off;
+      off += (size_t)round_up((int64_t)bytes, 256);
+      return p;
+    };
+    fixed_ws.at = reinterpret_cast<int8_t*>(take(at_bytes));
+    fixed_ws.as = reinterpret_cast<float*>(take((size_t)Mp * sizeof(float)));
+    fixed_ws.cols = reinterpret_cast<float*>(take(col_cap * 2 * sizeof(float)));
+    fixed_ws.col_cap = col_cap;
+    fixed_ws.sink = reinterpret_cast<float*>(take(4096));
+    if (part_bytes) fixed_ws.part = reinterpret_cast<int*>(take(part_bytes));
+    if (pmax_bytes) fixed_ws.pmax = reinterpret_cast<float*>(take(pmax_bytes));
+    if (off > (size_t)SDQ_NOALLOC_SCRATCH_BYTES)
+      return set_error(SDQ_ERR_INVALID,
+                       "sdq_qlinear_noalloc: M=" + std::to_string(M) + ", K=" + std::to_string(K) +
+                           ", N=" + std::to_string(N) + " needs " + std::to_string(off) +
+                           " bytes of scratch; the no-alloc entry point has " +
+                           std::to_string((size_t)SDQ_NOALLOC_SCRATCH_BYTES));
+    ws = &fixed_ws;
+  } else if ((rc = workspace(w->device, s, at_bytes, (size_t)Mp * sizeof(float), col_cap,
+                             part_bytes, pmax_bytes, &ws))) {
     return rc;
+  }
   EpiArgs ea = make_epi(epi, K);
   if (rmax_out) {
     ea.rmax = rmax_out->p;
@@ -1099,6 +1151,23 @@ int sdq_stream_sync(void* stream) {
 int sdq_profile_begin(void) {
   t_prof = true;
   return SDQ_OK;
+}
+
+int sdq_qlinear_noalloc(const sdq_weight* w, const float* A, int64_t M, int64_t K,
+                        const sdq_epilogue* epi, void* Y, void* stream) {
+  int rc = check_weight(w, K);
+  if (rc) return rc;
+  if ((rc = ensure_device(w->device))) return rc;
+  char* p = nullptr;
+  std::string why;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    p = g_dev[w->device].scratch;
+    why = g_dev[w->device].scratch_err;
+  }
+  if (!p) return set_error(SDQ_ERR_HIP, "sdq_qlinear_noalloc: scratch unavailable (" + why + ")");
+  return qlinear_device(w, A, M, K, epi, Y, static_cast<hipStream_t>(stream), nullptr, nullptr,
+                        nullptr, p);
 }
 
 int sdq_qlinear_plan(const sdq_weight* w, int64_t M, int epi_kind, sdq_gemm_plan* out) {

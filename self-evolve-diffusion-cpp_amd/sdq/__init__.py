@@ -72,6 +72,8 @@ SIGNATURES = {
     "sdq_weight_export_host": (ctypes.c_int, [_vp, _vp, _vp]),
     "sdq_qlinear": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp, _vp]),
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "sdq_qlinear_noalloc": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp,
+                                           _vp]),
     "sdq_rmsnorm_rope_batch": (ctypes.c_int, [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_float,
                                               _vp]),
     "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
@@ -374,6 +376,23 @@ def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, ga
     e = _epilogue_args(c, kind, M, w.N, out, bias, gate, resid, gate_fma)
     c.done()
     _check(_lib.sdq_qlinear(h, pa, M, w.K, ctypes.byref(e), _ptr(out), _stream(stream)))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # SDQ_NOALLOC_SCRATCH_BYTES
+
+
+def qlinear_noalloc(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None,
+                    gate_fma=True, stream=None):
+    """qlinear without any device allocation (sdq_qlinear_noalloc: scratch in a
+    static per-GPU array; calls that overlap on one GPU race)."""
+    c = _Args()
+    h = _weight(w)
+    pa = c(A, "A", "f32", (None, w.K))
+    M = A.shape[0]
+    e = _epilogue_args(c, kind, M, w.N, out, bias, gate, resid, gate_fma)
+    c.done()
+    _check(_lib.sdq_qlinear_noalloc(h, pa, M, w.K, ctypes.byref(e), _ptr(out), _stream(stream)))
     return out
 
 
