@@ -270,6 +270,21 @@ int sdq_sdpa_batched(const float* q, int64_t ldq, const float* k, int64_t ldk, c
                      int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
                      int head_dim, int batch, void* stream);
 
+/* The F32 branch of mlin (src/model/ovi_dit.cpp:80-82 -> blk::linear,
+ * src/model/blocks.cpp:14-16 -> sd::matmul, src/core/gemm.cpp:115-160), for
+ * the Linears a pack keeps in fp32 (the audio head [20, 3072]):
+ *   y[M,N] = x[M,K] . w[K,N] (+ bias[N])
+ * with w in the [in, out] layout lin() gives F32 weights (transp2d,
+ * ovi_dit.cpp:409). Bit-exact with the reference's matmul: per output one
+ * fused multiply-add chain over k in order from +0 (gemm.cpp:45-75), then
+ * fl(c + bias) (add_bias, gemm.cpp:33-40); K == 0 gives 0 (+ bias). The
+ * OpenBLAS route the reference takes above 64M multiply-adds in an OpenBLAS
+ * build sums in another order and is not reproduced. bias nullable; x, w,
+ * bias, y device arrays (y must not overlap x or w). Stream-ordered.
+ * Replaces: blk::linear / sd::matmul for F32 Linears. */
+int sdq_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t N,
+                   const float* bias, float* y, void* stream);
+
 /* Plain sd::qgemm: Y = qgemm(A, W) with no bias (src/core/qgemm.cpp:73). */
 int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* Y, void* stream);
 

@@ -43,6 +43,7 @@ def _load():
     lib.orc_bias_add.argtypes = [_f32p, _f32p, _i64, _i64]
     lib.orc_gated_add.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_int]
     lib.orc_add.argtypes = [_f32p, _f32p, _i64]
+    lib.orc_linear_f32.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_void_p, _f32p]
     lib.orc_gelu_tanh.argtypes = [_f32p, _i64]
     lib.orc_layernorm.argtypes = [_f32p, _i64, _i64, ctypes.c_float, _f32p]
     lib.orc_layernorm_affine.argtypes = [_f32p, _i64, _i64, ctypes.c_void_p, ctypes.c_void_p,
@@ -188,6 +189,19 @@ def add(x, y):
     x = np.array(x, np.float32, copy=True, order="C")
     lib().orc_add(x.reshape(-1), np.ascontiguousarray(y, np.float32).reshape(-1), x.size)
     return x
+
+
+def linear_f32(x, w, bias=None):
+    """The F32 Linear (blk::linear -> sd::matmul): x [M,K] . w [K,N] (+ bias)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    M, K = x.shape
+    K2, N = w.shape
+    assert K == K2, (x.shape, w.shape)
+    y = np.empty((M, N), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_linear_f32(x, M, K, w, N, None if b is None else b.ctypes.data, y)
+    return y
 
 
 def gelu_tanh(x):
@@ -363,6 +377,8 @@ class Ref:
         L.sdref_rope_freqs_1d.restype = ctypes.c_int
         L.sdref_sdpa.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_int, _f32p]
         L.sdref_sdpa.restype = ctypes.c_int
+        L.sdref_matmul.argtypes = [_f32p, _i64, _i64, _f32p, _i64, ctypes.c_void_p, _f32p]
+        L.sdref_matmul.restype = ctypes.c_int
         self.L = L
         self.set_nthreads(nthreads or nthreads_default())
 
@@ -383,6 +399,18 @@ class Ref:
         out = np.empty((M, N), np.float32)
         if self.L.sdref_qgemm(A, Bq, bs, M, K, N, out) != 0:
             raise RuntimeError("reference qgemm threw")
+        return out
+
+    def matmul(self, x, w, bias=None):
+        """sd::matmul (gemm.cpp:115): x [M,K] . w [K,N] (+ bias)."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        M, K = x.shape
+        N = w.shape[1]
+        out = np.empty((M, N), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        if self.L.sdref_matmul(x, M, K, w, N, None if b is None else b.ctypes.data, out) != 0:
+            raise RuntimeError("reference matmul threw")
         return out
 
     def quantize_rowwise(self, W):

@@ -49,6 +49,14 @@
  *                          reference golden replica (lround) bit-exact.
  *   orc_quant_rows       - closed form of the packer's numpy expression
  *                          (float32 semantics) evaluated by numpy itself.
+ *   orc_linear_f32       - compiled reference sd::matmul (oracle/_ref, AVX2+FMA
+ *                          path) bit-exact, incl. K = 0, no bias, -0 bias,
+ *                          denormal products; exact rational evaluation of
+ *                          the fma chain (each step rounded once) on tiny
+ *                          cases; exact integer dot products when every
+ *                          partial sum is an integer below 2^24; committed
+ *                          outputs of the reference build
+ *                          (tests/golden/ref_linear_f32.npz).
  *   orc_randu            - compiled reference sd::randu bit-exact.
  *   orc_randn            - closed-form splitmix64 + Box-Muller in numpy float64.
  *
@@ -225,6 +233,26 @@ void orc_gated_add(float* x, const float* y, const float* g, int64_t M, int64_t 
       int64_t o = i * N + j;
       if (use_fma) x[o] = fmaf(y[o], g[j], x[o]);
       else { float p = y[o] * g[j]; x[o] = x[o] + p; }
+    }
+}
+
+/* The F32 branch of mlin (src/model/ovi_dit.cpp:80-82): blk::linear
+ * (src/model/blocks.cpp:14-16) -> sd::matmul (src/core/gemm.cpp:115-160) as
+ * the reference build runs it without OpenBLAS (or below its 64M
+ * multiply-add threshold, gemm.cpp:16, 132): row_group (gemm.cpp:45-75)
+ * clears each output's accumulator to +0 and adds one fused multiply-add per
+ * k in order; add_bias (gemm.cpp:33-40) then adds b[j] in a separate pass.
+ * K == 0 leaves the zero output (+ bias, gemm.cpp:123-126).
+ * x [M,K], w [K,N] (lin()'s transposed layout, ovi_dit.cpp:409), bias
+ * nullable, y [M,N]. */
+void orc_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t N,
+                    const float* bias, float* y) {
+  for (int64_t i = 0; i < M; i++)
+    for (int64_t j = 0; j < N; j++) {
+      float c = 0.f;
+      for (int64_t k = 0; k < K; k++) c = fmaf(x[i * K + k], w[k * N + j], c);
+      if (bias) c = c + bias[j];
+      y[i * N + j] = c;
     }
 }
 

@@ -53,6 +53,22 @@ int sdref_qgemm(const float* A, const int8_t* Bq, const float* bs, int64_t M, in
   }
 }
 
+// sd::matmul (src/core/gemm.cpp:115): C[M,N] = A[M,K] . B[K,N] (+ bias[N]),
+// the fp32 Linear of blk::linear (src/model/blocks.cpp:14-16).
+int sdref_matmul(const float* A, int64_t M, int64_t K, const float* B, int64_t N,
+                 const float* bias, float* out) {
+  try {
+    sd::Tensor a = view(A, {M, K}, sd::DType::F32, 4);
+    sd::Tensor b = view(B, {K, N}, sd::DType::F32, 4);
+    sd::Tensor o;
+    sd::matmul(a, b, o, bias);
+    if (M * N > 0) std::memcpy(out, o.data, (size_t)(M * N) * 4);
+    return 0;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}
+
 // sd::quantize_rowwise (src/core/tensor.cpp:63).
 int sdref_quantize_rowwise(const float* W, int64_t N, int64_t K, int8_t* q, float* s) {
   sd::Tensor w = view(W, {N, K}, sd::DType::F32, 4);

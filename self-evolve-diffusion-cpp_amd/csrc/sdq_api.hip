@@ -1004,6 +1004,31 @@ int sdq_add(float* x, const float* y, int64_t n, void* stream) {
   return e == hipSuccess ? SDQ_OK : hip_error(e, "add launch");
 }
 
+int sdq_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t N,
+                   const float* bias, float* y, void* stream) {
+  if (M < 0 || K < 0 || N < 0) return set_error(SDQ_ERR_INVALID, "linear_f32: negative dims");
+  if (M == 0 || N == 0) return SDQ_OK;
+  if (!y || (K > 0 && (!x || !w))) return set_error(SDQ_ERR_INVALID, "linear_f32: null pointer");
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+  const hipError_t e = launch_linear_f32(x, M, K, w, N, bias, y, g_dev[dev].cu_count, s);
+  if (e != hipSuccess) return hip_error(e, "linear_f32 launch");
+  if (t_prof) {
+    hipEvent_t p1 = prof_mark(s);
+    if (p0 && p1) {
+      t_recs.push_back({"linear_f32", p0, p1});
+    } else {
+      for (hipEvent_t ev : {p0, p1})
+        if (ev) (void)hipEventDestroy(ev);
+    }
+  }
+  return SDQ_OK;
+}
+
 int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
              float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
              void* stream) {

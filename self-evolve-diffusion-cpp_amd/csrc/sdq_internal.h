@@ -122,6 +122,10 @@ hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* s
                            const float* b, float* y, hipStream_t s);
 // x[i] += y[i], i < n.
 hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s);
+// y[M,N] = x[M,K] . w[K,N] (+ bias): one fmaf chain per output over k in
+// order from +0, then + bias (sd::matmul's per-output steps).
+hipError_t launch_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t N,
+                             const float* bias, float* y, int cu_count, hipStream_t s);
 // Attention, head_dim 128 (launch_sdpa rejects nothing else; the API checks):
 // out[i, head cols] = softmax(q_i . k_j / sqrt(128)) v_j over j < Lk.
 // batch > 1: `batch` sequences stacked along the rows (sequence b: query rows

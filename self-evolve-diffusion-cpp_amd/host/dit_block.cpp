@@ -110,23 +110,6 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
           "DitBlock ffn");
 }
 
-DeviceFloats::DeviceFloats(size_t n) {
-  void* p = nullptr;
-  check(sdq_device_alloc(n * sizeof(float), &p), "DeviceFloats");
-  p_ = static_cast<float*>(p);
-}
-
-DeviceFloats& DeviceFloats::operator=(DeviceFloats&& o) noexcept {
-  if (this != &o) {
-    sdq_device_free(p_);
-    p_ = o.p_;
-    o.p_ = nullptr;
-  }
-  return *this;
-}
-
-DeviceFloats::~DeviceFloats() { sdq_device_free(p_); }
-
 void DitBlock::set_norms(const sd_dit_norms& n) {
   const float* v[kNorms] = {n.sa_nq, n.sa_nk, n.ca_nq, n.ca_nk, n.ln3_w,
                             n.ln3_b, n.nk_fusion, n.pnf_w, n.pnf_b};

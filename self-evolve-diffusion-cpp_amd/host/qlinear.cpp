@@ -1,6 +1,7 @@
 // sd::gpu::QLinear — see sd/qlinear.h.
 #include "sd/qlinear.h"
 
+#include <algorithm>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -308,6 +309,117 @@ LinearPart linear_part_from_pack(const std::unordered_map<std::string, Tensor>& 
 QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                           const std::string& base, int64_t in, int64_t out) {
   return QLinear(std::vector<LinearPart>{linear_part_from_pack(pack, base, in, out)});
+}
+
+DeviceFloats::DeviceFloats(size_t n) {
+  void* p = nullptr;
+  check(sdq_device_alloc(n * sizeof(float), &p), "DeviceFloats");
+  p_ = static_cast<float*>(p);
+}
+
+DeviceFloats& DeviceFloats::operator=(DeviceFloats&& o) noexcept {
+  if (this != &o) {
+    sdq_device_free(p_);
+    p_ = o.p_;
+    o.p_ = nullptr;
+  }
+  return *this;
+}
+
+DeviceFloats::~DeviceFloats() { sdq_device_free(p_); }
+
+namespace {
+
+// A pack entry's values as floats (to_f32 for BF16, src/core/tensor.cpp:44-53).
+std::vector<float> entry_floats(const Tensor& t) {
+  const int64_t n = t.numel();
+  std::vector<float> v((size_t)n);
+  if (t.dtype == DType::F32) {
+    std::memcpy(v.data(), t.data, (size_t)n * sizeof(float));
+  } else {
+    const uint16_t* h = static_cast<const uint16_t*>(t.data);
+    for (int64_t i = 0; i < n; i++) {
+      const uint32_t bits = (uint32_t)h[i] << 16;
+      std::memcpy(&v[(size_t)i], &bits, 4);
+    }
+  }
+  return v;
+}
+
+}  // namespace
+
+Linear::Linear(const float* w_out_in, const float* bias, int64_t out, int64_t in)
+    : in_(in), out_(out), f32_(true) {
+  if (!w_out_in || out <= 0 || in < 0) throw std::runtime_error("Linear: bad fp32 weight");
+  std::vector<float> t((size_t)(in * out));
+  for (int64_t o = 0; o < out; o++)
+    for (int64_t i = 0; i < in; i++) t[(size_t)(i * out + o)] = w_out_in[o * in + i];
+  if (!t.empty()) {
+    w_ = DeviceFloats(t.size());
+    check(sdq_memcpy(w_.get(), t.data(), t.size() * sizeof(float), SDQ_H2D, nullptr),
+          "Linear weight upload");
+  }
+  if (bias) {
+    b_ = DeviceFloats((size_t)out);
+    check(sdq_memcpy(b_.get(), bias, (size_t)out * sizeof(float), SDQ_H2D, nullptr),
+          "Linear bias upload");
+  }
+  check(sdq_stream_sync(nullptr), "Linear upload");
+}
+
+Linear::Linear(QLinear&& q) : q_(std::move(q)) {
+  in_ = q_.in_features();
+  out_ = q_.out_features();
+}
+
+void Linear::forward_device(const float* x, int64_t M, float* y, void* stream) const {
+  if (!f32_) {
+    q_.forward_device(x, M, SDQ_EPI_NONE, nullptr, nullptr, y, stream);
+    return;
+  }
+  check(sdq_linear_f32(x, M, in_, w_.get(), out_, b_.get(), y, stream), "Linear::forward_device");
+}
+
+void Linear::mlin(const Tensor& x, Tensor& y) const {
+  if (!f32_) {
+    q_.mlin(x, y);
+    return;
+  }
+  if (x.dtype != DType::F32) throw std::runtime_error("Linear: x must be F32");
+  const int64_t M = x.rows(), K = x.cols();
+  if (K != in_)
+    throw std::runtime_error("Linear: x has " + std::to_string(K) + " columns, weight expects " +
+                             std::to_string(in_));
+  y = Tensor({M, out_}, DType::F32);
+  if (M == 0) return;
+  DeviceFloats dx((size_t)std::max<int64_t>(M * K, 1)), dy((size_t)(M * out_));
+  if (M * K > 0)
+    check(sdq_memcpy(dx.get(), x.data, (size_t)(M * K) * sizeof(float), SDQ_H2D, nullptr),
+          "Linear x");
+  forward_device(dx.get(), M, dy.get(), nullptr);
+  check(sdq_memcpy(y.data, dy.get(), (size_t)(M * out_) * sizeof(float), SDQ_D2H, nullptr),
+        "Linear y");
+  check(sdq_stream_sync(nullptr), "Linear");
+}
+
+Linear linear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                        const std::string& base, int64_t in, int64_t out) {
+  auto get = [&](const std::string& n) -> const Tensor& {
+    auto it = pack.find(n);
+    if (it == pack.end() || !it->second.data)
+      throw std::runtime_error("ovi_dit: missing tensor " + n);
+    return it->second;
+  };
+  const Tensor& w = get(base + ".weight");
+  if (w.shape.size() != 2 || w.shape[0] != out || w.shape[1] != in)
+    throw std::runtime_error("ovi_dit: bad shape for " + base + ".weight");
+  if (w.dtype == DType::I8) return Linear(qlinear_from_pack(pack, base, in, out));
+  const std::vector<float> wf = entry_floats(w);
+  const Tensor& b = get(base + ".bias");
+  if (b.shape.size() != 1 || b.shape[0] != out || b.dtype == DType::I8)
+    throw std::runtime_error("ovi_dit: bad shape for " + base + ".bias");
+  const std::vector<float> bf = entry_floats(b);
+  return Linear(wf.data(), bf.data(), out, in);
 }
 
 }  // namespace gpu

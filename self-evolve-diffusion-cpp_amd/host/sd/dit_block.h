@@ -175,23 +175,6 @@ const char* sd_dit_last_error(void);
 namespace sd {
 namespace gpu {
 
-// Owning device array of floats (sdq_device_alloc), move-only.
-class DeviceFloats {
- public:
-  DeviceFloats() = default;
-  explicit DeviceFloats(size_t n);
-  DeviceFloats(const DeviceFloats&) = delete;
-  DeviceFloats& operator=(const DeviceFloats&) = delete;
-  DeviceFloats(DeviceFloats&& o) noexcept : p_(o.p_) { o.p_ = nullptr; }
-  DeviceFloats& operator=(DeviceFloats&& o) noexcept;
-  ~DeviceFloats();
-  float* get() const { return p_; }
-  explicit operator bool() const { return p_ != nullptr; }
-
- private:
-  float* p_ = nullptr;
-};
-
 class DitBlock {
  public:
   enum Lin { Q, K, V, O, CQ, CK, CV, CO, KF, VF, FC1, FC2, kCount };

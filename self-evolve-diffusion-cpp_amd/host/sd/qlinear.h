@@ -96,6 +96,60 @@ QLinear qlinear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
 LinearPart linear_part_from_pack(const std::unordered_map<std::string, Tensor>& pack,
                                  const std::string& base, int64_t in, int64_t out);
 
+// Owning device array of floats (sdq_device_alloc), move-only.
+class DeviceFloats {
+ public:
+  DeviceFloats() = default;
+  explicit DeviceFloats(size_t n);
+  DeviceFloats(const DeviceFloats&) = delete;
+  DeviceFloats& operator=(const DeviceFloats&) = delete;
+  DeviceFloats(DeviceFloats&& o) noexcept : p_(o.p_) { o.p_ = nullptr; }
+  DeviceFloats& operator=(DeviceFloats&& o) noexcept;
+  ~DeviceFloats();
+  float* get() const { return p_; }
+  explicit operator bool() const { return p_ != nullptr; }
+
+ private:
+  float* p_ = nullptr;
+};
+
+// mlin (src/model/ovi_dit.cpp:66-84) for either weight dtype a pack holds:
+// I8 -> the int8 path (QLinear: qgemm + the bias pass), F32 / BF16 -> the
+// fp32 matmul of blk::linear (sdq_linear_f32: one fused multiply-add chain
+// per output in k order, then + bias, as sd::matmul computes it,
+// src/core/gemm.cpp:115-160). Both branches are bit-exact with the reference.
+class Linear {
+ public:
+  Linear() = default;
+  // An fp32 Linear from the torch [out, in] weight (transposed to [in, out]
+  // on upload, as lin() does, ovi_dit.cpp:409); bias [out] or nullptr. Host arrays.
+  Linear(const float* w_out_in, const float* bias, int64_t out, int64_t in);
+  explicit Linear(QLinear&& q);
+  Linear(Linear&&) noexcept = default;
+  Linear& operator=(Linear&&) noexcept = default;
+  bool is_int8() const { return !f32_; }
+  const QLinear& int8() const { return q_; }
+  int64_t in_features() const { return in_; }
+  int64_t out_features() const { return out_; }
+  // y = x W^T + b on host tensors (synchronous).
+  void mlin(const Tensor& x, Tensor& y) const;
+  // Device arrays x [M, in], y [M, out], stream-ordered.
+  void forward_device(const float* x, int64_t M, float* y, void* stream) const;
+
+ private:
+  QLinear q_;
+  DeviceFloats w_, b_;  // fp32 branch: [in, out] weight, bias (or empty)
+  int64_t in_ = 0, out_ = 0;
+  bool f32_ = false;
+};
+
+// OviDit::load_impl's lin() (ovi_dit.cpp:397-415) for either dtype:
+// "<base>.weight" [out, in] (I8 with its scale blob right after the int8
+// data, or F32 / BF16) and "<base>.bias" [out]; the reference's checks and
+// "ovi_dit: …" messages.
+Linear linear_from_pack(const std::unordered_map<std::string, Tensor>& pack,
+                        const std::string& base, int64_t in, int64_t out);
+
 // Throws std::runtime_error with sdq_last_error() when rc != SDQ_OK.
 void check(int rc, const char* what);
 

@@ -78,6 +78,7 @@ SIGNATURES = {
                                               _vp]),
     "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
     "sdq_add": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "sdq_linear_f32": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "sdq_sdpa": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
                                 ctypes.c_int, ctypes.c_int, _vp]),
     "sdq_sdpa_batched": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
@@ -470,6 +471,23 @@ def layernorm(x, y, w=None, b=None, eps=1e-6, stream=None):
     c.done()
     _check(_lib.sdq_layernorm(px, M, K, pw, pb, eps, py, _stream(stream)))
     return y
+
+
+def linear_f32(x, w, out, bias=None, stream=None):
+    """out = x . w (+ bias): the F32 branch of mlin (blk::linear -> sd::matmul,
+    src/core/gemm.cpp:115-160), bit-exact. x [M,K], w [K,N] (the [in, out]
+    layout lin() gives F32 weights), bias [N] or None, out [M,N]."""
+    c = _Args()
+    px = c(x, "x", "f32", (None, None))
+    M, K = x.shape
+    pw = c(w, "w", "f32", (K, None))
+    N = w.shape[1]
+    py = c(out, "out", "f32", (M, N))
+    pb = c(bias, "bias", "f32", (N,), optional=True)
+    load_library()
+    c.done()
+    _check(_lib.sdq_linear_f32(px, M, K, pw, N, pb, py, _stream(stream)))
+    return out
 
 
 def add_(x, y, stream=None):

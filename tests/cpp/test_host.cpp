@@ -124,6 +124,33 @@ int main(int argc, char** argv) {
       write_file(argv[11], y.data, y.nbytes);
       return 0;
     }
+    // mlin for either weight dtype (sd::gpu::linear_from_pack: I8 or F32)
+    if (cmd == "mlin_any" && argc == 9) {
+      gpu::check(sdq_init(0), "sdq_init");
+      std::shared_ptr<void> owner;
+      auto pack = load_sdcpp(argv[2], owner);
+      const int64_t in = std::atoll(argv[4]), out = std::atoll(argv[5]), M = std::atoll(argv[6]);
+      gpu::Linear lin = gpu::linear_from_pack(pack, argv[3], in, out);
+      std::printf("int8 %d\n", lin.is_int8() ? 1 : 0);
+      Tensor x = load_tensor(argv[7], {M, in}, DType::F32);
+      Tensor y;
+      lin.mlin(x, y);
+      write_file(argv[8], y.data, y.nbytes);
+      return 0;
+    }
+    if (cmd == "mlin_any_err" && argc == 6) {
+      std::shared_ptr<void> owner;
+      auto pack = load_sdcpp(argv[2], owner);
+      try {
+        gpu::Linear lin = gpu::linear_from_pack(pack, argv[3], std::atoll(argv[4]),
+                                                std::atoll(argv[5]));
+      } catch (const std::runtime_error& e) {
+        std::printf("%s\n", e.what());
+        return 0;
+      }
+      std::printf("no throw\n");
+      return 1;
+    }
     if (cmd == "linear_err" && argc == 6) {
       std::shared_ptr<void> owner;
       auto pack = load_sdcpp(argv[2], owner);

@@ -159,3 +159,13 @@ def test_block_step_argument_checks():
     io = dict(M=8, Mc=4, Mt=0, h_sa=x, att=x, gate_sa=torch.zeros(256), xq=x, ctx=ctx, xt=x,
               h_ffn=x, gate_ffn=torch.zeros(256), qkv=torch.zeros((8, 767)))
     _raises(r"qkv: shape \(8, 767\)", blk.forward, **io)
+
+
+def test_linear_f32_checks():
+    x, w, y = torch.zeros((4, 32)), torch.zeros((32, 20)), torch.zeros((4, 20))
+    _raises("x: must be on the GPU", sdq.linear_f32, x, w, y)
+    _raises(r"w: shape \(31, 20\)", sdq.linear_f32, x, torch.zeros((31, 20)), y)
+    _raises(r"out: shape \(4, 19\)", sdq.linear_f32, x, w, torch.zeros((4, 19)))
+    _raises(r"bias: shape \(19,\)", sdq.linear_f32, x, w, y, bias=torch.zeros(19))
+    _raises("x: dtype", sdq.linear_f32, x.double(), w, y)
+    _raises("w: must be contiguous", sdq.linear_f32, x, torch.zeros((20, 32)).t(), y)

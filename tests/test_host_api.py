@@ -139,7 +139,47 @@ def test_linear_from_pack_checks(tmp_path, oracle):
     assert r.returncode == 0 and "not an int8" in r.stdout
 
 
+def test_linear_any_from_pack_checks(tmp_path, oracle):
+    """lin()'s checks for either dtype (ovi_dit.cpp:397-415): shapes, a
+    missing bias; no GPU call is made before they pass."""
+    p = str(tmp_path / "h.sdcpp")
+    oracle.write_sdcpp(p, {"head.weight": np.zeros((20, 300), np.float32),
+                           "head.bias": np.zeros(20, np.float32),
+                           "nob.weight": np.zeros((4, 8), np.float32)})
+    r = run("mlin_any_err", p, "head", 300, 21, check=False)
+    assert r.returncode == 0 and "bad shape for head.weight" in r.stdout
+    r = run("mlin_any_err", p, "nob", 8, 4, check=False)
+    assert r.returncode == 0 and "missing tensor nob.bias" in r.stdout
+
+
 # ------------------------------------------------------------------ GPU
+@pytest.mark.gpu
+def test_linear_any_from_pack_both_dtypes(tmp_path, sdq_dev, oracle):
+    """mlin's dispatch (ovi_dit.cpp:66-84) through sd::gpu::linear_from_pack:
+    an F32 pack entry (the audio head's [20, 3072] shape: fewer than 65536
+    values, so the packer keeps it fp32) runs the fp32 matmul, an I8 one the
+    int8 path; each bit-exact with the reference's branch."""
+    p = str(tmp_path / "m.sdcpp")
+    W = (oracle.randn(20 * 3072, 11) * np.float32(0.02)).reshape(20, 3072)
+    b = oracle.randn(20, 12)
+    W8 = (oracle.randn(160 * 512, 13) * np.float32(0.02)).reshape(160, 512)  # >= 65536: int8
+    b8 = oracle.randn(160, 14)
+    written = oracle.write_sdcpp(p, {"head.weight": W, "head.bias": b,
+                                     "proj.weight": W8, "proj.bias": b8})
+    M = 157
+    x = oracle.randn(M * 3072, 15).reshape(M, 3072)
+    x.tofile(tmp_path / "x.bin")
+    r = run("mlin_any", p, "head", 3072, 20, M, tmp_path / "x.bin", tmp_path / "o.bin")
+    assert "int8 0" in r.stdout
+    got = np.fromfile(tmp_path / "o.bin", np.float32).reshape(M, 20)
+    assert_bitexact(got, oracle.linear_f32(x, np.ascontiguousarray(W.T), b), "F32 head")
+    x8 = oracle.randn(M * 512, 16).reshape(M, 512)
+    x8.tofile(tmp_path / "x8.bin")
+    r = run("mlin_any", p, "proj", 512, 160, M, tmp_path / "x8.bin", tmp_path / "o8.bin")
+    assert "int8 1" in r.stdout
+    _, q, s = written["proj.weight"]
+    got = np.fromfile(tmp_path / "o8.bin", np.float32).reshape(M, 160)
+    assert_bitexact(got, oracle.linear(x8, q, s, bias=b8), "I8 proj")
 @pytest.mark.gpu
 def test_sd_qgemm_host_tensor_api(tmp_path, sdq_dev, oracle):
     M, K, N = 77, 1000, 300
