@@ -155,6 +155,28 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale);
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
                 void* Y, void* stream);
 
+/* Several independent Linears at once: the same results, bit for bit, as one
+ * sdq_qlinear per item, with fewer and fuller launches. Items that share K,
+ * epilogue kind, bias / gate presence and run on the 128x128 tile path (the
+ * medium and small row counts of the DiT's Linears) are quantized by one
+ * launch and multiplied by one persistent launch that walks all their tiles;
+ * other items run as separate sdq_qlinear calls. For the Linears of a block
+ * (or of both branches of a twin layer) that read inputs already computed:
+ * q|k|v, cross q, the text k|v, the fusion k|v (ovi_dit.cpp:179-181,
+ * 194-196, 235-237, 244-245), or the output projections of two branches.
+ * Items must not overlap: no item's Y may be another item's A, resid or Y.
+ * n <= SDQ_MAX_GROUP; M == 0 items are skipped. Stream-ordered.
+ * Replaces: a sequence of independent mlin calls (ovi_dit.cpp:66-84). */
+typedef struct sdq_group_item {
+  const sdq_weight* w;
+  const float* A;    /* [M, K] device, K = the weight's K */
+  int64_t M;
+  sdq_epilogue epi;  /* as for sdq_qlinear (resid: this item's own) */
+  void* Y;           /* [M, N] device */
+} sdq_group_item;
+#define SDQ_MAX_GROUP 16
+int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream);
+
 /* sdq_qlinear for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference. The same results as sdq_qlinear, bit for

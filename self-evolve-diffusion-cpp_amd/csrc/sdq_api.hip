@@ -21,10 +21,10 @@
 #include <mutex>
 #include <new>
 #include <set>
-#include <vector>
 #include <string>
 #include <thread>
 #include <utility>
+#include <vector>
 
 #include "sdq_internal.h"
 
@@ -78,6 +78,8 @@ struct Workspace {
   size_t st_bytes = 0;
   float* rinv = nullptr;  // rmsnorm 1/rms per row
   size_t rinv_bytes = 0;
+  char* grp = nullptr;  // sdq_qlinear_group's per-item scratch
+  size_t grp_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -703,6 +705,39 @@ bool read_spans(int fd, const std::vector<ReadSpan>& spans, int threads) {
 
 }  // namespace
 
+namespace {
+
+// Whether item `it` takes sdq_qlinear_group's shared launches: the plain
+// quantizer's single-kernel form and the 128x128 persistent GEMM without
+// split-K, the path sdq_qlinear itself would take for it.
+bool groupable(const sdq_group_item& it, int cu_count) {
+  const sdq_weight* w = it.w;
+  const int kind = it.epi.kind;
+  if (kind != SDQ_EPI_NONE && kind != SDQ_EPI_GELU && kind != SDQ_EPI_GATED &&
+      kind != SDQ_EPI_RESID)
+    return false;
+  if (w->K == 0 || it.M > (int64_t(1) << 30)) return false;
+  const int64_t N = w->N;
+  if (choose_gemm_cfg(it.M, N, w->KFp, kind, cu_count) != kCfg128x128) return false;
+  if (choose_splitk(kCfg128x128, it.M, N, w->KFp, cu_count) != 1) return false;
+  const int64_t Mp = round_up(it.M, gemm_cfg_bm(kCfg128x128));
+  if (act_quant_pmax_floats(Mp, w->KFp, cu_count) != 0) return false;
+  if (N % 4 != 0 || !aligned16(it.Y)) return false;
+  if (it.epi.bias && !aligned16(it.epi.bias)) return false;
+  if (it.epi.gate && !aligned16(it.epi.gate)) return false;
+  if (it.epi.resid && !aligned16(it.epi.resid)) return false;
+  return w->KFp * 1024 * 8 <= 0x7FFFFFFF && N * 4 * 256 <= 0x7FFFFFF0;
+}
+
+// Items that may share one GEMM launch: same k-fragments and epilogue form.
+bool same_group(const sdq_group_item& a, const sdq_group_item& b) {
+  return a.w->KFp == b.w->KFp && a.epi.kind == b.epi.kind &&
+         (a.epi.bias != nullptr) == (b.epi.bias != nullptr) &&
+         (a.epi.gate != nullptr) == (b.epi.gate != nullptr) && a.epi.gate_fma == b.epi.gate_fma;
+}
+
+}  // namespace
+
 extern "C" {
 
 int sdq_weight_upload_batch(const sdq_weight_src* src, int n, void* stream, sdq_weight** out) {
@@ -877,6 +912,140 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale) {
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
                 void* Y, void* stream) {
   return qlinear_device(w, A, M, K, epi, Y, static_cast<hipStream_t>(stream));
+}
+
+
+int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
+  if (n < 0 || n > SDQ_MAX_GROUP) return set_error(SDQ_ERR_INVALID, "group: n must be 0..16");
+  if (n > 0 && !items) return set_error(SDQ_ERR_INVALID, "group: null items");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  // the checks sdq_qlinear makes, for every item before anything runs
+  for (int i = 0; i < n; i++) {
+    const sdq_group_item& it = items[i];
+    if (!it.w) return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": null weight");
+    if ((rc = check_weight(it.w, it.w->K))) return rc;
+    if ((rc = validate_epi(&it.epi))) return rc;
+    if (it.M < 0) return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": negative M");
+    if (it.M > 0 && it.w->N > 0 && ((!it.A && it.w->K > 0) || !it.Y))
+      return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": null A or Y");
+  }
+  if ((rc = ensure_device(dev))) return rc;
+  const int cu_count = g_dev[dev].cu_count;
+  // items of the shared launches, and the rest
+  std::vector<int> shared, single;
+  for (int i = 0; i < n; i++) {
+    if (items[i].M == 0 || items[i].w->N == 0) continue;
+    (groupable(items[i], cu_count) ? shared : single).push_back(i);
+  }
+  // a lone groupable item gains nothing from the shared launches
+  if (shared.size() == 1) {
+    single.push_back(shared[0]);
+    shared.clear();
+  }
+  if (!shared.empty()) {
+    // scratch: per item its quantized rows, row scales and padded column copies
+    struct Carve {
+      size_t at, as, cols;
+    };
+    std::vector<Carve> cv(shared.size());
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      const size_t o = off;
+      off += (size_t)round_up((int64_t)bytes, 256);
+      return o;
+    };
+    const size_t sink_off = take(4096);
+    for (size_t j = 0; j < shared.size(); j++) {
+      const sdq_group_item& it = items[shared[j]];
+      const int64_t Mp = round_up(it.M, gemm_cfg_bm(kCfg128x128));
+      cv[j].at = take((size_t)(Mp / kFragRows) * (size_t)it.w->KFp * kFragBytes);
+      cv[j].as = take((size_t)Mp * sizeof(float));
+      cv[j].cols = take((size_t)(it.w->Np + kColPad) * 2 * sizeof(float));
+    }
+    char* base = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      Workspace& ws = g_ws[{dev, s}];
+      if ((rc = grow(s, reinterpret_cast<void**>(&ws.grp), &ws.grp_bytes, off))) return rc;
+      base = ws.grp;
+    }
+    QuantSegs qs{};
+    qs.count = (int)shared.size();
+    int64_t units = 0;
+    for (size_t j = 0; j < shared.size(); j++) {
+      const sdq_group_item& it = items[shared[j]];
+      const int64_t Mp = round_up(it.M, gemm_cfg_bm(kCfg128x128));
+      const int64_t cap = it.w->Np + kColPad;
+      QuantSeg& q = qs.s[j];
+      q.A = it.A;
+      q.M = it.M;
+      q.K = it.w->K;
+      q.KFp = it.w->KFp;
+      q.vec = (aligned16(it.A) && it.w->K % 4 == 0) ? 1 : 0;
+      q.at = reinterpret_cast<int8_t*>(base + cv[j].at);
+      q.as = reinterpret_cast<float*>(base + cv[j].as);
+      float* cols = reinterpret_cast<float*>(base + cv[j].cols);
+      q.cc.bias = it.epi.bias;
+      q.cc.gate = it.epi.gate;
+      q.cc.bias_pad = it.epi.bias ? cols : nullptr;
+      q.cc.gate_pad = it.epi.gate ? cols + cap : nullptr;
+      q.cc.N = it.w->N;
+      q.cc.CP = cap;
+      q.unit0 = units;
+      units += Mp / 8;
+    }
+    qs.total = units;
+    hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
+    hipError_t e = launch_act_quant_segs(qs, s);
+    if (e != hipSuccess) return hip_error(e, "group act_quant launch");
+    hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
+    // one GEMM launch per set of items with the same K and epilogue form
+    std::vector<bool> done(shared.size(), false);
+    for (size_t j = 0; j < shared.size(); j++) {
+      if (done[j]) continue;
+      GemmGroup g{};
+      const sdq_group_item& first = items[shared[j]];
+      for (size_t k = j; k < shared.size(); k++) {
+        const sdq_group_item& it = items[shared[k]];
+        if (done[k] || !same_group(first, it)) continue;
+        done[k] = true;
+        GemmProblem& p = g.p[g.count++];
+        p.wt = it.w->frags;
+        p.scale = it.w->scale;
+        p.bias = qs.s[k].cc.bias_pad;
+        p.gate = qs.s[k].cc.gate_pad;
+        p.at = qs.s[k].at;
+        p.as = qs.s[k].as;
+        p.resid = it.epi.resid;
+        p.Y = it.Y;
+        p.M = (int)it.M;
+        p.N = (int)it.w->N;
+      }
+      EpiArgs ea = make_epi(&first.epi, first.w->K);
+      ea.bias = ea.gate = ea.resid = nullptr;  // per problem, from the table
+      e = launch_qgemm_group(g, first.w->KFp, ea, reinterpret_cast<float*>(base + sink_off),
+                             cu_count, s);
+      if (e != hipSuccess) return hip_error(e, "group qgemm launch");
+    }
+    if (t_prof) {
+      hipEvent_t p2 = prof_mark(s);
+      if (p0 && p1 && p2) {
+        t_recs.push_back({"act_quant_group", p0, p1});
+        t_recs.push_back({"qgemm_group", p1, p2});
+      } else {
+        for (hipEvent_t ev : {p0, p1, p2})
+          if (ev) (void)hipEventDestroy(ev);
+      }
+    }
+  }
+  for (int i : single) {
+    const sdq_group_item& it = items[i];
+    if ((rc = qlinear_device(it.w, it.A, it.M, it.w->K, &it.epi, it.Y, s))) return rc;
+  }
+  return SDQ_OK;
 }
 
 int sdq_ffn(const sdq_weight* fc1, const float* b1, const sdq_weight* fc2, const float* b2,

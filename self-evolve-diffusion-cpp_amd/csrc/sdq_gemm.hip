@@ -394,13 +394,32 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // SPLITK: the work items are (tile, k-range) pairs, `splits` contiguous
 // k-ranges per tile, each writing raw int32 sums to its own [M,N] slice of
 // Y (EPI_ACC); splitk_reduce adds the slices and applies the epilogue.
+// The grouped launches' problem table (GROUPED), or nothing.
+struct NoGroup {};
+template <bool GROUPED>
+using GroupArg = typename std::conditional<GROUPED, GemmGroup, NoGroup>::type;
+// Field reads that compile for both argument types (only called when GROUPED).
+__device__ __forceinline__ int group_total(const GemmGroup& g) { return g.total; }
+__device__ __forceinline__ int group_total(const NoGroup&) { return 0; }
+__device__ __forceinline__ int64_t group_m(const GemmGroup& g, int p) { return g.p[p].M; }
+__device__ __forceinline__ int64_t group_m(const NoGroup&, int) { return 0; }
+__device__ __forceinline__ int64_t group_n(const GemmGroup& g, int p) { return g.p[p].N; }
+__device__ __forceinline__ int64_t group_n(const NoGroup&, int) { return 0; }
+__device__ __forceinline__ void* group_y(const GemmGroup& g, int p) { return g.p[p].Y; }
+__device__ __forceinline__ void* group_y(const NoGroup&, int) { return nullptr; }
+__device__ __forceinline__ const float* group_resid(const GemmGroup& g, int p) {
+  return g.p[p].resid;
+}
+__device__ __forceinline__ const float* group_resid(const NoGroup&, int) { return nullptr; }
+
 template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI, bool BIAS,
-          bool SPLITK>
+          bool SPLITK, bool GROUPED = false>
 __global__ void __launch_bounds__(WN* WM * 64, OCC)
 qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restrict__ at,
               const float* __restrict__ as, int64_t M, int64_t N, int64_t KFp, int tiles_n,
-              int tiles_m, EpiArgs epi, void* Y, int splits) {
+              int tiles_m, EpiArgs epi, void* Y, int splits, GroupArg<GROUPED> grp) {
   static_assert(!SPLITK || EPI == SDQ_EPI_ACC, "split-K partials are raw accumulators");
+  static_assert(!(GROUPED && SPLITK), "grouped launches do not split K");
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -414,8 +433,9 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
   static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
-  // GELU's epilogue spills SGPRs; their reloads can sit next to a DMA
-  constexpr int kDmaNop = EPI == SDQ_EPI_GELU ? 4 : 0;
+  // GELU's epilogue spills SGPRs, and the grouped kernels read their
+  // problem table into spilled SGPRs; the reloads can sit next to a DMA
+  constexpr int kDmaNop = (EPI == SDQ_EPI_GELU || GROUPED) ? 4 : 0;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
@@ -431,7 +451,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int wn = w % WN, wm = w / WN;
   const uint32_t lane_off = (uint32_t)lane * 16u;
 
-  const int T = tiles_n * tiles_m;
+  const int T = GROUPED ? group_total(grp) : tiles_n * tiles_m;
   const int S = SPLITK ? splits : 1;
   const int TS = T * S;  // work items
   const int G = gridDim.x;
@@ -439,10 +459,11 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int klen = (int)(KFp / S);  // k-fragments per work item
   const int nks = klen / KS;
 
-  // Work item i of this workgroup -> (tm, tn, k-range ks): XCD-aware
-  // grouped order applied to the virtual block id blockIdx.x + i*G (G is a
-  // multiple of 8, so it stays on this XCD).
-  auto coords = [&](int i, int& tm, int& tn, int& ks) {
+  // Work item i of this workgroup -> (tm, tn, k-range ks) of problem pb:
+  // XCD-aware grouped order applied to the virtual block id blockIdx.x + i*G
+  // (G is a multiple of 8, so it stays on this XCD); a grouped launch first
+  // finds the problem whose tiles hold the item.
+  auto coords = [&](int i, int& tm, int& tn, int& ks, int& pb) {
     const int bid = (int)blockIdx.x + i * G;
     const int xcd = bid & 7, jx = bid >> 3, q8 = TS >> 3, r8 = TS & 7;
     int lin = xcd * q8 + (xcd < r8 ? xcd : r8) + jx;
@@ -452,13 +473,30 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       lin -= ks * T;
     }
     constexpr int GROUP_M = SDQ_PERSIST_GROUP_M;
-    const int per_group = GROUP_M * tiles_n;
-    const int g = lin / per_group;
-    const int first_m = g * GROUP_M;
-    const int gsz = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
-    const int rem = lin - g * per_group;
-    tm = first_m + rem % gsz;
-    tn = rem / gsz;
+    pb = 0;
+    if constexpr (GROUPED) {
+#pragma unroll
+      for (int q = 1; q < kMaxGemmGroup; q++)
+        if (q < grp.count && lin >= grp.p[q].tile0) pb = q;
+      pb = __builtin_amdgcn_readfirstlane(pb);  // uniform: the table reads stay scalar
+      lin -= grp.p[pb].tile0;
+      const int ptn = grp.p[pb].tiles_n, ptm = grp.p[pb].tiles_m;
+      const int per_group = GROUP_M * ptn;
+      const int g = lin / per_group;
+      const int first_m = g * GROUP_M;
+      const int gsz = (ptm - first_m) < GROUP_M ? (ptm - first_m) : GROUP_M;
+      const int rem = lin - g * per_group;
+      tm = first_m + rem % gsz;
+      tn = rem / gsz;
+    } else {
+      const int per_group = GROUP_M * tiles_n;
+      const int g = lin / per_group;
+      const int first_m = g * GROUP_M;
+      const int gsz = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+      const int rem = lin - g * per_group;
+      tm = first_m + rem % gsz;
+      tn = rem / gsz;
+    }
   };
 
   // ---- issue cursor: the next stage to load (segment cj, stage cks), with
@@ -471,14 +509,19 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   const int wso0 = ((w / KS) * (int)KFp + (w % KS)) * 1024;
   const int tso = (NW / KS) * (int)KFp * 1024;
   const uint32_t lds0 = lds_addr32(lds) + (uint32_t)w * 1024u;
-  int cj = 0, cks = 0, ctm = 0, ctn = 0, cgs = 0, csp = 0;
+  int cj = 0, cks = 0, ctm = 0, ctn = 0, cgs = 0, csp = 0, cpb = 0;
   int wso = wso0;
   bool col_due = true;  // the segment's first stage was issued; its column loads follow
   v4u wr, ar;
   auto set_tile = [&](int i) {
-    coords(i, ctm, ctn, csp);
-    wr = raw_rsrc(wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
-    ar = raw_rsrc(at + (int64_t)ctm * apanel, (uint32_t)apanel);
+    coords(i, ctm, ctn, csp, cpb);
+    if constexpr (GROUPED) {
+      wr = raw_rsrc(grp.p[cpb].wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
+      ar = raw_rsrc(grp.p[cpb].at + (int64_t)ctm * apanel, (uint32_t)apanel);
+    } else {
+      wr = raw_rsrc(wt + (int64_t)ctn * wpanel, (uint32_t)wpanel);
+      ar = raw_rsrc(at + (int64_t)ctm * apanel, (uint32_t)apanel);
+    }
     wso = wso0 + csp * klen * 1024;  // the work item's first k-fragment
   };
   set_tile(0);
@@ -502,11 +545,21 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     if (col_due) {
       col_due = false;
       const int par = cj & 1;
-      if (w < 3) {
-        const float* src = w == 0 ? cols.scale : (w == 1 ? cols.bias : cols.gate);
-        if (src) dma_row(src, (int64_t)ctn * BN, BN, &colb[par][w][0]);
-      } else if (w == 3) {
-        dma_row(as, (int64_t)ctm * BM, BM, &rowb[par][0]);
+      if constexpr (GROUPED) {
+        const GemmProblem& q = grp.p[cpb];
+        if (w < 3) {
+          const float* src = w == 0 ? q.scale : (w == 1 ? q.bias : q.gate);
+          if (src) dma_row(src, (int64_t)ctn * BN, BN, &colb[par][w][0]);
+        } else if (w == 3) {
+          dma_row(q.as, (int64_t)ctm * BM, BM, &rowb[par][0]);
+        }
+      } else {
+        if (w < 3) {
+          const float* src = w == 0 ? cols.scale : (w == 1 ? cols.bias : cols.gate);
+          if (src) dma_row(src, (int64_t)ctn * BN, BN, &colb[par][w][0]);
+        } else if (w == 3) {
+          dma_row(as, (int64_t)ctm * BM, BM, &rowb[par][0]);
+        }
       }
     }
     cgs++;
@@ -647,24 +700,29 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     }
     constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
     // ---- epilogue of tile j
-    int tm, tn, ksp;
-    coords(j, tm, tn, ksp);
+    int tm, tn, ksp, pb;
+    coords(j, tm, tn, ksp, pb);
     const int par = j & 1;
-    const int64_t ybase = (((int64_t)ksp * M + (int64_t)tm * BM) * N + (int64_t)tn * BN) * 4;
+    const int64_t Mq = GROUPED ? group_m(grp, pb) : M;
+    const int64_t Nq = GROUPED ? group_n(grp, pb) : N;
+    void* const Yq = GROUPED ? group_y(grp, pb) : Y;
+    const float* const rq = GROUPED ? group_resid(grp, pb) : epi.resid;
+    const int64_t ybase = (((int64_t)ksp * Mq + (int64_t)tm * BM) * Nq + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<char*>(Y) + ybase, (short)0, kBigRange, kRsrcWord3);
+        static_cast<char*>(Yq) + ybase, (short)0, kBigRange, kRsrcWord3);
     const bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        has_x ? const_cast<float*>(epi.resid) + (ybase >> 2) : static_cast<float*>(Y), (short)0,
+        has_x ? const_cast<float*>(rq) + (ybase >> 2) : static_cast<float*>(Yq), (short)0,
         has_x ? kBigRange : 0, kRsrcWord3);
     // 32-bit row / column checks: M <= 2^30, and N fits the 32-bit offsets
     const int mrow0 = tm * BM + wrow + rr;
     const int ncol0 = tn * BN + wcol + 4 * rc;
-    const int M32 = (int)M, N32 = (int)N;
+    const int M32 = (int)Mq, N32 = (int)Nq;
     // Opaque copy of the lane's offset: keeps the compiler from hoisting the
     // per-row output offsets out of the tile loop (they would stay live
     // across the main loop and spill).
-    int vlane = voff_lane;
+    const int ldyq = GROUPED ? N32 * 4 : ldy4;
+    int vlane = GROUPED ? (wrow + rr) * ldyq + (wcol + 4 * rc) * 4 : voff_lane;
     asm volatile("" : "+v"(vlane));
     // GELU: running max |Y| of the lane's rows over its columns (for the
     // next GEMM's activation quantizer); NaN never wins, as in the
@@ -698,7 +756,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
           const bool ok = n_ok && (mrow0 + rl < M32);
           // All offsets in the VGPR, soffset 0: the compiler then inserts
           // the wait states a wide store's data VGPRs need before reuse.
-          const int voff = ok ? vlane + rl * ldy4 + a * 128 : kOutOfRange;
+          const int voff = ok ? vlane + rl * ldyq + a * 128 : kOutOfRange;
           if constexpr (EPI == SDQ_EPI_ACC) {
             __builtin_amdgcn_raw_buffer_store_b128(t4[i], yr, voff, 0, kStreamStore);
           } else {
@@ -1025,13 +1083,13 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
     if (epi.kind != SDQ_EPI_ACC) return hipErrorInvalidValue;
     hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, SDQ_EPI_ACC, false, true>),
                        dim3((unsigned)G), dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp,
-                       tiles_n, tiles_m, epi, Y, splits);
+                       tiles_n, tiles_m, epi, Y, splits, NoGroup{});
     return hipGetLastError();
   }
 #define SDQ_LAUNCH_PERSIST(K, B)                                                                  \
   hipLaunchKernelGGL((qgemm_persist<BN, BM, WN, WM, KS, STAGES, OCC, K, B, false>),              \
                      dim3((unsigned)G), dim3(WN * WM * 64), 0, s, wt, cols, at, as, M, N, KFp,  \
-                     tiles_n, tiles_m, epi, Y, 1)
+                     tiles_n, tiles_m, epi, Y, 1, NoGroup{})
 #define SDQ_LAUNCH_PERSIST_B(K)    \
   if (epi.bias)                    \
     SDQ_LAUNCH_PERSIST(K, true);   \
@@ -1047,6 +1105,55 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   }
 #undef SDQ_LAUNCH_PERSIST_B
 #undef SDQ_LAUNCH_PERSIST
+  return hipGetLastError();
+}
+
+// One launch of the 128x128 persistent kernel over the tiles of several
+// problems (GemmGroup): the same per-tile work as separate launches, without
+// the partly empty rounds and launch gaps of many small ones.
+hipError_t run_persist_group(GemmGroup& g, int64_t KFp, const EpiArgs& epi, float* sink,
+                             int cu_count, hipStream_t s) {
+  constexpr int BN = 128, BM = 128, KS = 2, STAGES = 4;
+  if (g.count < 1 || g.count > kMaxGemmGroup || KFp % KS != 0 || KFp / KS < STAGES ||
+      epi.kzero || epi.rmax || !sink)
+    return hipErrorInvalidValue;
+  int64_t total = 0;
+  const bool bias = g.p[0].bias != nullptr;
+  for (int i = 0; i < g.count; i++) {
+    GemmProblem& p = g.p[i];
+    if (p.M <= 0 || p.N <= 0 || !p.wt || !p.scale || !p.at || !p.as || !p.Y ||
+        (p.bias != nullptr) != bias)
+      return hipErrorInvalidValue;
+    p.tiles_n = (int)ceil_div(p.N, BN);
+    p.tiles_m = (int)ceil_div(p.M, BM);
+    p.tile0 = (int)total;
+    total += (int64_t)p.tiles_n * p.tiles_m;
+  }
+  if (total > 0x7FFFFFFF / 2) return hipErrorInvalidValue;
+  g.total = (int)total;
+  const int64_t max_groups = 2 * (int64_t)(cu_count > 0 ? cu_count : 256);
+  int G = (int)(total < max_groups ? total : max_groups);
+  if (G >= 8) G &= ~7;
+  const ColOps cols{g.p[0].scale, g.p[0].bias, g.p[0].gate};
+#define SDQ_LAUNCH_GROUP(K, B)                                                                    \
+  hipLaunchKernelGGL((qgemm_persist<BN, BM, 2, 2, KS, STAGES, 2, K, B, false, true>),            \
+                     dim3((unsigned)G), dim3(256), 0, s, g.p[0].wt, cols, g.p[0].at, g.p[0].as,   \
+                     (int64_t)g.p[0].M, (int64_t)g.p[0].N, KFp, g.p[0].tiles_n,                  \
+                     g.p[0].tiles_m, epi, static_cast<void*>(sink), 1, g)
+#define SDQ_LAUNCH_GROUP_B(K)   \
+  if (bias)                     \
+    SDQ_LAUNCH_GROUP(K, true);  \
+  else                          \
+    SDQ_LAUNCH_GROUP(K, false)
+  switch (epi.kind) {
+    case SDQ_EPI_NONE: SDQ_LAUNCH_GROUP_B(SDQ_EPI_NONE); break;
+    case SDQ_EPI_GELU: SDQ_LAUNCH_GROUP_B(SDQ_EPI_GELU); break;
+    case SDQ_EPI_GATED: SDQ_LAUNCH_GROUP_B(SDQ_EPI_GATED); break;
+    case SDQ_EPI_RESID: SDQ_LAUNCH_GROUP_B(SDQ_EPI_RESID); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef SDQ_LAUNCH_GROUP_B
+#undef SDQ_LAUNCH_GROUP
   return hipGetLastError();
 }
 
@@ -1217,6 +1324,11 @@ int gemm_rmax_chunks(int cfg, int64_t N) {
   if (cfg == kCfg128x128) return (int)ceil_div(N, 128) * 2;
   if (cfg == kCfg256x256) return (int)ceil_div(N, 256) * 2;
   return 0;
+}
+
+hipError_t launch_qgemm_group(GemmGroup& g, int64_t KFp, const EpiArgs& epi, float* sink,
+                              int cu_count, hipStream_t s) {
+  return run_persist_group(g, KFp, epi, sink, cu_count, s);
 }
 
 int64_t tail_split_rows(int64_t M, int64_t N, int cu_count) {

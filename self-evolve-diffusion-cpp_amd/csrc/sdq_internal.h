@@ -79,6 +79,25 @@ int64_t act_quant_pmax_floats(int64_t Mp, int64_t KFp, int cu_count);
 hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t Mp, int64_t KFp,
                                   int8_t* at, float* as, const ColCopy& cc, float* pmax,
                                   int cu_count, hipStream_t s);
+// Several plain fragment-layout quantizations in one launch (single-kernel
+// form only: act_quant_pmax_floats(Mp, KFp) == 0 for every segment). Segment
+// i takes units (Mp / 8 workgroups) [unit0, next unit0 or total).
+constexpr int kMaxQuantSegs = 16;
+struct QuantSeg {
+  const float* A;
+  int64_t M, K, KFp;
+  int vec;  // A 16-byte aligned and K % 4 == 0
+  int8_t* at;
+  float* as;
+  ColCopy cc;
+  int64_t unit0;
+};
+struct QuantSegs {
+  QuantSeg s[kMaxQuantSegs];
+  int count;
+  int64_t total;
+};
+hipError_t launch_act_quant_segs(const QuantSegs& segs, hipStream_t s);
 // mod_rows(layernorm(A)) as the quantized rows (the DiT's norm + modulation
 // before q|k|v and the FFN, blocks.cpp:18-43 + ovi_dit.cpp:161-172): per-row
 // (mean, 1/std) into st[M] (bit-exact serial sums), then the quantizer on the
@@ -194,6 +213,34 @@ struct GemmAux {
                      // second, 128x128 launch (two kernels ran), else 0
   hipEvent_t mid;    // nullable: recorded between those two launches (per-kernel timing)
 };
+// Grouped persistent GEMM: up to kMaxGemmGroup independent problems with
+// the same K (KFp), epilogue kind and bias presence in one launch of the
+// 128x128 persistent kernel, their tiles walked as one list (problem p owns
+// tiles [tile0, tile0 + tiles_n * tiles_m)). Each problem has its own
+// weight, quantized activations (at / as, rows padded to 128), padded column
+// operands (scale, bias, gate: as GemmAux / ColOps), residual and output.
+constexpr int kMaxGemmGroup = 16;
+struct GemmProblem {
+  const int8_t* wt;
+  const float* scale;
+  const float* bias;
+  const float* gate;
+  const int8_t* at;
+  const float* as;
+  const float* resid;
+  void* Y;
+  int M, N, tiles_n, tiles_m, tile0;
+};
+struct GemmGroup {
+  GemmProblem p[kMaxGemmGroup];
+  int count;
+  int total;  // tiles of all problems
+};
+// epi: kind, gate_fma (per-problem pointers come from the group; no row
+// maxima). sink: >= 1 KB scratch (as GemmAux::sink).
+hipError_t launch_qgemm_group(GemmGroup& g, int64_t KFp, const EpiArgs& epi, float* sink,
+                              int cu_count, hipStream_t s);
+
 // Column chunks of the row maxima a GELU launch of this config writes.
 int gemm_rmax_chunks(int cfg, int64_t N);
 

@@ -255,22 +255,18 @@ act_quant_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KL, 
 // blocks.cpp:18-43): value v of row r, column k becomes
 //   fmaf(fl(fl(v - mu_r) * inv_r) + 0, 1 + scale[k], shift[k])
 // with (mu_r, inv_r) from ln_stats_kernel; padding columns stay 0.
+// One R-row unit (`unit`) of a quantizer launch.
 template <int R, int NW, int CACHE, bool PRE, bool XF>
-__global__ void __launch_bounds__(NW * 64)
-act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
-                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc,
-                       const float* __restrict__ pre, int pc, int pstride, LnModArgs lm) {
+__device__ __forceinline__ void
+act_quant_unit(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
+               int8_t* __restrict__ out, float* __restrict__ as,
+               const float* __restrict__ pre, int pc, int pstride, LnModArgs lm,
+               const int64_t unit) {
   static_assert(R == 8 || R == 16, "unit height");
   static_assert(!(PRE && XF), "given maxima are for the plain rows");
   constexpr int F = 32 / R;  // fragments per lane group
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    if (cc.bias_pad) cc.bias_pad[i] = i < cc.N ? cc.bias[i] : 0.f;
-    if (cc.gate_pad) cc.gate_pad[i] = i < cc.N ? cc.gate[i] : 0.f;
-  }
   const int w = threadIdx.x >> 6;
   const int l = threadIdx.x & 63;
-  const int64_t unit = blockIdx.x;
   const int64_t row = unit * R + (l % R);
   const bool row_ok = row < M;
   const float* rowp = A + (row_ok ? row : 0) * K;
@@ -344,6 +340,42 @@ act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_
     fetch(g, t);
     emit(g, t);
   }
+}
+
+template <int R, int NW, int CACHE, bool PRE, bool XF>
+__global__ void __launch_bounds__(NW * 64)
+act_quant_units_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t KFp, int vec,
+                       int8_t* __restrict__ out, float* __restrict__ as, ColCopy cc,
+                       const float* __restrict__ pre, int pc, int pstride, LnModArgs lm) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cc.CP;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (cc.bias_pad) cc.bias_pad[i] = i < cc.N ? cc.bias[i] : 0.f;
+    if (cc.gate_pad) cc.gate_pad[i] = i < cc.N ? cc.gate[i] : 0.f;
+  }
+  act_quant_unit<R, NW, CACHE, PRE, XF>(A, M, K, KFp, vec, out, as, pre, pc, pstride, lm,
+                                        blockIdx.x);
+}
+
+// Several independent quantizations in one launch (the inputs of Linears
+// that do not depend on each other): workgroup b quantizes unit
+// b - segs.s[i].unit0 of the segment i whose units it falls in.
+__global__ void __launch_bounds__(kQuantUnitWaves * 64)
+act_quant_segs_kernel(QuantSegs segs) {
+  const int64_t b = blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxQuantSegs; q++)
+    if (q < segs.count && b >= segs.s[q].unit0) i = q;
+  const QuantSeg& g = segs.s[i];
+  const int64_t unit = b - g.unit0;
+  const int64_t units = (i + 1 < segs.count ? segs.s[i + 1].unit0 : segs.total) - g.unit0;
+  const ColCopy& cc = g.cc;
+  for (int64_t c = unit * blockDim.x + threadIdx.x; c < cc.CP; c += units * blockDim.x) {
+    if (cc.bias_pad) cc.bias_pad[c] = c < cc.N ? cc.bias[c] : 0.f;
+    if (cc.gate_pad) cc.gate_pad[c] = c < cc.N ? cc.gate[c] : 0.f;
+  }
+  act_quant_unit<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false, false>(
+      g.A, g.M, g.K, g.KFp, g.vec, g.at, g.as, nullptr, 0, 0, LnModArgs{}, unit);
 }
 
 // Split form of the fragment-layout quantizer for few rows, where one
@@ -484,6 +516,15 @@ hipError_t launch_act_quant_frags(const float* A, int64_t M, int64_t K, int64_t 
   hipLaunchKernelGGL((act_quant_units_kernel<kQuantRows, kQuantUnitWaves, kQuantUnitCache, false, false>),
                      dim3((unsigned)units), dim3(kQuantUnitWaves * 64), 0, s, A, M, K, KFp, vec,
                      at, as, cc, nullptr, 0, 0, LnModArgs{});
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_segs(const QuantSegs& segs, hipStream_t s) {
+  if (segs.count < 1 || segs.count > kMaxQuantSegs || segs.total <= 0 ||
+      segs.total > 0x7FFFFFFF)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(act_quant_segs_kernel, dim3((unsigned)segs.total),
+                     dim3(kQuantUnitWaves * 64), 0, s, segs);
   return hipGetLastError();
 }
 

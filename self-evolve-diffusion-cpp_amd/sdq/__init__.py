@@ -36,6 +36,11 @@ class Epilogue(ctypes.Structure):
                 ("resid", ctypes.c_void_p)]
 
 
+class GroupItem(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("A", ctypes.c_void_p), ("M", ctypes.c_int64),
+                ("epi", Epilogue), ("Y", ctypes.c_void_p)]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int), ("cu_count", ctypes.c_int),
                 ("max_clock_khz", ctypes.c_int), ("mem_clock_khz", ctypes.c_int),
@@ -74,6 +79,7 @@ SIGNATURES = {
     "sdq_qgemm": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "sdq_qlinear_noalloc": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp,
                                            _vp]),
+    "sdq_qlinear_group": (ctypes.c_int, [ctypes.POINTER(GroupItem), ctypes.c_int, _vp]),
     "sdq_rmsnorm_rope_batch": (ctypes.c_int, [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_float,
                                               _vp]),
     "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
@@ -378,6 +384,31 @@ def qlinear(w: Weight, A, out, kind="none", bias=None, gate=None, resid=None, ga
     c.done()
     _check(_lib.sdq_qlinear(h, pa, M, w.K, ctypes.byref(e), _ptr(out), _stream(stream)))
     return out
+
+
+MAX_GROUP = 16  # SDQ_MAX_GROUP
+
+
+def qlinear_group(items, stream=None):
+    """Several independent Linears in one call (sdq_qlinear_group): the same
+    results as qlinear on each item. items: dicts with keys w, A, out and
+    optionally kind, bias, gate, resid, gate_fma (as qlinear's arguments)."""
+    if len(items) > MAX_GROUP:
+        raise _bad(f"at most {MAX_GROUP} items")
+    c = _Args()
+    arr = (GroupItem * max(1, len(items)))()
+    for i, it in enumerate(items):
+        w = it["w"]
+        arr[i].w = _weight(w, f"items[{i}].w")
+        arr[i].A = c(it["A"], f"items[{i}].A", "f32", (None, w.K))
+        M = it["A"].shape[0]
+        arr[i].M = M
+        arr[i].epi = _epilogue_args(c, it.get("kind", "none"), M, w.N, it["out"], it.get("bias"),
+                                    it.get("gate"), it.get("resid"), it.get("gate_fma", True))
+        arr[i].Y = c(it["out"], f"items[{i}].out", "i32" if arr[i].epi.kind == EPI_ACC else "f32",
+                     (M, w.N))
+    c.done()
+    _check(_lib.sdq_qlinear_group(arr, len(items), _stream(stream)))
 
 
 NOALLOC_SCRATCH_BYTES = 64 << 20  # SDQ_NOALLOC_SCRATCH_BYTES

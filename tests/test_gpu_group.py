@@ -1,0 +1,132 @@
+"""sdq_qlinear_group: several independent Linears in one call (one segmented
+quantizer launch, one persistent GEMM launch per set of items with the same
+K and epilogue form, the other items as separate calls) gives the same bits
+as one sdq_qlinear per item, and the oracle's results."""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(sdq, oracle, N, K, seed):
+    W = (oracle.randn(N * K, seed) * np.float32(0.03)).reshape(N, K)
+    q, s = oracle.quant_rows(W)
+    return sdq.Weight.from_host(q, s), q, s
+
+
+def _items(sdq, torch, oracle, dev, specs, seed0):
+    """specs: (M, K, N, kind, bias?) -> item dicts with inputs on the GPU."""
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)  # noqa: E731
+    items, host = [], []
+    for i, (M, K, N, kind, has_bias) in enumerate(specs):
+        sd = seed0 + 10 * i
+        w, q, s = _weight(sdq, oracle, N, K, sd)
+        A = oracle.randn(M * K, sd + 1).reshape(M, K)
+        b = oracle.randn(N, sd + 2) if has_bias else None
+        g = oracle.randn(N, sd + 3)
+        r = oracle.randn(M * N, sd + 4).reshape(M, N)
+        it = dict(w=w, A=t(A), out=torch.full((M, N), float("nan"), device=dev), kind=kind,
+                  bias=None if b is None else t(b))
+        if kind == "gated":
+            it.update(gate=t(g), resid=it["out"])
+            it["out"].copy_(t(r))
+        elif kind == "resid":
+            it.update(resid=it["out"])
+            it["out"].copy_(t(r))
+        items.append(it)
+        host.append(dict(A=A, q=q, s=s, b=b, g=g, r=r, kind=kind))
+    return items, host
+
+
+def _separate(sdq, torch, items, host):
+    outs = []
+    for it, h in zip(items, host):
+        y = torch.from_numpy(h["r"]).to(it["out"].device).contiguous() if h["kind"] in (
+            "gated", "resid") else torch.empty_like(it["out"])
+        sdq.qlinear(it["w"], it["A"], y, kind=h["kind"], bias=it["bias"], gate=it.get("gate"),
+                    resid=y if h["kind"] in ("gated", "resid") else None)
+        outs.append(y)
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in outs]
+
+
+def _oracle(oracle, h):
+    kw = dict(bias=h["b"])
+    if h["kind"] == "gated":
+        kw.update(epilogue="gated", gate=h["g"], resid=h["r"])
+    elif h["kind"] == "resid":
+        kw.update(epilogue="resid", resid=h["r"])
+    return oracle.linear(h["A"], h["q"], h["s"], **kw)
+
+
+@pytest.mark.parametrize("case", ["one_set", "mixed"])
+def test_group_equals_separate_calls(sdq_dev, oracle, case):
+    import torch
+
+    import sdq
+
+    if case == "one_set":
+        specs = [(100, 512, 384, "none", True), (157, 512, 256, "none", True),
+                 (300, 512, 640, "none", True), (65, 512, 128, "none", True)]
+    else:
+        specs = [(120, 512, 256, "gated", True), (90, 512, 512, "resid", True),
+                 (77, 512, 256, "gelu", True), (20, 512, 256, "none", True),   # skinny: alone
+                 (200, 512, 96, "none", False), (150, 1024, 256, "none", True),
+                 (133, 512, 384, "none", True), (0, 512, 128, "none", True),
+                 (2100, 512, 1024, "none", True), (129, 1024, 384, "none", True)]
+    print(f"[group] {case}: {len(specs)} items", flush=True)
+    items, host = _items(sdq, torch, oracle, sdq_dev, specs, 100)
+    sdq.qlinear_group(items)
+    torch.cuda.synchronize()
+    got = [it["out"].cpu().numpy() for it in items]
+    want = _separate(sdq, torch, items, host)
+    for i, (g, w, h) in enumerate(zip(got, want, host)):
+        assert_bitexact(g, w, f"item {i} ({specs[i]}) vs its own sdq_qlinear")
+        if h["kind"] != "gelu" and specs[i][0] > 0:
+            assert_bitexact(g, _oracle(oracle, h), f"item {i} vs the oracle")
+    for it in items:
+        it["w"].free()
+
+
+def test_group_repeated_growing_and_shrinking(sdq_dev, oracle):
+    """Consecutive calls of different sizes on one stream (the group scratch
+    grows, then is reused by a smaller call)."""
+    import torch
+
+    import sdq
+
+    for rnd, specs in enumerate(([(70, 512, 128, "none", True), (80, 512, 256, "none", True)],
+                                 [(700, 1024, 1024, "none", True), (300, 1024, 512, "none", True),
+                                  (257, 1024, 768, "none", True)],
+                                 [(66, 512, 128, "resid", True), (99, 512, 256, "resid", True)])):
+        print(f"[group] round {rnd}", flush=True)
+        items, host = _items(sdq, torch, oracle, sdq_dev, specs, 500 + 50 * rnd)
+        sdq.qlinear_group(items)
+        torch.cuda.synchronize()
+        for i, (it, h) in enumerate(zip(items, host)):
+            assert_bitexact(it["out"].cpu().numpy(), _oracle(oracle, h), f"round {rnd} item {i}")
+            it["w"].free()
+
+
+def test_group_raw_abi_errors(sdq_dev, oracle):
+    import ctypes
+
+    import sdq
+
+    lib = sdq.load_library()
+    assert lib.sdq_qlinear_group(None, -1, None) == sdq.ERR_INVALID
+    assert lib.sdq_qlinear_group(None, 17, None) == sdq.ERR_INVALID
+    assert lib.sdq_qlinear_group(None, 0, None) == 0
+    arr = (sdq.GroupItem * 1)()
+    assert lib.sdq_qlinear_group(arr, 1, None) == sdq.ERR_INVALID  # null weight
+    w, _, _ = _weight(sdq, oracle, 128, 512, 9)
+    arr[0].w = w.h
+    arr[0].M = 5
+    assert lib.sdq_qlinear_group(arr, 1, None) == sdq.ERR_INVALID  # null A / Y
+    assert b"null A or Y" in lib.sdq_last_error()
+    arr[0].epi.kind = 2  # gated without gate / resid
+    arr[0].A = arr[0].Y = ctypes.c_void_p(16)
+    assert lib.sdq_qlinear_group(arr, 1, None) == sdq.ERR_INVALID
+    w.free()
