@@ -326,13 +326,26 @@ def bench_twin(torch, sdq, args):
                 sa.wait_stream(sv)
             cur.wait_stream(sv)
             cur.wait_stream(sa)
+        # Both blocks of a layer through forward_pair (one stream): their
+        # attention Linears and the two cross-attention output projections
+        # each as one grouped launch (sdq_qlinear_group).
+        def fn3():
+            for i in range(layers):
+                blocks[2 * i].forward_pair(blocks[2 * i + 1], iov, ioa)
+
         ms_seq = _timed(torch, fn, 2, max(args.steps // 10, 3))
-        ms = _timed(torch, fn2, 2, max(args.steps // 10, 3))
+        ms_two = _timed(torch, fn2, 2, max(args.steps // 10, 3))
+        ms_grp = _timed(torch, fn3, 2, max(args.steps // 10, 3))
+        ms = min(ms_two, ms_grp)
         ops = sum(blocks[2 * i].ops(Mv, Mc, Ma) + blocks[2 * i + 1].ops(Ma, Mc, Mv)
                   for i in range(layers))
         lw = wbytes * (2 * layers) / len(blocks)  # bytes of the blocks this pass uses
         res["layers"][str(layers)] = {"ms_per_pass": round(ms, 4), "TOPS": round(ops / ms / 1e9, 2),
+                                      "ms_per_pass_grouped_pair": round(ms_grp, 4),
+                                      "ms_per_pass_two_streams": round(ms_two, 4),
                                       "ms_per_pass_one_stream": round(ms_seq, 4),
+                                      "kernel_ms_grouped_pair": (_kernel_split(sdq, fn3, 1)
+                                                                 if layers == 28 else None),
                                       "weight_GB": round(lw / 1e9, 3),
                                       "weight_stream_GBps": round(lw / ms / 1e6, 1),
                                       "repack_ms_total": round(t_repack * 1e3, 1)}

@@ -77,30 +77,88 @@ DitBlock::DitBlock(const LinearPart (&l)[kCount], bool fusion, bool on_device) :
   fc2_ = QLinear(std::vector<LinearPart>{l[FC2]}, on_device);
 }
 
-void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
+// One Linear of a run: out[M, N] = epilogue(A[M, K] W^T + b).
+struct LinCall {
+  const QLinear* l;
+  const float* A;
+  int64_t M;
+  int kind;
+  const float* gate;
+  float* Y;  // also the residual of the GATED / RESID kinds (in place)
+};
+
+namespace {
+
+bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+  if (!a || !b || !na || !nb) return false;
+  const char* pa = static_cast<const char*>(a);
+  const char* pb = static_cast<const char*>(b);
+  return pa < pb + nb && pb < pa + na;
+}
+
+// The calls in order: one sdq_qlinear_group when no call's output overlaps
+// another call's input or output (then the order cannot matter), else one
+// call after the other.
+void run_linears(const std::vector<LinCall>& calls, void* s) {
+  bool independent = calls.size() <= SDQ_MAX_GROUP;
+  for (size_t i = 0; independent && i < calls.size(); i++) {
+    const LinCall& c = calls[i];
+    const size_t yb = (size_t)(c.M * c.l->out_features()) * sizeof(float);
+    for (size_t j = 0; j < calls.size(); j++) {
+      if (i == j) continue;
+      const LinCall& d = calls[j];
+      const size_t ab = (size_t)(d.M * d.l->in_features()) * sizeof(float);
+      const size_t db = (size_t)(d.M * d.l->out_features()) * sizeof(float);
+      if (overlap(c.Y, yb, d.A, ab) || overlap(c.Y, yb, d.Y, db)) {
+        independent = false;
+        break;
+      }
+    }
+  }
+  auto epi = [](const LinCall& c) {
+    const bool res = c.kind == SDQ_EPI_GATED || c.kind == SDQ_EPI_RESID;
+    return sdq_epilogue{c.kind, 1, c.l->bias_device(), c.gate, res ? c.Y : nullptr};
+  };
+  if (!independent) {
+    for (const LinCall& c : calls) c.l->forward_device(c.A, c.M, c.kind, c.gate, c.Y, c.Y, s);
+    return;
+  }
+  std::vector<sdq_group_item> items;
+  for (const LinCall& c : calls) items.push_back(sdq_group_item{c.l->handle(), c.A, c.M, epi(c), c.Y});
+  check(sdq_qlinear_group(items.data(), (int)items.size(), s), "DitBlock linears");
+}
+
+}  // namespace
+
+// The Linears of the self and cross attention that read inputs the caller
+// already has (ovi_dit.cpp:176-188, 229-254): q|k|v (unless the block
+// normalizes x itself: then it runs first, from x), o into x, cross q, the
+// text k|v, the fusion k|v.
+void DitBlock::attn_linears(const sd_dit_block_io& io, std::vector<LinCall>& out) const {
+  if (!(io.shift_sa && io.scale_sa))
+    out.push_back({&qkv_, io.h_sa, io.M, SDQ_EPI_NONE, nullptr, io.qkv});
+  out.push_back({&o_, io.att, io.M, SDQ_EPI_GATED, io.gate_sa, io.x});
+  out.push_back({&cq_, io.xq, io.M, SDQ_EPI_NONE, nullptr, io.cq});
+  if (io.Mc > 0) out.push_back({&ckv_, io.ctx, io.Mc, SDQ_EPI_NONE, nullptr, io.ckv});
+  if (fusion_ && io.Mt > 0) out.push_back({&kvf_, io.tn, io.Mt, SDQ_EPI_NONE, nullptr, io.kvt});
+}
+
+void DitBlock::check_io(const sd_dit_block_io& io) const {
   need(io.M >= 0 && io.Mc >= 0 && io.Mt >= 0, "negative row count");
   need(io.x && io.gate_sa && io.gate_ffn, "x and gates are required");
-  // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-188, 205-212)
-  const bool ln_sa = io.shift_sa && io.scale_sa, ln_ffn = io.shift_ffn && io.scale_ffn;
-  if (ln_sa) {
-    sdq_epilogue e{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
-    check(sdq_qlinear_lnmod(qkv_.handle(), io.x, io.M, dim_, io.shift_sa, io.scale_sa, io.eps, &e,
-                            io.qkv, s),
-          "DitBlock q|k|v");
-  } else {
-    qkv_.forward_device(io.h_sa, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.qkv, s);
-  }
-  o_.forward_device(io.att, io.M, SDQ_EPI_GATED, io.gate_sa, io.x, io.x, s);
-  // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
-  // the other branch, then x += o(xt)                (ovi_dit.cpp:229-254)
-  cq_.forward_device(io.xq, io.M, SDQ_EPI_NONE, nullptr, nullptr, io.cq, s);
-  if (io.Mc > 0) ckv_.forward_device(io.ctx, io.Mc, SDQ_EPI_NONE, nullptr, nullptr, io.ckv, s);
-  if (fusion_ && io.Mt > 0)
-    kvf_.forward_device(io.tn, io.Mt, SDQ_EPI_NONE, nullptr, nullptr, io.kvt, s);
-  co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
+}
+
+void DitBlock::qkv_lnmod(const sd_dit_block_io& io, void* s) const {
+  sdq_epilogue e{SDQ_EPI_NONE, 1, qkv_.bias_device(), nullptr, nullptr};
+  check(sdq_qlinear_lnmod(qkv_.handle(), io.x, io.M, dim_, io.shift_sa, io.scale_sa, io.eps, &e,
+                          io.qkv, s),
+        "DitBlock q|k|v");
+}
+
+void DitBlock::ffn_linears(const sd_dit_block_io& io, void* s) const {
   // ffn: hid = gelu(fc1(h)); x += fc2(hid) * e[5]    (ovi_dit.cpp:214-222); one
   // call, so fc1's epilogue hands hid's row maxima to fc2's quantizer
-  if (ln_ffn)
+  if (io.shift_ffn && io.scale_ffn)
     check(sdq_ffn_lnmod(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.x,
                         io.M, io.shift_ffn, io.scale_ffn, io.eps, io.gate_ffn, 1, io.hid, s),
           "DitBlock ffn");
@@ -108,6 +166,38 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
     check(sdq_ffn(fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(), io.h_ffn,
                   io.M, io.gate_ffn, 1, io.hid, io.x, s),
           "DitBlock ffn");
+}
+
+void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
+  check_io(io);
+  // self attention: q|k|v, then x += o(att) * e[2]   (ovi_dit.cpp:176-188, 205-212);
+  // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
+  // the other branch (229-254). Independent given the inputs: one grouped
+  // run when no output overlaps another Linear's input.
+  if (io.shift_sa && io.scale_sa) qkv_lnmod(io, s);
+  std::vector<LinCall> calls;
+  attn_linears(io, calls);
+  run_linears(calls, s);
+  // then x += o(xt)                                   (251)
+  co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
+  ffn_linears(io, s);
+}
+
+void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
+                          const sd_dit_block_io& ib, void* s) {
+  a.check_io(ia);
+  b.check_io(ib);
+  if (ia.shift_sa && ia.scale_sa) a.qkv_lnmod(ia, s);
+  if (ib.shift_sa && ib.scale_sa) b.qkv_lnmod(ib, s);
+  std::vector<LinCall> calls;
+  a.attn_linears(ia, calls);
+  b.attn_linears(ib, calls);
+  run_linears(calls, s);
+  run_linears({{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x},
+               {&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}},
+              s);
+  a.ffn_linears(ia, s);
+  b.ffn_linears(ib, s);
 }
 
 void DitBlock::set_norms(const sd_dit_norms& n) {
@@ -578,6 +668,15 @@ int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void*
     return SDQ_ERR_INVALID;
   }
   return guarded([&] { b->blk.forward_linears(*io, stream); });
+}
+
+int sd_dit_block_forward_pair(const sd_dit_block* a, const sd_dit_block_io* ia,
+                              const sd_dit_block* b, const sd_dit_block_io* ib, void* stream) {
+  if (!a || !ia || !b || !ib) {
+    t_dit_err = "sd_dit_block_forward_pair: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded([&] { sd::gpu::forward_linears_pair(a->blk, *ia, b->blk, *ib, stream); });
 }
 
 int sd_dit_block_free(sd_dit_block* b) {

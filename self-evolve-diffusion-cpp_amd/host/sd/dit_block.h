@@ -120,6 +120,13 @@ int sd_dit_block_create(const sd_linear* lin, int fusion, int on_device, sd_dit_
 // streamed weight upload; out[i] receives block i.
 int sd_dit_block_create_many(const sd_linear* lin, int nblocks, int fusion, sd_dit_block** out);
 int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void* stream);
+// The linear stacks of two blocks whose inputs do not depend on each other
+// (the video and audio blocks of one twin layer, each with its own io): the
+// same results as sd_dit_block_forward on each, with the attention Linears
+// of both and the two cross-attention output projections each run as one
+// grouped launch (sdq_qlinear_group) when no output overlaps another input.
+int sd_dit_block_forward_pair(const sd_dit_block* a, const sd_dit_block_io* ia,
+                              const sd_dit_block* b, const sd_dit_block_io* ib, void* stream);
 int sd_dit_block_free(sd_dit_block* b);
 // Copies the block's norm vectors to the device (required before
 // sd_dit_block_step_forward; the fusion ones for fusion blocks, ln3 for others).
@@ -175,6 +182,8 @@ const char* sd_dit_last_error(void);
 namespace sd {
 namespace gpu {
 
+struct LinCall;  // one Linear of a grouped run (dit_block.cpp)
+
 class DitBlock {
  public:
   enum Lin { Q, K, V, O, CQ, CK, CV, CO, KF, VF, FC1, FC2, kCount };
@@ -189,6 +198,8 @@ class DitBlock {
   bool fusion() const { return fusion_; }
   // Runs the linear stack, stream-ordered (throws std::runtime_error).
   void forward_linears(const sd_dit_block_io& io, void* stream) const;
+  friend void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia,
+                                   const DitBlock& b, const sd_dit_block_io& ib, void* stream);
   double ops(int64_t M, int64_t Mc, int64_t Mt) const;
   // The whole block (norms, RoPE, attention and Linears) on device arrays.
   void set_norms(const sd_dit_norms& n);
@@ -208,6 +219,10 @@ class DitBlock {
   enum Norm { SA_NQ, SA_NK, CA_NQ, CA_NK, LN3_W, LN3_B, NK_F, PNF_W, PNF_B, kNorms };
   const float* norm(Norm n) const { return norms_.get() + n * dim_; }
   void self_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const;
+  void check_io(const sd_dit_block_io& io) const;
+  void qkv_lnmod(const sd_dit_block_io& io, void* s) const;
+  void attn_linears(const sd_dit_block_io& io, std::vector<LinCall>& out) const;
+  void ffn_linears(const sd_dit_block_io& io, void* s) const;
   void cross_ffn_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const;
   friend std::vector<DitBlock> dit_blocks_from_pack_file(const std::string&, const std::string&,
                                                          const std::vector<int>&, int64_t,
@@ -217,6 +232,11 @@ class DitBlock {
   int64_t dim_ = 0, ffn_ = 0;
   bool fusion_ = false;
 };
+
+// Both blocks' forward_linears (independent inputs), their attention Linears
+// and cross-attention output projections grouped (sd_dit_block_forward_pair).
+void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
+                          const sd_dit_block_io& ib, void* stream);
 
 // Block `layer` of a backbone in a load_sdcpp map, with the names and checks
 // of OviDit::load_impl (ovi_dit.cpp:505-530): "<prefix>blocks.<layer>.

@@ -747,6 +747,10 @@ def load_host_library(path: str = HOST_LIB_PATH):
                                            ctypes.POINTER(ctypes.c_void_p)]
     h.sd_dit_block_forward.restype = ctypes.c_int
     h.sd_dit_block_forward.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO), ctypes.c_void_p]
+    h.sd_dit_block_forward_pair.restype = ctypes.c_int
+    h.sd_dit_block_forward_pair.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO),
+                                            ctypes.c_void_p, ctypes.POINTER(BlockIO),
+                                            ctypes.c_void_p]
     h.sd_dit_block_set_norms.restype = ctypes.c_int
     h.sd_dit_block_set_norms.argtypes = [ctypes.c_void_p, ctypes.POINTER(DitNorms)]
     h.sd_dit_block_workspace_bytes.restype = ctypes.c_size_t
@@ -897,10 +901,7 @@ class DitBlock:
         _hcheck(_host.sd_dit_block_modulation(self.h, pt, pe, _stream(stream)))
         return e
 
-    def forward(self, stream=None, **io):
-        """io: M, Mc, Mt and the device tensors named in BlockIO; each tensor
-        given is checked against its [rows, cols] before the launch."""
-        c = _Args()
+    def _block_io(self, c, io):
         b = BlockIO()
         b.M, b.Mc, b.Mt = int(io.get("M", 0)), int(io.get("Mc", 0)), int(io.get("Mt", 0))
         shapes = self._io_shapes(b.M, b.Mc, b.Mt)
@@ -910,8 +911,25 @@ class DitBlock:
                 t = None  # a fusion input of a call without target rows is not read
             setattr(b, name, c(t, name, "f32", shapes[name], optional=True))
         b.eps = float(io.get("eps", 1e-6))
+        return b
+
+    def forward(self, stream=None, **io):
+        """io: M, Mc, Mt and the device tensors named in BlockIO; each tensor
+        given is checked against its [rows, cols] before the launch."""
+        c = _Args()
+        b = self._block_io(c, io)
         c.done()
         _hcheck(_host.sd_dit_block_forward(self.h, ctypes.byref(b), _stream(stream)))
+
+    def forward_pair(self, other, io, io_other, stream=None):
+        """forward(**io) on this block and forward(**io_other) on `other` (two
+        blocks with independent inputs, e.g. the video and audio blocks of a
+        twin layer), their attention Linears grouped (sd_dit_block_forward_pair)."""
+        c = _Args()
+        a, b = self._block_io(c, io), other._block_io(c, io_other)
+        c.done()
+        _hcheck(_host.sd_dit_block_forward_pair(self.h, ctypes.byref(a), other.h, ctypes.byref(b),
+                                                _stream(stream)))
 
     def ops(self, M, Mc=0, Mt=0) -> float:
         return _host.sd_dit_block_ops(self.h, M, Mc, Mt)

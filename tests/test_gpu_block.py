@@ -242,3 +242,63 @@ def test_block_create_many_matches_single(sdq_dev, oracle):
                  inp, True, Mt)
     for blk in many:
         blk.free()
+
+
+def _outs(torch, dev, M, Mc, Mt, dim, ffn):
+    return dict(qkv=torch.empty((M, 3 * dim), device=dev), cq=torch.empty((M, dim), device=dev),
+                ckv=torch.empty((Mc, 2 * dim), device=dev),
+                kvt=torch.empty((max(Mt, 1), 2 * dim), device=dev),
+                hid=torch.empty((M, ffn), device=dev))
+
+
+@pytest.mark.parametrize("dim,ffn,Mv,Ma,Mc", [(512, 1408, 300, 90, 77), (3072, 14336, 768, 157, 512)])
+def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc):
+    """forward_pair: the video and audio blocks of one twin layer with their
+    attention Linears (and the two cross-o projections) grouped; every output
+    of both blocks against the oracle."""
+    import torch
+
+    import sdq
+
+    print(f"[block-pair] dim={dim} Mv={Mv} Ma={Ma} Mc={Mc}", flush=True)
+    lv, la = _weights(oracle, dim, ffn, 900, True), _weights(oracle, dim, ffn, 950, True)
+    iv, ia = _inputs(oracle, Mv, Mc, Ma, dim, 300), _inputs(oracle, Ma, Mc, Mv, dim, 400)
+    bv, ba = sdq.DitBlock(lv, True), sdq.DitBlock(la, True)
+    t = lambda inp: {k: torch.from_numpy(np.ascontiguousarray(v)).to(sdq_dev)  # noqa: E731
+                     for k, v in inp.items()}
+    dv, da = t(iv), t(ia)
+    ov, oa = _outs(torch, sdq_dev, Mv, Mc, Ma, dim, ffn), _outs(torch, sdq_dev, Ma, Mc, Mv, dim, ffn)
+    bv.forward_pair(ba, dict(M=Mv, Mc=Mc, Mt=Ma, **dv, **ov), dict(M=Ma, Mc=Mc, Mt=Mv, **da, **oa))
+    torch.cuda.synchronize()
+    for got_o, d, lin, inp, Mt in ((ov, dv, lv, iv, Ma), (oa, da, la, ia, Mv)):
+        got = {k: v.cpu().numpy() for k, v in got_o.items()}
+        got["x"] = d["x"].cpu().numpy()
+        _check_small(oracle, got, lin, inp, True, Mt)
+    bv.free()
+    ba.free()
+
+
+def test_block_aliased_cross_q_runs_in_order(sdq_dev, oracle):
+    """Cross q reading x itself (as a fusion block's q does): the o projection
+    writes x, so the Linears may not be grouped; cross q must see x after
+    x += o(att) * gate, exactly as the reference order has it."""
+    import torch
+
+    import sdq
+
+    dim, ffn, M, Mc, Mt = 512, 1408, 200, 64, 40
+    lin = _weights(oracle, dim, ffn, 1200, True)
+    inp = _inputs(oracle, M, Mc, Mt, dim, 1300)
+    blk = sdq.DitBlock(lin, True)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(sdq_dev) for k, v in inp.items()}
+    d["xq"] = d["x"]  # the same tensor
+    outs = _outs(torch, sdq_dev, M, Mc, Mt, dim, ffn)
+    blk.forward(M=M, Mc=Mc, Mt=Mt, **d, **outs)
+    torch.cuda.synchronize()
+    L = lambda A, n, **kw: oracle.linear(A, lin[n][0], lin[n][1], bias=lin[n][2], **kw)  # noqa
+    x1 = L(inp["att"], "o", epilogue="gated", gate=inp["gate_sa"], resid=inp["x"])
+    assert_bitexact(outs["cq"].cpu().numpy(), L(x1, "cq"), "cross q on the updated x")
+    x2 = L(inp["xt"], "co", epilogue="resid", resid=x1)
+    x3 = L(outs["hid"].cpu().numpy(), "fc2", epilogue="gated", gate=inp["gate_ffn"], resid=x2)
+    assert_bitexact(d["x"].cpu().numpy(), x3, "residual stream x")
+    blk.free()
