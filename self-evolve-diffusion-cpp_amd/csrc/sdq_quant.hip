@@ -160,6 +160,7 @@ ln_stats_kernel(const float* __restrict__ x, int64_t M, int64_t K, float eps,
   const float* r = x + (ok ? row : 0) * K;
   float mu = ln_pass<VEC, 0, D>(r, K, l, tb, 0.f);
   mu = mu / (float)K;
+  mu = __shfl(mu, l & 7);  // lanes 0-7 hold the rows' sums; lane l works on row l & 7
   const float var = ln_pass<VEC, 1, D>(r, K, l, tb, mu);
   if (l < 8 && ok) {
     const float den = var / (float)K + eps;

@@ -49,49 +49,31 @@ __device__ __forceinline__ float4 mask4(float4 v, int64_t c, int64_t K) {
   return v;
 }
 
-// Serial sum of one 32-column tile of this lane's row (lanes 0-7) from the
-// transposed tile in LDS: PASS 0 adds the values, PASS 1 the rounded
-// (v - mu)^2, PASS 2 the rounded v^2; n = columns of the tile inside the row
-// (32 but for the last).
+// The summed term of value v: v (PASS 0), the rounded (v - mu)^2 (PASS 1),
+// the rounded v^2 (PASS 2).
 template <int PASS>
+__device__ __forceinline__ float ln_term(float v, float mu) {
+  if constexpr (PASS == 0) {
+    return v;
+  } else if constexpr (PASS == 1) {
+    const float d = v - mu;
+    return d * d;
+  } else {
+    return v * v;
+  }
+}
+
+// Serial sum of one 32-column tile of this lane's row (lanes 0-7) from the
+// transposed tile of terms in LDS; n = columns of the tile inside the row
+// (32 but for the last).
 __device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int l, float acc,
-                                             float mu, int n) {
-  auto add = [&](float v) {
-    if constexpr (PASS == 0) {
-      acc = acc + v;
-    } else if constexpr (PASS == 1) {
-      const float d = v - mu;
-      const float dd = d * d;
-      acc = acc + dd;
-    } else {
-      const float vv = v * v;
-      acc = acc + vv;
-    }
-  };
+                                             int n) {
   if (n == 32) {
-    // all eight reads first (one LDS latency per tile), then the 32 terms
-    // (the rounded squares, in place), then the 32 adds back to back: the
-    // chain then holds only the dependent adds
+    // all eight reads first (one LDS latency per tile), then the 32 dependent
+    // adds back to back
     float4 v[8];
 #pragma unroll
     for (int q = 0; q < 8; q++) v[q] = tb[q * 8 + l];
-    if constexpr (PASS != 0) {
-      auto term = [&](float x) {
-        if constexpr (PASS == 1) {
-          const float d = x - mu;
-          return d * d;
-        } else {
-          return x * x;
-        }
-      };
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        v[q].x = term(v[q].x);
-        v[q].y = term(v[q].y);
-        v[q].z = term(v[q].z);
-        v[q].w = term(v[q].w);
-      }
-    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 8; q++) {
@@ -104,14 +86,17 @@ __device__ __forceinline__ float ln_tile_sum(const float4* __restrict__ tb, int 
     for (int c = 0; c < n; c++) {
       const float4 v = tb[(c >> 2) * 8 + l];
       const int e = c & 3;
-      add(e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w)));
+      acc = acc + (e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w)));
     }
   }
   return acc;
 }
 
 // For one-wave workgroups only (64 threads: tb is the wave's own tile
-// buffer, and no barrier orders other waves).
+// buffer, and no barrier orders other waves). Every lane turns its 4 values
+// into terms before the tile goes to LDS (PASS 1 needs the row's mean in
+// every lane: lane l holds row l & 7), so the 8 adding lanes run only the
+// chain of dependent adds.
 template <bool VEC, int PASS, int D>
 __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K, int l,
                                          float4 (&tb)[2][64], float mu) {
@@ -125,7 +110,15 @@ __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K,
 #pragma unroll
     for (int u = 0; u < D; u++) {
       const int64_t t = t0 + u;
-      tb[t & 1][l] = mask4(buf[u], t * 32 + 4 * j, K);
+      float4 v = mask4(buf[u], t * 32 + 4 * j, K);
+      if constexpr (PASS != 0) {
+        // columns past K: never summed (ln_tile_sum adds n terms)
+        v.x = ln_term<PASS>(v.x, mu);
+        v.y = ln_term<PASS>(v.y, mu);
+        v.z = ln_term<PASS>(v.z, mu);
+        v.w = ln_term<PASS>(v.w, mu);
+      }
+      tb[t & 1][l] = v;
       buf[u] = load4<VEC>(r, (t + D) * 32 + 4 * j, K);
       // The workgroup is one wave (64 threads): its LDS operations execute
       // in issue order, so waiting for the tile's LDS write is enough. A
@@ -134,7 +127,7 @@ __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K,
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (l < 8 && t < nt) {
         const int n = (int)((K - t * 32) < 32 ? (K - t * 32) : 32);
-        acc = ln_tile_sum<PASS>(tb[t & 1], l, acc, mu, n);
+        acc = ln_tile_sum(tb[t & 1], l, acc, n);
       }
     }
   }
