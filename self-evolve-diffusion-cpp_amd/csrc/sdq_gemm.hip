@@ -1343,10 +1343,11 @@ int64_t tail_split_rows(int64_t M, int64_t N, int cu_count) {
 }
 
 int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count) {
-  // Long K on a grid that leaves CUs idle: split K so the 128x128 kernel's
-  // (tile, k-range) items number at most one per CU (measured: more items
-  // than CUs is slower, the two workgroups of a CU then share its LDS and
-  // load bandwidth and the slices grow); each item keeps >= 16 k-fragments.
+  // Long K on a grid that leaves workgroup slots idle: split K so the
+  // 128x128 kernel's (tile, k-range) items fill up to its 2 slots per CU,
+  // at most 4 ways, each item keeping >= 16 k-fragments. Measured at K =
+  // 14336: N = 3072, M = 768 (144 tiles) 71 -> 58 us with S = 2 (288 items);
+  // M = 157 (48 tiles) best at S = 4 (24 us; S = 8: 25-29 us).
   // SDQ_FORCE_SPLITK=S overrides the factor (1 = never split); a factor
   // that does not divide the k-fragments into >= 16 per item is lowered.
   if (cfg != kCfg128x128 || N % 4 != 0) return 1;
@@ -1355,8 +1356,8 @@ int choose_splitk(int cfg, int64_t M, int64_t N, int64_t KFp, int cu_count) {
   if (S == 0) {
     if (KFp < 192) return 1;
     const int64_t T = ceil_div(M, 128) * ceil_div(N, 128);
-    const int64_t per = (cu_count > 0 ? cu_count : 256) / T;
-    S = per < 1 ? 1 : (per > 8 ? 8 : (int)per);
+    const int64_t per = 2 * (int64_t)(cu_count > 0 ? cu_count : 256) / T;
+    S = per < 1 ? 1 : (per > 4 ? 4 : (int)per);
   }
   if (S > 8) S = 8;
   while (S > 1 && (KFp % (2 * S) != 0 || KFp / S < 16)) S--;

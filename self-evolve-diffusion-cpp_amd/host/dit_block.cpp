@@ -312,15 +312,18 @@ void DitBlock::cross_ffn_phase(const sd_dit_block_step& st, int batch, float* ws
     check(sdq_layernorm(st.x, BM, C, norm(LN3_W), norm(LN3_B), st.eps, aux, s), "norm3");
     qin = aux;
   }
-  cq_.forward_device(qin, BM, SDQ_EPI_NONE, nullptr, nullptr, cq, s);
-  ckv_.forward_device(st.ctx, BMc, SDQ_EPI_NONE, nullptr, nullptr, ckv, s);
+  // cross q, the text k|v and the fusion k|v (on the layernormed target)
+  // read inputs that are ready here: one grouped run
   float* kvt = ws + c.kvt;
-  if (fusion_) {  // the target's k|v first, so the three norms share one launch
+  std::vector<LinCall> calls{{&cq_, qin, BM, SDQ_EPI_NONE, nullptr, cq},
+                             {&ckv_, st.ctx, BMc, SDQ_EPI_NONE, nullptr, ckv}};
+  if (fusion_) {
     float* tn = ws + c.tn;
     check(sdq_layernorm(st.target, BMt, C, norm(PNF_W), norm(PNF_B), st.eps, tn, s),
           "pre_attn_norm_fusion");
-    kvf_.forward_device(tn, BMt, SDQ_EPI_NONE, nullptr, nullptr, kvt, s);
+    calls.push_back({&kvf_, tn, BMt, SDQ_EPI_NONE, nullptr, kvt});
   }
+  run_linears(calls, s);
   // rmsnorm of cross q and context k (no rotation); fusion: rmsnorm_k_fusion
   // + the target's rotation of k_fusion. Independent row sets, one launch.
   const sdq_rms_seg nk[3] = {{cq, BM, C, norm(CA_NQ), nullptr, 0},
