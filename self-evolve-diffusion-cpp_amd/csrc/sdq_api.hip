@@ -80,6 +80,8 @@ struct Workspace {
   size_t rinv_bytes = 0;
   char* grp = nullptr;  // sdq_qlinear_group's per-item scratch
   size_t grp_bytes = 0;
+  float* sdpa_part = nullptr;  // attention key splits' partial outputs and states
+  size_t sdpa_part_bytes = 0;
 };
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -1225,8 +1227,15 @@ int sdq_sdpa_batched(const float* q, int64_t ldq, const float* k, int64_t ldk, c
   if (rc) return rc;
   if ((rc = ensure_device(dev))) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int cu_count = g_dev[dev].cu_count;
+  float* part = nullptr;
+  const int64_t pf = sdpa_part_floats(Lq, Lk, heads, batch, cu_count);
+  if (pf > 0 && (rc = ws_floats(dev, s, &Workspace::sdpa_part, &Workspace::sdpa_part_bytes,
+                                (size_t)pf * sizeof(float), &part)))
+    return rc;
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
-  hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s, batch);
+  hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s, batch, part,
+                             cu_count);
   if (e != hipSuccess) return hip_error(e, "sdpa launch");
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);

@@ -232,11 +232,22 @@ constexpr int kKB = 32;       // keys per block
 constexpr int kKPad = 132;    // LDS row of K (floats): conflict-free 16-byte reads
 constexpr int kVPd = 20;      // LDS row of V^T (dwords: 32 bf16 + pad; conflict-free stash)
 
-template <int NW>
+// Key split (SPLIT): workgroup z of the grid takes key blocks [z*kbs,
+// (z+1)*kbs) and writes its unnormalized output and its (max, sum) state to
+// part (layout in SdpaPart); sdpa_merge_kernel combines the splits.
+struct SdpaPart {
+  float* o;    // [splits][rows][heads * 128]: unnormalized sum of p * v
+  float2* ml;  // [splits][rows][heads]: (running max, sum of p), base 2
+  int64_t rows;  // batch * Lq
+  int heads;
+  int kbs;     // key blocks per split
+};
+
+template <int NW, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64)
 sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
             const float* __restrict__ V, int64_t ldv, float* __restrict__ O, int64_t ldo,
-            int64_t Lq, int64_t Lk, int qgroups, float scale_log2e) {
+            int64_t Lq, int64_t Lk, int qgroups, float scale_log2e, SdpaPart part) {
   // Sequence blockIdx.y of a batch: its Lq query rows and Lk key rows follow
   // the previous sequence's (stacked rows, attention stays inside each).
   Q += (int64_t)blockIdx.y * Lq * ldq;
@@ -255,6 +266,9 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   const int64_t q0 = ((int64_t)qg * NW + w) * 32;
   const int j = lane & 31, h = lane >> 5;
   const int64_t col = (int64_t)head * kHd;
+  // key blocks of this workgroup: all, or its split's range
+  int64_t kb0 = 0;
+  if constexpr (SPLIT) kb0 = (int64_t)blockIdx.z * part.kbs;
 
   // this lane's query row, dims 64h .. 64h+63
   float qr[64];
@@ -285,6 +299,7 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     return (p & 16) + (q == 1 ? 8 : q == 2 ? 4 : 4 * q) + (p & 3);
   };
   auto fetch_k = [&](int64_t kb) {
+    if constexpr (SPLIT) kb += kb0;
 #pragma unroll
     for (int c = 0; c < PER; c++) {
       const int f = tid + c * NT;
@@ -295,6 +310,7 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     }
   };
   auto fetch_v = [&](int64_t kb) {
+    if constexpr (SPLIT) kb += kb0;
 #pragma unroll
     for (int c = 0; c < PERV; c++) {
       const int f = tid + c * NT;
@@ -358,7 +374,8 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
 #pragma unroll
   for (int t = 0; t < 4; t++) acc[t] = v16f{};
   float m = -INFINITY, lsum = 0.f;
-  const int64_t nkb = (Lk + kKB - 1) / kKB;
+  int64_t nkb = (Lk + kKB - 1) / kKB;
+  if constexpr (SPLIT) nkb = (nkb - kb0) < part.kbs ? (nkb - kb0) : part.kbs;
   // prologue: K(0) -> scores; then K(1) and V(0) staged
   fetch_k(0);
   stash_k(0);
@@ -379,7 +396,8 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     // register r holds key kb*32 + 8(r/4) + 4h + r%4; keys past Lk are -inf.
     // v_exp_f32 flushes results below 2^-126 to 0, which moves a row sum
     // that holds a 1 (the max) by less than 2^-121.
-    const int rem = Lk - kb * kKB < kKB ? (int)(Lk - kb * kKB) : kKB;
+    const int64_t kba = SPLIT ? kb0 + kb : kb;  // the block's index among all keys
+    const int rem = Lk - kba * kKB < kKB ? (int)(Lk - kba * kKB) : kKB;
     float t[16];
     float mloc = -INFINITY;
 #pragma unroll
@@ -438,8 +456,26 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     __syncthreads();
   }
   // out[query][dim]: lane holds dims 32tt + 8(r/4) + 4h + r%4 of query j
-  const float inv = 1.f / (lsum + __shfl_xor(lsum, 32));
+  const float ltot = lsum + __shfl_xor(lsum, 32);
   const int64_t qi = q0 + j;
+  if constexpr (SPLIT) {
+    if (qi < Lq) {
+      const int64_t row = (int64_t)blockIdx.y * Lq + qi;
+      const int64_t sr = (int64_t)blockIdx.z * part.rows + row;
+      float* dst = part.o + sr * part.heads * kHd + col;
+#pragma unroll
+      for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 o = {acc[tt][4 * g], acc[tt][4 * g + 1], acc[tt][4 * g + 2],
+                            acc[tt][4 * g + 3]};
+          *reinterpret_cast<float4*>(dst + 32 * tt + 8 * g + 4 * h) = o;
+        }
+      if (h == 0) part.ml[sr * part.heads + head] = float2{m, ltot};
+    }
+    return;
+  }
+  const float inv = 1.f / ltot;
   if (qi < Lq) {
     float* dst = O + qi * ldo + col;
 #pragma unroll
@@ -453,11 +489,91 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   }
 }
 
+// out[row][head dims] = sum_s w_s o_s / sum_s w_s l_s, w_s = 2^(m_s - max m):
+// the splits' partial softmax states combined. One thread per 4 dims.
+__global__ void __launch_bounds__(256)
+sdpa_merge_kernel(SdpaPart part, int splits, int64_t Lq, float* __restrict__ O, int64_t ldo) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = (int64_t)part.heads * (kHd / 4);
+  if (idx >= part.rows * per_row) return;
+  const int64_t row = idx / per_row;
+  const int rem = (int)(idx - row * per_row);
+  const int head = rem / (kHd / 4), d4 = rem - head * (kHd / 4);
+  float mx = -INFINITY;
+  for (int sp = 0; sp < splits; sp++)
+    mx = fmaxf(mx, part.ml[((int64_t)sp * part.rows + row) * part.heads + head].x);
+  float lt = 0.f;
+  float4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < splits; sp++) {
+    const int64_t sr = (int64_t)sp * part.rows + row;
+    const float2 ml = part.ml[sr * part.heads + head];
+    const float w = __builtin_amdgcn_exp2f(ml.x - mx);  // an empty split: -inf - mx -> 0
+    lt += w * ml.y;
+    const float4 v = *reinterpret_cast<const float4*>(part.o + sr * part.heads * kHd +
+                                                      (int64_t)head * kHd + 4 * d4);
+    o.x += w * v.x;
+    o.y += w * v.y;
+    o.z += w * v.z;
+    o.w += w * v.w;
+  }
+  const float inv = 1.f / lt;
+  // rows of batch b's Lq queries are contiguous in O (row = b * Lq + q)
+  *reinterpret_cast<float4*>(O + row * ldo + (int64_t)head * kHd + 4 * d4) =
+      float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+}
+
 }  // namespace
+
+// Waves per workgroup of a key-split launch: 8 (256 queries share each
+// staged K / V block) from 512 queries up, else 2.
+int sdpa_split_nw(int64_t Lq) { return Lq >= 512 ? 8 : 2; }
+
+// Key splits for a sequence of Lq queries, Lk keys: the factor S that
+// minimizes the rounds of resident workgroups per unit of work (rounds / S;
+// the kernel's registers and LDS allow one 8-wave or two 2-wave workgroups
+// per CU), each split keeping >= 3 key blocks and none empty; a split must
+// beat the unsplit launch by 10% (the merge reads the partial outputs back).
+// Depends on the sequence only, not on the batch, so stacked and separate
+// calls give the same bits.
+int sdpa_splits(int64_t Lq, int64_t Lk, int heads, int cu_count) {
+  if (Lq >= 1024 || Lq <= 0 || Lk <= 0 || heads <= 0) return 1;  // many queries: no split
+  if (const char* e = getenv("SDQ_SDPA_SPLIT")) {
+    const int f = atoi(e);
+    return f < 2 ? 1 : (f > 16 ? 16 : f);
+  }
+  const int64_t cus = cu_count > 0 ? cu_count : 256;
+  const int nw = sdpa_split_nw(Lq);
+  const int64_t groups = ceil_div(Lq, 32 * nw) * heads;
+  const int64_t cap = nw == 8 ? cus : 2 * cus;
+  // the unsplit launch (2-wave groups below 1024 queries)
+  const double unsplit = (double)ceil_div(ceil_div(Lq, 64) * heads, 2 * cus);
+  const int64_t nkb = ceil_div(Lk, kKB);
+  const int64_t smax = nkb / 3 < 16 ? nkb / 3 : 16;
+  int best = 1;
+  double best_cost = unsplit;
+  for (int64_t S = 2; S <= smax; S++) {
+    if (ceil_div(nkb, ceil_div(nkb, S)) != S) continue;  // no empty split
+    // rounds of resident groups, each walking 1/S of the keys (a group of
+    // either width takes about as long per key block)
+    const double cost = (double)ceil_div(groups * S, cap) / (double)S;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = (int)S;
+    }
+  }
+  return best_cost <= 0.9 * unsplit ? best : 1;
+}
+
+int64_t sdpa_part_floats(int64_t Lq, int64_t Lk, int heads, int batch, int cu_count) {
+  const int S = sdpa_splits(Lq, Lk, heads, cu_count);
+  if (S <= 1) return 0;
+  const int64_t rows = (int64_t)batch * Lq;
+  return (int64_t)S * rows * heads * (kHd + 2);
+}
 
 hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                        int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
-                       hipStream_t s, int batch) {
+                       hipStream_t s, int batch, float* part, int cu_count) {
   if (Lq <= 0 || batch == 0) return hipSuccess;
   if (Lk <= 0 || heads <= 0 || batch < 0 || batch > 65535) return hipErrorInvalidValue;
   const float scale_log2e = (1.f / sqrtf((float)kHd)) * 1.4426950408889634f;
@@ -468,12 +584,34 @@ hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk,
     return v == 2 || v == 4 || v == 8 ? v : 0;
   }();
   const int nw = forced ? forced : Lq >= 1024 ? 8 : 2;
+  const int S = part && !forced ? sdpa_splits(Lq, Lk, heads, cu_count) : 1;
+  if (S > 1) {
+    // key splits, then the merge (part: sdpa_part_floats floats)
+    SdpaPart pp{part, nullptr, (int64_t)batch * Lq, heads, 0};
+    pp.ml = reinterpret_cast<float2*>(part + (int64_t)S * pp.rows * heads * kHd);
+    pp.kbs = (int)ceil_div(ceil_div(Lk, kKB), S);
+    const int snw = sdpa_split_nw(Lq);
+    const int qgroups = (int)ceil_div(Lq, 32 * snw);
+    const dim3 grid((unsigned)(qgroups * heads), (unsigned)batch, (unsigned)S);
+    if (snw == 8)
+      hipLaunchKernelGGL((sdpa_kernel<8, true>), grid, dim3(512), 0, s, q, ldq, k, ldk, v, ldv,
+                         out, ldo, Lq, Lk, qgroups, scale_log2e, pp);
+    else
+      hipLaunchKernelGGL((sdpa_kernel<2, true>), grid, dim3(128), 0, s, q, ldq, k, ldk, v, ldv,
+                         out, ldo, Lq, Lk, qgroups, scale_log2e, pp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t n = pp.rows * heads * (kHd / 4);
+    hipLaunchKernelGGL(sdpa_merge_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, pp,
+                       S, Lq, out, ldo);
+    return hipGetLastError();
+  }
   auto go = [&](auto nwc) {
     constexpr int NW = decltype(nwc)::value;
     const int qgroups = (int)ceil_div(Lq, 32 * NW);
-    hipLaunchKernelGGL((sdpa_kernel<NW>), dim3((unsigned)(qgroups * heads), (unsigned)batch),
+    hipLaunchKernelGGL((sdpa_kernel<NW, false>), dim3((unsigned)(qgroups * heads), (unsigned)batch),
                        dim3(NW * 64), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, qgroups,
-                       scale_log2e);
+                       scale_log2e, SdpaPart{});
   };
   if (nw == 8)
     go(std::integral_constant<int, 8>{});

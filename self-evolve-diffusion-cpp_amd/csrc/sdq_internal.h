@@ -150,9 +150,16 @@ hipError_t launch_linear_f32(const float* x, int64_t M, int64_t K, const float* 
 // batch > 1: `batch` sequences stacked along the rows (sequence b: query rows
 // [b*Lq, (b+1)*Lq), key / value rows [b*Lk, (b+1)*Lk)), each attending only
 // to its own keys.
+// part (nullable): scratch of sdpa_part_floats floats; with it, few queries
+// run as key splits (more workgroups) merged by a second kernel; without it,
+// one workgroup walks all keys. cu_count: the device's CUs.
 hipError_t launch_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                        int64_t ldv, float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads,
-                       hipStream_t s, int batch = 1);
+                       hipStream_t s, int batch = 1, float* part = nullptr, int cu_count = 0);
+// Key splits launch_sdpa uses for a sequence (1 = none), and the scratch
+// floats they need for `batch` stacked sequences (0 = none).
+int sdpa_splits(int64_t Lq, int64_t Lk, int heads, int cu_count);
+int64_t sdpa_part_floats(int64_t Lq, int64_t Lk, int heads, int batch, int cu_count);
 // Same output, with the row maxima already known: max_c rmax[row*rstride + c]
 // over c < rchunks (e.g. written by the producing GEMM's epilogue), so A is
 // read once.

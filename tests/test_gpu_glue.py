@@ -64,12 +64,14 @@ def test_rmsnorm_rope_errors(sdq_dev):
 
 
 @pytest.mark.parametrize("Lq,Lk,heads", [(37, 53, 2), (300, 300, 3), (157, 512, 2), (1100, 157, 2),
-                                         (64, 1, 1)])
+                                         (64, 1, 1), (157, 768, 24), (768, 768, 24)])
 def test_sdpa_matches_oracle(sdq_dev, oracle, Lq, Lk, heads):
     """Attention on q|k|v-style strided inputs against the oracle (bit-exact
     with the reference build's sdpa): within 2e-5 of the output scale (QK^T
     on the fp32 MFMA, PV as three bf16 MFMA products per fp32 product, and an
-    online softmax sum in another order)."""
+    online softmax sum in another order). Few queries run as key splits
+    merged afterwards (here 300x300, 157x512, and the twin backbone's audio
+    fusion and video self-attention shapes)."""
     import torch
 
     import sdq
@@ -91,6 +93,43 @@ def test_sdpa_matches_oracle(sdq_dev, oracle, Lq, Lk, heads):
     err = np.abs(got.astype(np.float64) - want) / (np.abs(want).max() + 1e-30)
     print(f"  max rel err {err.max():.3e}", flush=True)
     assert err.max() <= 2e-5, float(err.max())
+
+
+@pytest.mark.parametrize("Lq,Lk", [(157, 512), (768, 768)])
+def test_sdpa_split_stacked_equals_separate(sdq_dev, oracle, Lq, Lk):
+    """Key-split shapes (24 heads): two sequences stacked in one call give
+    the bits of two separate calls (the split factor depends on the sequence,
+    not on the batch), and forcing no split stays within the tolerance."""
+    import os
+
+    import torch
+
+    import sdq
+
+    from conftest import assert_bitexact
+
+    heads, B = 24, 2
+    C = heads * 128
+    rng = np.random.default_rng(Lq + 3 * Lk)
+    q = torch.from_numpy((rng.standard_normal((B * Lq, C)) * 0.6).astype(np.float32)).to(sdq_dev)
+    kv = torch.from_numpy(rng.standard_normal((B * Lk, 2 * C)).astype(np.float32)).to(sdq_dev)
+    out = torch.empty((B * Lq, C), device=sdq_dev)
+    sdq.sdpa(q, kv, kv, out, heads, kcol=0, vcol=C, batch=B)
+    for b in range(B):
+        one = torch.empty((Lq, C), device=sdq_dev)
+        qs, ks = q[b * Lq:(b + 1) * Lq], kv[b * Lk:(b + 1) * Lk]
+        sdq.sdpa(qs, ks, ks, one, heads, kcol=0, vcol=C)
+        torch.cuda.synchronize()
+        assert_bitexact(out[b * Lq:(b + 1) * Lq].cpu().numpy(), one.cpu().numpy(), f"seq {b}")
+    os.environ["SDQ_SDPA_SPLIT"] = "1"
+    try:
+        whole = torch.empty((Lq, C), device=sdq_dev)
+        sdq.sdpa(q[:Lq], kv[:Lk], kv[:Lk], whole, heads, kcol=0, vcol=C)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["SDQ_SDPA_SPLIT"]
+    a, w = out[:Lq].cpu().numpy().astype(np.float64), whole.cpu().numpy().astype(np.float64)
+    assert np.abs(a - w).max() / np.abs(w).max() <= 2e-5
 
 
 def test_sdpa_fullsize_sampled(sdq_dev, oracle):
