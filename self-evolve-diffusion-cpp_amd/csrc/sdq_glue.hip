@@ -20,9 +20,12 @@
 namespace sdq {
 namespace {
 
+using rowsum::kFullMaxBytes;
 using rowsum::kLnDepthFew;
+using rowsum::kLnDepthFull;
 using rowsum::kLnDepthMany;
 using rowsum::ln_pass;
+using rowsum::ln_pass_full;
 
 // Up to kMaxRmsSegs column blocks of strided rows in one launch (e.g. the q
 // and k blocks of q|k|v, or cross q, context k and fusion k): their serial
@@ -54,6 +57,33 @@ rms_stats_kernel(RmsSegs sg, int64_t C, float eps) {
   const bool ok = row < g.L;
   const float* r = g.x + (ok ? row : 0) * g.ld;
   const float ss = ln_pass<VEC, 2, D>(r, C, l, tb, 0.f);
+  if (l < 8 && ok) {
+    const float den = ss / (float)C + eps;
+    g.inv[row] = 1.f / sqrtf(den);
+  }
+}
+
+// Bytes the segment's rows span: (L-1) strides and one row of C.
+__host__ __device__ inline int64_t seg_span_bytes(const RmsSeg& g, int64_t C) {
+  return ((g.L - 1) * g.ld + C) * 4;
+}
+
+// The same statistics when every segment has C % 32 == 0, 16-byte aligned
+// rows and a span of at most kFullMaxBytes: whole 32-column tiles through a
+// buffer descriptor over the segment's rows.
+__global__ void __launch_bounds__(64)
+rms_stats_full_kernel(RmsSegs sg, int64_t C, float eps) {
+  __shared__ float4 tb[3][64];
+  const int l = threadIdx.x;
+  const int i = seg_of(sg.blk0, sg.n, (int64_t)blockIdx.x);
+  const RmsSeg& g = sg.s[i];
+  const int64_t row = ((int64_t)blockIdx.x - sg.blk0[i]) * 8 + (l & 7);
+  const bool ok = row < g.L;
+  const int64_t bytes = seg_span_bytes(g, C);
+  const auto rs = rowsum::row_rsrc(g.x, bytes);
+  // rows past L start at the range's end: all their loads return 0
+  const int voff = (int)(ok ? (row * g.ld + 4 * (l >> 3)) * 4 : bytes);
+  const float ss = ln_pass_full<2, kLnDepthFull>(rs, voff, (int)(C / 32), l, tb, 0.f);
   if (l < 8 && ok) {
     const float den = ss / (float)C + eps;
     g.inv[row] = 1.f / sqrtf(den);
@@ -112,7 +142,7 @@ hipError_t launch_rmsnorm_rope_segs(const RmsSeg* segs, int nseg, int64_t C, int
     return hipErrorInvalidValue;
   RmsSegs st{};
   st.n = nseg;
-  bool vec = C % 4 == 0, few = true, any_w = false;
+  bool vec = C % 4 == 0, few = true, any_w = false, full = C % 32 == 0;
   for (int i = 0; i < nseg; i++) {
     const RmsSeg& g = segs[i];
     if (g.L < 0 || g.ld < C || g.nr < 0 || g.nr > C / heads / 2 || (!g.w && !g.cs) ||
@@ -124,11 +154,15 @@ hipError_t launch_rmsnorm_rope_segs(const RmsSeg* segs, int nseg, int64_t C, int
     vec = vec && aligned16(g.x) && g.ld % 4 == 0;
     few = few && g.L <= 4096;
     any_w = any_w || (g.w && g.L > 0);
+    full = full && (g.L == 0 || seg_span_bytes(g, C) <= kFullMaxBytes);
   }
+  full = full && vec;
   // segments without a weight (rotation only) own no stats blocks
   if (any_w) {
     const dim3 g((unsigned)st.blk0[nseg]), b(64);
-    if (vec && few)
+    if (full)
+      hipLaunchKernelGGL(rms_stats_full_kernel, g, b, 0, s, st, C, eps);
+    else if (vec && few)
       hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthFew>), g, b, 0, s, st, C, eps);
     else if (vec)
       hipLaunchKernelGGL((rms_stats_kernel<true, kLnDepthMany>), g, b, 0, s, st, C, eps);

@@ -141,9 +141,12 @@ __device__ __forceinline__ void lnmod16(float v[16], int64_t k0, int64_t K, floa
   }
 }
 
+using rowsum::kFullMaxBytes;
 using rowsum::kLnDepthFew;
+using rowsum::kLnDepthFull;
 using rowsum::kLnDepthMany;
 using rowsum::ln_pass;
+using rowsum::ln_pass_full;
 
 // Row statistics of blocks.cpp:18-43 (no affine), bit-exact with the
 // reference build: the mean and the variance are serial float sums in k
@@ -162,6 +165,30 @@ ln_stats_kernel(const float* __restrict__ x, int64_t M, int64_t K, float eps,
   mu = mu / (float)K;
   mu = __shfl(mu, l & 7);  // lanes 0-7 hold the rows' sums; lane l works on row l & 7
   const float var = ln_pass<VEC, 1, D>(r, K, l, tb, mu);
+  if (l < 8 && ok) {
+    const float den = var / (float)K + eps;
+    st[row] = float2{mu, 1.f / sqrtf(den)};
+  }
+}
+
+// The same statistics for K % 32 == 0, 16-byte aligned rows and M*K*4 <=
+// kFullMaxBytes: whole 32-column tiles through a buffer descriptor.
+__global__ void __launch_bounds__(64)
+ln_stats_full_kernel(const float* __restrict__ x, int64_t M, int64_t K, float eps,
+                     float2* __restrict__ st) {
+  __shared__ float4 tb[3][64];
+  const int l = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (l & 7);
+  const bool ok = row < M;
+  const int64_t bytes = M * K * 4;
+  const auto rs = rowsum::row_rsrc(x, bytes);
+  // rows past M start at the range's end: all their loads return 0
+  const int voff = (int)(ok ? (row * K + 4 * (l >> 3)) * 4 : bytes);
+  const int nt = (int)(K / 32);
+  float mu = ln_pass_full<0, kLnDepthFull>(rs, voff, nt, l, tb, 0.f);
+  mu = mu / (float)K;
+  mu = __shfl(mu, l & 7);  // lanes 0-7 hold the rows' sums; lane l works on row l & 7
+  const float var = ln_pass_full<1, kLnDepthFull>(rs, voff, nt, l, tb, mu);
   if (l < 8 && ok) {
     const float den = var / (float)K + eps;
     st[row] = float2{mu, 1.f / sqrtf(den)};
@@ -535,7 +562,9 @@ hipError_t launch_ln_stats(const float* A, int64_t M, int64_t K, float eps, floa
   if (K <= 0 || !st) return hipErrorInvalidValue;
   const bool vx = aligned16(A) && (K % 4) == 0, few = M <= 4096;
   const dim3 g((unsigned)ceil_div(M, 8)), b(64);
-  if (vx && few)
+  if (vx && K % 32 == 0 && M * K * 4 <= kFullMaxBytes)
+    hipLaunchKernelGGL(ln_stats_full_kernel, g, b, 0, s, A, M, K, eps, st);
+  else if (vx && few)
     hipLaunchKernelGGL((ln_stats_kernel<true, kLnDepthFew>), g, b, 0, s, A, M, K, eps, st);
   else if (vx)
     hipLaunchKernelGGL((ln_stats_kernel<true, kLnDepthMany>), g, b, 0, s, A, M, K, eps, st);

@@ -135,5 +135,86 @@ __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K,
 }
 
 
+// Full tiles (K % 32 == 0, 16-byte aligned rows) through a buffer
+// descriptor over the rows (range: the bytes the rows span, below 2^31):
+// lane l loads at voff (its row's byte offset, or the range itself for a
+// row past the end) plus 128 bytes per tile, and loads past the range return
+// 0 without touching memory, so the loop needs no address clamps and no
+// column masks (tiles past the row end are loaded but never summed). Three
+// LDS buffers: iteration t reads tile t+1 (written and waited in iteration
+// t-1), writes tile t+2, adds tile t from registers, then waits, so the LDS
+// latency runs under the adds. D (a multiple of 3) tiles of loads in
+// flight. Same sums, in the same order, as ln_pass.
+typedef float v4f_rs __attribute__((ext_vector_type(4)));
+constexpr int kLnDepthFull = 12;
+// Largest range: voff + (nt + 2D + 2) * 128 stays below 2^31.
+constexpr int64_t kFullMaxBytes = 0x7FFF0000;
+
+template <int PASS, int D>
+__device__ __forceinline__ float ln_pass_full(__amdgpu_buffer_rsrc_t rs, int voff, int nt, int l,
+                                              float4 (&tb)[3][64], float mu) {
+  static_assert(D % 3 == 0, "buffer rotation needs D % 3 == 0");
+  float acc = 0.f;
+  v4f_rs buf[D];
+#pragma unroll
+  for (int u = 0; u < D; u++)
+    buf[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + u * 128, 0, 0);
+  auto prep = [&](v4f_rs v) {
+    float4 o = {v.x, v.y, v.z, v.w};
+    if constexpr (PASS != 0) {
+      o.x = ln_term<PASS>(o.x, mu);
+      o.y = ln_term<PASS>(o.y, mu);
+      o.z = ln_term<PASS>(o.z, mu);
+      o.w = ln_term<PASS>(o.w, mu);
+    }
+    return o;
+  };
+  tb[0][l] = prep(buf[0]);
+  tb[1][l] = prep(buf[1]);
+  buf[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + D * 128, 0, 0);
+  buf[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (D + 1) * 128, 0, 0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  float4 w[8];
+  if (l < 8) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) w[q] = tb[0][q * 8 + l];
+  }
+  for (int t0 = 0; t0 < nt; t0 += D) {
+    const int vt = voff + t0 * 128;
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+      float4 wn[8];
+      if (l < 8) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) wn[q] = tb[(u + 1) % 3][q * 8 + l];
+      }
+      tb[(u + 2) % 3][l] = prep(buf[(u + 2) % D]);
+      buf[(u + 2) % D] = __builtin_amdgcn_raw_buffer_load_b128(rs, vt + (u + 2 + D) * 128, 0, 0);
+      if (l < 8 && t0 + u < nt) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          acc = acc + w[q].x;
+          acc = acc + w[q].y;
+          acc = acc + w[q].z;
+          acc = acc + w[q].w;
+        }
+      }
+      // one wave per workgroup: waiting for its own LDS operations suffices
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int q = 0; q < 8; q++) w[q] = wn[q];
+    }
+  }
+  return acc;
+}
+
+// Raw descriptor (stride 0) over `bytes` bytes from p; the last dword sets
+// DATA_FORMAT to 32 bits (a zero format would make every load return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+
 }  // namespace rowsum
 }  // namespace sdq

@@ -199,6 +199,51 @@ def test_layernorm_bitexact(sdq_dev, oracle, M, K, affine):
     assert_bitexact(xd.cpu().numpy(), want, "layernorm in place")
 
 
+@pytest.mark.parametrize("M,nt", [(1, 1), (9, 2), (13, 11), (8, 12), (15, 13), (17, 25), (5, 96)])
+def test_row_stats_tile_counts(sdq_dev, oracle, M, nt):
+    """The row sums of whole 32-column tiles (K = 32*nt, aligned rows) at tile
+    counts below, at and past the loads kept in flight, rows past M in the
+    last group of 8, and a row whose last tile ends the allocation: layernorm
+    and rmsnorm (rows of stride ld = C + 32, the weight-less rest of the row
+    never read) bit-exact against the oracle; the same rows at an unaligned
+    start (the per-column path) give the same bits."""
+    import torch
+
+    import sdq
+
+    K = 32 * nt
+    print(f"[row stats] M={M} K={K}", flush=True)
+    rng = np.random.default_rng(nt * 7 + M)
+    x = (oracle.randn(M * K, 90 + nt).reshape(M, K) * rng.uniform(0.1, 20, (M, 1))
+         + rng.uniform(-9, 9, (M, 1))).astype(np.float32)
+    x[0, 0] = np.float32(-0.0)
+    want = oracle.layernorm(x, 1e-6, None, None)
+    xd = torch.from_numpy(x).to(sdq_dev)
+    y = torch.full_like(xd, float("nan"))
+    sdq.layernorm(xd, y, None, None, 1e-6)
+    # the same rows one float into a larger buffer: not 16-byte aligned
+    big = torch.zeros(M * K + 1, device=sdq_dev)
+    big[1:].copy_(xd.reshape(-1))
+    xu = big[1:].view(M, K)
+    yu = torch.full_like(xd, float("nan"))
+    sdq.layernorm(xu, yu, None, None, 1e-6)
+    torch.cuda.synchronize()
+    assert_bitexact(y.cpu().numpy(), want, "layernorm, whole tiles")
+    assert_bitexact(yu.cpu().numpy(), want, "layernorm, unaligned rows")
+
+    heads = 1 if nt < 4 else nt // 2 if nt % 2 == 0 else nt
+    C, ld = K, K + 32
+    w = oracle.randn(C, 91)
+    rows = np.zeros((M, ld), np.float32)
+    rows[:, 32:] = x  # the normalised block ends each row (and the last one the buffer)
+    d = torch.from_numpy(rows).to(sdq_dev)
+    sdq.rmsnorm_rope(d, C, torch.from_numpy(w).to(sdq_dev), heads, None, col0=32)
+    torch.cuda.synchronize()
+    got = d.cpu().numpy()
+    assert_bitexact(got[:, 32:], oracle.rmsnorm(x, w, 1e-6), "rmsnorm, whole tiles")
+    assert_bitexact(got[:, :32], rows[:, :32], "columns before the block untouched")
+
+
 def test_rope_only_and_add(sdq_dev, oracle):
     """The fusion attention's late rotation of q (no rmsnorm, w = NULL) and
     the x += y of its two attention outputs, bit-exact."""
