@@ -710,7 +710,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int64_t ybase = (((int64_t)ksp * Mq + (int64_t)tm * BM) * Nq + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<char*>(Yq) + ybase, (short)0, kBigRange, kRsrcWord3);
-    const bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
+    constexpr bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         has_x ? const_cast<float*>(rq) + (ybase >> 2) : static_cast<float*>(Yq), (short)0,
         has_x ? kBigRange : 0, kRsrcWord3);
@@ -736,6 +736,22 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       const float4 s4 = *reinterpret_cast<const float4*>(&colb[par][0][cl]);
       const float4 b4 = *reinterpret_cast<const float4*>(&colb[par][1][cl]);
       const float4 g4 = *reinterpret_cast<const float4*>(&colb[par][2][cl]);
+      // The residual of this column chunk's rows, all loads issued before
+      // the first use: one memory latency per chunk column instead of one
+      // per store. Each lane reads only the elements it writes afterwards,
+      // so this is safe when the residual is Y itself.
+      v4f xa[has_x ? FM : 1][4];
+      if constexpr (has_x) {
+#pragma unroll
+        for (int b = 0; b < FM; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int rl = b * 32 + 8 * i;
+            const bool ok = n_ok && (mrow0 + rl < M32);
+            xa[b][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                xr, ok ? vlane + rl * ldyq + a * 128 : kOutOfRange, 0, 0);
+          }
+      }
 #pragma unroll
       for (int b = 0; b < FM; b++) {
         const v16i& c = acc[a][b];
@@ -783,18 +799,19 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
                 rm[b][i] = rm[b][i] < av ? av : rm[b][i];
               }
             } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
-              const v4f x = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, 0, 0);
+              const v4f x = xa[b][i];
               if constexpr (EPI == SDQ_EPI_RESID) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
-              } else if (epi.gate_fma) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) v[r] = __builtin_fmaf(v[r], gv[r], x[r]);
               } else {
+                // both forms, then a select on the uniform flag: no branch
+                // between the loads and their uses
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
+                  const float f = __builtin_fmaf(v[r], gv[r], x[r]);
                   const float p = v[r] * gv[r];
-                  v[r] = x[r] + p;
+                  const float q = x[r] + p;
+                  v[r] = epi.gate_fma ? f : q;
                 }
               }
             }
