@@ -330,6 +330,13 @@ int sdq_device_free(void* p);
 /* Stream-ordered copy; `kind` is SDQ_H2D / SDQ_D2H / SDQ_D2D. */
 int sdq_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
 int sdq_stream_sync(void* stream);
+/* Work enqueued on `waiter` after this call starts only after the work
+ * enqueued on `signaler` before it has finished (an event recorded on
+ * signaler, waited on by waiter; the host does not block). The same stream
+ * twice: nothing to do. No counterpart in the reference (one CPU thread pool,
+ * no streams): the twin-layer pair forward forks the two branches' FFNs onto
+ * two streams and joins them with it. */
+int sdq_stream_wait(void* waiter, void* signaler);
 
 /* ---- per-kernel timing -------------------------------------------------
  * Between sdq_profile_begin() and sdq_profile_end(), every kernel this

@@ -1351,6 +1351,20 @@ int sdq_stream_sync(void* stream) {
   return SDQ_OK;
 }
 
+int sdq_stream_wait(void* waiter, void* signaler) {
+  if (waiter == signaler) return SDQ_OK;
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return hip_error(e, "hipEventCreateWithFlags");
+  e = hipEventRecord(ev, static_cast<hipStream_t>(signaler));
+  if (e == hipSuccess) e = hipStreamWaitEvent(static_cast<hipStream_t>(waiter), ev, 0);
+  // destroying a pending event is allowed: its resources go when it completes
+  const hipError_t d = hipEventDestroy(ev);
+  if (e != hipSuccess) return hip_error(e, "stream wait");
+  if (d != hipSuccess) return hip_error(d, "hipEventDestroy");
+  return SDQ_OK;
+}
+
 int sdq_profile_begin(void) {
   t_prof = true;
   return SDQ_OK;

@@ -183,8 +183,39 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   ffn_linears(io, s);
 }
 
+// Whether the two blocks' FFNs may run at the same time: neither writes
+// (hid, x) what the other reads (h_ffn, x, gate, shift, scale) or writes.
+namespace {
+
+bool ffns_independent(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
+                      const sd_dit_block_io& ib) {
+  struct Span {
+    const void* p;
+    size_t n;
+  };
+  auto rows = [](const sd_dit_block_io& io, int64_t w) { return (size_t)(io.M * w) * sizeof(float); };
+  auto writes = [&](const DitBlock& k, const sd_dit_block_io& io) {
+    return std::vector<Span>{{io.hid, rows(io, k.ffn_dim())}, {io.x, rows(io, k.dim())}};
+  };
+  auto touches = [&](const DitBlock& k, const sd_dit_block_io& io) {
+    const size_t v = (size_t)k.dim() * sizeof(float);
+    return std::vector<Span>{{io.hid, rows(io, k.ffn_dim())}, {io.x, rows(io, k.dim())},
+                             {io.h_ffn, rows(io, k.dim())}, {io.gate_ffn, v},
+                             {io.shift_ffn, v},           {io.scale_ffn, v}};
+  };
+  for (const Span& w : writes(a, ia))
+    for (const Span& t : touches(b, ib))
+      if (overlap(w.p, w.n, t.p, t.n)) return false;
+  for (const Span& w : writes(b, ib))
+    for (const Span& t : touches(a, ia))
+      if (overlap(w.p, w.n, t.p, t.n)) return false;
+  return true;
+}
+
+}  // namespace
+
 void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
-                          const sd_dit_block_io& ib, void* s) {
+                          const sd_dit_block_io& ib, void* s, void* s2) {
   a.check_io(ia);
   b.check_io(ib);
   if (ia.shift_sa && ia.scale_sa) a.qkv_lnmod(ia, s);
@@ -196,8 +227,16 @@ void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const Di
   run_linears({{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x},
                {&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}},
               s);
-  a.ffn_linears(ia, s);
-  b.ffn_linears(ib, s);
+  if (s2 && s2 != s && ffns_independent(a, ia, b, ib)) {
+    // neither FFN touches what the other reads or writes: fork b's onto s2
+    check(sdq_stream_wait(s2, s), "pair fork");
+    a.ffn_linears(ia, s);
+    b.ffn_linears(ib, s2);
+    check(sdq_stream_wait(s, s2), "pair join");
+  } else {
+    a.ffn_linears(ia, s);
+    b.ffn_linears(ib, s);
+  }
 }
 
 void DitBlock::set_norms(const sd_dit_norms& n) {
@@ -680,6 +719,17 @@ int sd_dit_block_forward_pair(const sd_dit_block* a, const sd_dit_block_io* ia,
     return SDQ_ERR_INVALID;
   }
   return guarded([&] { sd::gpu::forward_linears_pair(a->blk, *ia, b->blk, *ib, stream); });
+}
+
+int sd_dit_block_forward_pair2(const sd_dit_block* a, const sd_dit_block_io* ia,
+                               const sd_dit_block* b, const sd_dit_block_io* ib, void* stream,
+                               void* stream2) {
+  if (!a || !ia || !b || !ib) {
+    t_dit_err = "sd_dit_block_forward_pair2: null argument";
+    return SDQ_ERR_INVALID;
+  }
+  return guarded(
+      [&] { sd::gpu::forward_linears_pair(a->blk, *ia, b->blk, *ib, stream, stream2); });
 }
 
 int sd_dit_block_free(sd_dit_block* b) {

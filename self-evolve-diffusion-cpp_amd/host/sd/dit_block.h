@@ -127,6 +127,13 @@ int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void*
 // grouped launch (sdq_qlinear_group) when no output overlaps another input.
 int sd_dit_block_forward_pair(const sd_dit_block* a, const sd_dit_block_io* ia,
                               const sd_dit_block* b, const sd_dit_block_io* ib, void* stream);
+// The same with b's FFN (fc1 then fc2) on stream2, forked from `stream`
+// after the grouped launches and joined back into it (sdq_stream_wait), so
+// the two FFNs run side by side; stream2 NULL or equal to stream: as
+// sd_dit_block_forward_pair. Same results.
+int sd_dit_block_forward_pair2(const sd_dit_block* a, const sd_dit_block_io* ia,
+                               const sd_dit_block* b, const sd_dit_block_io* ib, void* stream,
+                               void* stream2);
 int sd_dit_block_free(sd_dit_block* b);
 // Copies the block's norm vectors to the device (required before
 // sd_dit_block_step_forward; the fusion ones for fusion blocks, ln3 for others).
@@ -199,7 +206,8 @@ class DitBlock {
   // Runs the linear stack, stream-ordered (throws std::runtime_error).
   void forward_linears(const sd_dit_block_io& io, void* stream) const;
   friend void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia,
-                                   const DitBlock& b, const sd_dit_block_io& ib, void* stream);
+                                   const DitBlock& b, const sd_dit_block_io& ib, void* stream,
+                                   void* stream2);
   double ops(int64_t M, int64_t Mc, int64_t Mt) const;
   // The whole block (norms, RoPE, attention and Linears) on device arrays.
   void set_norms(const sd_dit_norms& n);
@@ -234,9 +242,10 @@ class DitBlock {
 };
 
 // Both blocks' forward_linears (independent inputs), their attention Linears
-// and cross-attention output projections grouped (sd_dit_block_forward_pair).
+// and cross-attention output projections grouped (sd_dit_block_forward_pair);
+// with stream2 (not stream), b's FFN runs there, forked and joined.
 void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
-                          const sd_dit_block_io& ib, void* stream);
+                          const sd_dit_block_io& ib, void* stream, void* stream2 = nullptr);
 
 // Block `layer` of a backbone in a load_sdcpp map, with the names and checks
 // of OviDit::load_impl (ovi_dit.cpp:505-530): "<prefix>blocks.<layer>.

@@ -102,6 +102,7 @@ SIGNATURES = {
     "sdq_device_free": (ctypes.c_int, [_vp]),
     "sdq_memcpy": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
     "sdq_stream_sync": (ctypes.c_int, [_vp]),
+    "sdq_stream_wait": (ctypes.c_int, [_vp, _vp]),
     "sdq_profile_begin": (ctypes.c_int, []),
     "sdq_profile_end": (ctypes.c_int, [ctypes.POINTER(KernelTime), ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_int)]),
@@ -662,6 +663,12 @@ def sync():
     _check(_lib.sdq_sync())
 
 
+def stream_wait(waiter=None, signaler=None):
+    """sdq_stream_wait: work enqueued on `waiter` from now on starts after the
+    work already enqueued on `signaler` (torch streams, raw handles or None)."""
+    _check(load_library().sdq_stream_wait(_stream(waiter), _stream(signaler)))
+
+
 # ---- the DiT block linear stack (C++ host mirror, lib/libsd_host.so) ----
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libsd_host.so")
 _host = None
@@ -751,6 +758,10 @@ def load_host_library(path: str = HOST_LIB_PATH):
     h.sd_dit_block_forward_pair.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO),
                                             ctypes.c_void_p, ctypes.POINTER(BlockIO),
                                             ctypes.c_void_p]
+    h.sd_dit_block_forward_pair2.restype = ctypes.c_int
+    h.sd_dit_block_forward_pair2.argtypes = [ctypes.c_void_p, ctypes.POINTER(BlockIO),
+                                             ctypes.c_void_p, ctypes.POINTER(BlockIO),
+                                             ctypes.c_void_p, ctypes.c_void_p]
     h.sd_dit_block_set_norms.restype = ctypes.c_int
     h.sd_dit_block_set_norms.argtypes = [ctypes.c_void_p, ctypes.POINTER(DitNorms)]
     h.sd_dit_block_workspace_bytes.restype = ctypes.c_size_t
@@ -921,15 +932,22 @@ class DitBlock:
         c.done()
         _hcheck(_host.sd_dit_block_forward(self.h, ctypes.byref(b), _stream(stream)))
 
-    def forward_pair(self, other, io, io_other, stream=None):
+    def forward_pair(self, other, io, io_other, stream=None, stream2=None):
         """forward(**io) on this block and forward(**io_other) on `other` (two
         blocks with independent inputs, e.g. the video and audio blocks of a
-        twin layer), their attention Linears grouped (sd_dit_block_forward_pair)."""
+        twin layer), their attention Linears grouped (sd_dit_block_forward_pair);
+        with stream2, other's FFN runs there beside this block's
+        (sd_dit_block_forward_pair2, forked from and joined into stream)."""
         c = _Args()
         a, b = self._block_io(c, io), other._block_io(c, io_other)
         c.done()
-        _hcheck(_host.sd_dit_block_forward_pair(self.h, ctypes.byref(a), other.h, ctypes.byref(b),
-                                                _stream(stream)))
+        if stream2 is None:
+            _hcheck(_host.sd_dit_block_forward_pair(self.h, ctypes.byref(a), other.h,
+                                                    ctypes.byref(b), _stream(stream)))
+        else:
+            _hcheck(_host.sd_dit_block_forward_pair2(self.h, ctypes.byref(a), other.h,
+                                                     ctypes.byref(b), _stream(stream),
+                                                     _stream(stream2)))
 
     def ops(self, M, Mc=0, Mt=0) -> float:
         return _host.sd_dit_block_ops(self.h, M, Mc, Mt)

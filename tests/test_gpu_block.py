@@ -251,16 +251,18 @@ def _outs(torch, dev, M, Mc, Mt, dim, ffn):
                 hid=torch.empty((M, ffn), device=dev))
 
 
+@pytest.mark.parametrize("streams", [1, 2])
 @pytest.mark.parametrize("dim,ffn,Mv,Ma,Mc", [(512, 1408, 300, 90, 77), (3072, 14336, 768, 157, 512)])
-def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc):
+def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc, streams):
     """forward_pair: the video and audio blocks of one twin layer with their
     attention Linears (and the two cross-o projections) grouped; every output
-    of both blocks against the oracle."""
+    of both blocks against the oracle. streams=2: the audio block's FFN on a
+    second stream beside the video block's (forward_pair2)."""
     import torch
 
     import sdq
 
-    print(f"[block-pair] dim={dim} Mv={Mv} Ma={Ma} Mc={Mc}", flush=True)
+    print(f"[block-pair] dim={dim} Mv={Mv} Ma={Ma} Mc={Mc} streams={streams}", flush=True)
     lv, la = _weights(oracle, dim, ffn, 900, True), _weights(oracle, dim, ffn, 950, True)
     iv, ia = _inputs(oracle, Mv, Mc, Ma, dim, 300), _inputs(oracle, Ma, Mc, Mv, dim, 400)
     bv, ba = sdq.DitBlock(lv, True), sdq.DitBlock(la, True)
@@ -268,12 +270,43 @@ def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc):
                      for k, v in inp.items()}
     dv, da = t(iv), t(ia)
     ov, oa = _outs(torch, sdq_dev, Mv, Mc, Ma, dim, ffn), _outs(torch, sdq_dev, Ma, Mc, Mv, dim, ffn)
-    bv.forward_pair(ba, dict(M=Mv, Mc=Mc, Mt=Ma, **dv, **ov), dict(M=Ma, Mc=Mc, Mt=Mv, **da, **oa))
+    bv.forward_pair(ba, dict(M=Mv, Mc=Mc, Mt=Ma, **dv, **ov), dict(M=Ma, Mc=Mc, Mt=Mv, **da, **oa),
+                    stream2=torch.cuda.Stream() if streams == 2 else None)
     torch.cuda.synchronize()
     for got_o, d, lin, inp, Mt in ((ov, dv, lv, iv, Ma), (oa, da, la, ia, Mv)):
         got = {k: v.cpu().numpy() for k, v in got_o.items()}
         got["x"] = d["x"].cpu().numpy()
         _check_small(oracle, got, lin, inp, True, Mt)
+    bv.free()
+    ba.free()
+
+
+def test_block_pair_shared_hidden_buffer_stays_in_order(sdq_dev, oracle):
+    """forward_pair with a second stream but one hidden-state buffer shared by
+    both blocks: the FFNs may not run side by side, so they run in order on
+    the first stream; x of both blocks equals the separate-buffer results."""
+    import torch
+
+    import sdq
+
+    dim, ffn, Mv, Ma, Mc = 512, 1408, 200, 90, 64
+    lv, la = _weights(oracle, dim, ffn, 1400, True), _weights(oracle, dim, ffn, 1450, True)
+    iv, ia = _inputs(oracle, Mv, Mc, Ma, dim, 1500), _inputs(oracle, Ma, Mc, Mv, dim, 1600)
+    bv, ba = sdq.DitBlock(lv, True), sdq.DitBlock(la, True)
+    t = lambda inp: {k: torch.from_numpy(np.ascontiguousarray(v)).to(sdq_dev)  # noqa: E731
+                     for k, v in inp.items()}
+    xs = []
+    for shared in (False, True):
+        dv, da = t(iv), t(ia)
+        ov, oa = _outs(torch, sdq_dev, Mv, Mc, Ma, dim, ffn), _outs(torch, sdq_dev, Ma, Mc, Mv, dim, ffn)
+        if shared:
+            oa["hid"] = ov["hid"][:Ma]  # the first Ma rows of the video block's buffer
+        bv.forward_pair(ba, dict(M=Mv, Mc=Mc, Mt=Ma, **dv, **ov),
+                        dict(M=Ma, Mc=Mc, Mt=Mv, **da, **oa), stream2=torch.cuda.Stream())
+        torch.cuda.synchronize()
+        xs.append((dv["x"].cpu().numpy(), da["x"].cpu().numpy()))
+    assert_bitexact(xs[1][0], xs[0][0], "video x, shared hid")
+    assert_bitexact(xs[1][1], xs[0][1], "audio x, shared hid")
     bv.free()
     ba.free()
 
