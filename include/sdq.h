@@ -156,10 +156,10 @@ int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const
                 void* Y, void* stream);
 
 /* Several independent Linears at once: the same results, bit for bit, as one
- * sdq_qlinear per item, with fewer and fuller launches. Items that share K,
- * epilogue kind, bias / gate presence and run on the 128x128 tile path (the
- * medium and small row counts of the DiT's Linears) are quantized by one
- * launch and multiplied by one persistent launch that walks all their tiles;
+ * sdq_qlinear per item, with fewer and fuller launches. Items that share K
+ * and run on the 128x128 tile path (the medium and small row counts of the
+ * DiT's Linears) are quantized by one launch and multiplied by one
+ * persistent launch that walks all their tiles, each with its own epilogue;
  * other items run as separate sdq_qlinear calls. For the Linears of a block
  * (or of both branches of a twin layer) that read inputs already computed:
  * q|k|v, cross q, the text k|v, the fusion k|v (ovi_dit.cpp:179-181,

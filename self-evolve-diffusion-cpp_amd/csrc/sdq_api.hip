@@ -731,11 +731,10 @@ bool groupable(const sdq_group_item& it, int cu_count) {
   return w->KFp * 1024 * 8 <= 0x7FFFFFFF && N * 4 * 256 <= 0x7FFFFFF0;
 }
 
-// Items that may share one GEMM launch: same k-fragments and epilogue form.
+// Items that may share one GEMM launch: the same k-fragments (the launch
+// reads each problem's epilogue form from its table).
 bool same_group(const sdq_group_item& a, const sdq_group_item& b) {
-  return a.w->KFp == b.w->KFp && a.epi.kind == b.epi.kind &&
-         (a.epi.bias != nullptr) == (b.epi.bias != nullptr) &&
-         (a.epi.gate != nullptr) == (b.epi.gate != nullptr) && a.epi.gate_fma == b.epi.gate_fma;
+  return a.w->KFp == b.w->KFp;
 }
 
 }  // namespace
@@ -1004,7 +1003,8 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
     hipError_t e = launch_act_quant_segs(qs, s);
     if (e != hipSuccess) return hip_error(e, "group act_quant launch");
     hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
-    // one GEMM launch per set of items with the same K and epilogue form
+    // one GEMM launch per set of items with the same K (each problem carries
+    // its own epilogue form)
     std::vector<bool> done(shared.size(), false);
     for (size_t j = 0; j < shared.size(); j++) {
       if (done[j]) continue;
@@ -1025,6 +1025,8 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
         p.Y = it.Y;
         p.M = (int)it.M;
         p.N = (int)it.w->N;
+        p.kind = it.epi.kind;
+        p.gate_fma = it.epi.gate_fma;
       }
       EpiArgs ea = make_epi(&first.epi, first.w->K);
       ea.bias = ea.gate = ea.resid = nullptr;  // per problem, from the table

@@ -411,6 +411,12 @@ __device__ __forceinline__ const float* group_resid(const GemmGroup& g, int p) {
   return g.p[p].resid;
 }
 __device__ __forceinline__ const float* group_resid(const NoGroup&, int) { return nullptr; }
+__device__ __forceinline__ int group_kind(const GemmGroup& g, int p) { return g.p[p].kind; }
+__device__ __forceinline__ int group_kind(const NoGroup&, int) { return 0; }
+__device__ __forceinline__ bool group_fma(const GemmGroup& g, int p) { return g.p[p].gate_fma != 0; }
+__device__ __forceinline__ bool group_fma(const NoGroup&, int) { return true; }
+__device__ __forceinline__ bool group_bias(const GemmGroup& g, int p) { return g.p[p].bias != nullptr; }
+__device__ __forceinline__ bool group_bias(const NoGroup&, int) { return false; }
 
 template <int BN, int BM, int WN, int WM, int KS, int STAGES, int OCC, int EPI, bool BIAS,
           bool SPLITK, bool GROUPED = false>
@@ -420,6 +426,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
               int tiles_m, EpiArgs epi, void* Y, int splits, GroupArg<GROUPED> grp) {
   static_assert(!SPLITK || EPI == SDQ_EPI_ACC, "split-K partials are raw accumulators");
   static_assert(!(GROUPED && SPLITK), "grouped launches do not split K");
+  static_assert(EPI != kEpiMixed || (GROUPED && !BIAS), "mixed epilogues come from a group's table");
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -710,7 +717,17 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     const int64_t ybase = (((int64_t)ksp * Mq + (int64_t)tm * BM) * Nq + (int64_t)tn * BN) * 4;
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<char*>(Yq) + ybase, (short)0, kBigRange, kRsrcWord3);
-    constexpr bool has_x = EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
+    // The tile's epilogue form: the kernel's own, or (mixed groups) its
+    // problem's, uniform over the workgroup. For a fixed form these fold to
+    // constants.
+    constexpr bool kMixed = EPI == kEpiMixed;
+    const int ek = kMixed ? group_kind(grp, pb) : EPI;
+    const bool ebias = kMixed ? group_bias(grp, pb) : BIAS;
+    const bool efma = kMixed ? group_fma(grp, pb) : epi.gate_fma != 0;
+    constexpr bool kMayX = kMixed || EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID;
+    const bool has_x = kMayX && (ek == SDQ_EPI_GATED || ek == SDQ_EPI_RESID);
+    (void)ebias;
+    (void)efma;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         has_x ? const_cast<float*>(rq) + (ybase >> 2) : static_cast<float*>(Yq), (short)0,
         has_x ? kBigRange : 0, kRsrcWord3);
@@ -740,8 +757,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       // the first use: one memory latency per chunk column instead of one
       // per store. Each lane reads only the elements it writes afterwards,
       // so this is safe when the residual is Y itself.
-      v4f xa[has_x ? FM : 1][4];
-      if constexpr (has_x) {
+      v4f xa[kMayX ? FM : 1][4];
+      if (kMayX && has_x) {
 #pragma unroll
         for (int b = 0; b < FM; b++)
 #pragma unroll
@@ -787,31 +804,56 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
               const float af = (float)t4[i][r];
               v[r] = af * sc;  // K > 0 here (the launcher requires it)
             }
-            if constexpr (BIAS) {
+            if constexpr (!kMixed) {
+              if constexpr (BIAS) {
 #pragma unroll
-              for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
-            }
-            if constexpr (EPI == SDQ_EPI_GELU) {
-#pragma unroll
-              for (int r = 0; r < 4; r++) {
-                v[r] = gelu_tanh(v[r]);
-                const float av = ok ? fabsf(v[r]) : 0.f;
-                rm[b][i] = rm[b][i] < av ? av : rm[b][i];
+                for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
               }
-            } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
-              const v4f x = xa[b][i];
-              if constexpr (EPI == SDQ_EPI_RESID) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
-              } else {
-                // both forms, then a select on the uniform flag: no branch
-                // between the loads and their uses
+              if constexpr (EPI == SDQ_EPI_GELU) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                  const float f = __builtin_fmaf(v[r], gv[r], x[r]);
-                  const float p = v[r] * gv[r];
-                  const float q = x[r] + p;
-                  v[r] = epi.gate_fma ? f : q;
+                  v[r] = gelu_tanh(v[r]);
+                  const float av = ok ? fabsf(v[r]) : 0.f;
+                  rm[b][i] = rm[b][i] < av ? av : rm[b][i];
+                }
+              } else if constexpr (EPI == SDQ_EPI_GATED || EPI == SDQ_EPI_RESID) {
+                const v4f x = xa[b][i];
+                if constexpr (EPI == SDQ_EPI_RESID) {
+#pragma unroll
+                  for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
+                } else {
+                  // both forms, then a select on the uniform flag: no branch
+                  // between the loads and their uses
+#pragma unroll
+                  for (int r = 0; r < 4; r++) {
+                    const float f = __builtin_fmaf(v[r], gv[r], x[r]);
+                    const float p = v[r] * gv[r];
+                    const float q = x[r] + p;
+                    v[r] = epi.gate_fma ? f : q;
+                  }
+                }
+              }
+            } else {
+              if (ebias) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = v[r] + bv[r];
+              }
+              if (ek == SDQ_EPI_GELU) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = gelu_tanh(v[r]);
+              } else if (has_x) {
+                const v4f x = xa[b][i];
+                if (ek == SDQ_EPI_RESID) {
+#pragma unroll
+                  for (int r = 0; r < 4; r++) v[r] = x[r] + v[r];
+                } else {
+#pragma unroll
+                  for (int r = 0; r < 4; r++) {
+                    const float f = __builtin_fmaf(v[r], gv[r], x[r]);
+                    const float p = v[r] * gv[r];
+                    const float q = x[r] + p;
+                    v[r] = efma ? f : q;
+                  }
                 }
               }
             }
@@ -1135,12 +1177,17 @@ hipError_t run_persist_group(GemmGroup& g, int64_t KFp, const EpiArgs& epi, floa
       epi.kzero || epi.rmax || !sink)
     return hipErrorInvalidValue;
   int64_t total = 0;
-  const bool bias = g.p[0].bias != nullptr;
+  const GemmProblem& p0 = g.p[0];
+  bool uniform = true;  // one epilogue form for every problem
   for (int i = 0; i < g.count; i++) {
     GemmProblem& p = g.p[i];
-    if (p.M <= 0 || p.N <= 0 || !p.wt || !p.scale || !p.at || !p.as || !p.Y ||
-        (p.bias != nullptr) != bias)
+    const bool kind_ok = p.kind == SDQ_EPI_NONE || p.kind == SDQ_EPI_GELU ||
+                         (p.kind == SDQ_EPI_GATED && p.gate && p.resid) ||
+                         (p.kind == SDQ_EPI_RESID && p.resid);
+    if (p.M <= 0 || p.N <= 0 || !p.wt || !p.scale || !p.at || !p.as || !p.Y || !kind_ok)
       return hipErrorInvalidValue;
+    uniform = uniform && p.kind == p0.kind && (p.bias != nullptr) == (p0.bias != nullptr) &&
+              (p.kind != SDQ_EPI_GATED || p.gate_fma == p0.gate_fma);
     p.tiles_n = (int)ceil_div(p.N, BN);
     p.tiles_m = (int)ceil_div(p.M, BM);
     p.tile0 = (int)total;
@@ -1151,22 +1198,27 @@ hipError_t run_persist_group(GemmGroup& g, int64_t KFp, const EpiArgs& epi, floa
   const int64_t max_groups = 2 * (int64_t)(cu_count > 0 ? cu_count : 256);
   int G = (int)(total < max_groups ? total : max_groups);
   if (G >= 8) G &= ~7;
-  const ColOps cols{g.p[0].scale, g.p[0].bias, g.p[0].gate};
+  const ColOps cols{p0.scale, p0.bias, p0.gate};
+  EpiArgs ea = epi;
+  ea.kind = uniform ? p0.kind : kEpiMixed;
+  ea.gate_fma = p0.gate_fma;
+  const bool bias = p0.bias != nullptr;
 #define SDQ_LAUNCH_GROUP(K, B)                                                                    \
   hipLaunchKernelGGL((qgemm_persist<BN, BM, 2, 2, KS, STAGES, 2, K, B, false, true>),            \
-                     dim3((unsigned)G), dim3(256), 0, s, g.p[0].wt, cols, g.p[0].at, g.p[0].as,   \
-                     (int64_t)g.p[0].M, (int64_t)g.p[0].N, KFp, g.p[0].tiles_n,                  \
-                     g.p[0].tiles_m, epi, static_cast<void*>(sink), 1, g)
+                     dim3((unsigned)G), dim3(256), 0, s, p0.wt, cols, p0.at, p0.as,               \
+                     (int64_t)p0.M, (int64_t)p0.N, KFp, p0.tiles_n, p0.tiles_m, ea,               \
+                     static_cast<void*>(sink), 1, g)
 #define SDQ_LAUNCH_GROUP_B(K)   \
   if (bias)                     \
     SDQ_LAUNCH_GROUP(K, true);  \
   else                          \
     SDQ_LAUNCH_GROUP(K, false)
-  switch (epi.kind) {
+  switch (ea.kind) {
     case SDQ_EPI_NONE: SDQ_LAUNCH_GROUP_B(SDQ_EPI_NONE); break;
     case SDQ_EPI_GELU: SDQ_LAUNCH_GROUP_B(SDQ_EPI_GELU); break;
     case SDQ_EPI_GATED: SDQ_LAUNCH_GROUP_B(SDQ_EPI_GATED); break;
     case SDQ_EPI_RESID: SDQ_LAUNCH_GROUP_B(SDQ_EPI_RESID); break;
+    case kEpiMixed: SDQ_LAUNCH_GROUP(kEpiMixed, false); break;  // bias per problem
     default: return hipErrorInvalidValue;
   }
 #undef SDQ_LAUNCH_GROUP_B

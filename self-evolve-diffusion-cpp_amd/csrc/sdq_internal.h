@@ -221,9 +221,10 @@ struct GemmAux {
   hipEvent_t mid;    // nullable: recorded between those two launches (per-kernel timing)
 };
 // Grouped persistent GEMM: up to kMaxGemmGroup independent problems with
-// the same K (KFp), epilogue kind and bias presence in one launch of the
-// 128x128 persistent kernel, their tiles walked as one list (problem p owns
-// tiles [tile0, tile0 + tiles_n * tiles_m)). Each problem has its own
+// the same K (KFp) in one launch of the 128x128 persistent kernel (each with
+// its own epilogue kind, bias and gate form), their tiles walked as one
+// list (problem p owns tiles [tile0, tile0 + tiles_n * tiles_m)). Each
+// problem has its own
 // weight, quantized activations (at / as, rows padded to 128), padded column
 // operands (scale, bias, gate: as GemmAux / ColOps), residual and output.
 constexpr int kMaxGemmGroup = 16;
@@ -237,7 +238,12 @@ struct GemmProblem {
   const float* resid;
   void* Y;
   int M, N, tiles_n, tiles_m, tile0;
+  int kind;      // the problem's epilogue (SDQ_EPI_NONE / GELU / GATED / RESID)
+  int gate_fma;  // GATED: fma form (else product, then add)
 };
+// A grouped launch whose problems differ in epilogue kind, bias presence or
+// gate form: the kernel reads each tile's form from the problem table.
+constexpr int kEpiMixed = 5;
 struct GemmGroup {
   GemmProblem p[kMaxGemmGroup];
   int count;

@@ -27,8 +27,10 @@ def _items(sdq, torch, oracle, dev, specs, seed0):
         b = oracle.randn(N, sd + 2) if has_bias else None
         g = oracle.randn(N, sd + 3)
         r = oracle.randn(M * N, sd + 4).reshape(M, N)
+        fma = kind != "gated_nofma"
+        kind = "gated" if kind == "gated_nofma" else kind
         it = dict(w=w, A=t(A), out=torch.full((M, N), float("nan"), device=dev), kind=kind,
-                  bias=None if b is None else t(b))
+                  bias=None if b is None else t(b), gate_fma=fma)
         if kind == "gated":
             it.update(gate=t(g), resid=it["out"])
             it["out"].copy_(t(r))
@@ -36,7 +38,7 @@ def _items(sdq, torch, oracle, dev, specs, seed0):
             it.update(resid=it["out"])
             it["out"].copy_(t(r))
         items.append(it)
-        host.append(dict(A=A, q=q, s=s, b=b, g=g, r=r, kind=kind))
+        host.append(dict(A=A, q=q, s=s, b=b, g=g, r=r, kind=kind, fma=fma))
     return items, host
 
 
@@ -46,7 +48,7 @@ def _separate(sdq, torch, items, host):
         y = torch.from_numpy(h["r"]).to(it["out"].device).contiguous() if h["kind"] in (
             "gated", "resid") else torch.empty_like(it["out"])
         sdq.qlinear(it["w"], it["A"], y, kind=h["kind"], bias=it["bias"], gate=it.get("gate"),
-                    resid=y if h["kind"] in ("gated", "resid") else None)
+                    resid=y if h["kind"] in ("gated", "resid") else None, gate_fma=h["fma"])
         outs.append(y)
     torch.cuda.synchronize()
     return [o.cpu().numpy() for o in outs]
@@ -55,13 +57,13 @@ def _separate(sdq, torch, items, host):
 def _oracle(oracle, h):
     kw = dict(bias=h["b"])
     if h["kind"] == "gated":
-        kw.update(epilogue="gated", gate=h["g"], resid=h["r"])
+        kw.update(epilogue="gated", gate=h["g"], resid=h["r"], use_fma=h["fma"])
     elif h["kind"] == "resid":
         kw.update(epilogue="resid", resid=h["r"])
     return oracle.linear(h["A"], h["q"], h["s"], **kw)
 
 
-@pytest.mark.parametrize("case", ["one_set", "mixed"])
+@pytest.mark.parametrize("case", ["one_set", "mixed", "mixed_forms"])
 def test_group_equals_separate_calls(sdq_dev, oracle, case):
     import torch
 
@@ -70,6 +72,12 @@ def test_group_equals_separate_calls(sdq_dev, oracle, case):
     if case == "one_set":
         specs = [(100, 512, 384, "none", True), (157, 512, 256, "none", True),
                  (300, 512, 640, "none", True), (65, 512, 128, "none", True)]
+    elif case == "mixed_forms":
+        # one launch whose problems differ in epilogue kind, bias and gate form
+        # (a block's q|k|v beside its gated output projection)
+        specs = [(768, 1024, 768, "none", True), (768, 1024, 256, "gated", True),
+                 (157, 1024, 256, "gated_nofma", False), (300, 1024, 384, "resid", False),
+                 (129, 1024, 512, "gelu", True), (90, 1024, 128, "none", False)]
     else:
         specs = [(120, 512, 256, "gated", True), (90, 512, 512, "resid", True),
                  (77, 512, 256, "gelu", True), (20, 512, 256, "none", True),   # skinny: alone
