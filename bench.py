@@ -333,8 +333,9 @@ def bench_twin(torch, sdq, args):
             for i in range(layers):
                 blocks[2 * i].forward_pair(blocks[2 * i + 1], iov, ioa)
 
-        # forward_pair with the audio block's FFN on a second stream beside
-        # the video block's (forked after the grouped launches, joined after)
+        # forward_pair on two streams: the video block's own Linears on one,
+        # the audio block's and the video block's text / fusion k|v on the
+        # other (forked and joined inside every layer)
         def fn4():
             for i in range(layers):
                 blocks[2 * i].forward_pair(blocks[2 * i + 1], iov, ioa, stream2=sa)
@@ -349,7 +350,7 @@ def bench_twin(torch, sdq, args):
         lw = wbytes * (2 * layers) / len(blocks)  # bytes of the blocks this pass uses
         res["layers"][str(layers)] = {"ms_per_pass": round(ms, 4), "TOPS": round(ops / ms / 1e9, 2),
                                       "ms_per_pass_grouped_pair": round(ms_grp, 4),
-                                      "ms_per_pass_grouped_pair_ffn_streams": round(ms_grp2, 4),
+                                      "ms_per_pass_pair_two_streams": round(ms_grp2, 4),
                                       "ms_per_pass_two_streams": round(ms_two, 4),
                                       "ms_per_pass_one_stream": round(ms_seq, 4),
                                       "kernel_ms_grouped_pair": (_kernel_split(sdq, fn3, 1)

@@ -183,32 +183,38 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   ffn_linears(io, s);
 }
 
-// Whether the two blocks' FFNs may run at the same time: neither writes
-// (hid, x) what the other reads (h_ffn, x, gate, shift, scale) or writes.
 namespace {
 
-bool ffns_independent(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
-                      const sd_dit_block_io& ib) {
-  struct Span {
-    const void* p;
-    size_t n;
-  };
-  auto rows = [](const sd_dit_block_io& io, int64_t w) { return (size_t)(io.M * w) * sizeof(float); };
-  auto writes = [&](const DitBlock& k, const sd_dit_block_io& io) {
-    return std::vector<Span>{{io.hid, rows(io, k.ffn_dim())}, {io.x, rows(io, k.dim())}};
-  };
-  auto touches = [&](const DitBlock& k, const sd_dit_block_io& io) {
-    const size_t v = (size_t)k.dim() * sizeof(float);
-    return std::vector<Span>{{io.hid, rows(io, k.ffn_dim())}, {io.x, rows(io, k.dim())},
-                             {io.h_ffn, rows(io, k.dim())}, {io.gate_ffn, v},
-                             {io.shift_ffn, v},           {io.scale_ffn, v}};
-  };
-  for (const Span& w : writes(a, ia))
-    for (const Span& t : touches(b, ib))
-      if (overlap(w.p, w.n, t.p, t.n)) return false;
-  for (const Span& w : writes(b, ib))
-    for (const Span& t : touches(a, ia))
-      if (overlap(w.p, w.n, t.p, t.n)) return false;
+// A buffer one stream's work reads or writes (bytes).
+struct Span {
+  const void* p;
+  size_t n;
+  bool write;
+};
+
+// What a block's Linears read and write (forward_linears with io); `own`:
+// q|k|v, o, cross q, cross o and the FFN; else the text k|v and fusion k|v
+// (inputs the caller has from outside the branch: the context and the
+// other branch's tokens).
+std::vector<Span> linear_spans(const DitBlock& k, const sd_dit_block_io& io, bool own) {
+  const size_t d = (size_t)k.dim() * sizeof(float), f = (size_t)k.ffn_dim() * sizeof(float);
+  const size_t M = (size_t)io.M, Mc = (size_t)io.Mc, Mt = (size_t)io.Mt;
+  if (!own)
+    return {{io.ctx, Mc * d, false}, {io.ckv, 2 * Mc * d, true},
+            {io.tn, Mt * d, false},  {io.kvt, 2 * Mt * d, true}};
+  return {{io.h_sa, M * d, false},     {io.att, M * d, false},      {io.xq, M * d, false},
+          {io.xt, M * d, false},       {io.h_ffn, M * d, false},    {io.gate_sa, d, false},
+          {io.gate_ffn, d, false},     {io.shift_sa, d, false},     {io.scale_sa, d, false},
+          {io.shift_ffn, d, false},    {io.scale_ffn, d, false},    {io.qkv, 3 * M * d, true},
+          {io.cq, M * d, true},        {io.hid, M * f, true},       {io.x, M * d, true}};
+}
+
+// Whether two sets of work may run at the same time: neither writes what
+// the other reads or writes.
+bool disjoint(const std::vector<Span>& u, const std::vector<Span>& v) {
+  for (const Span& a : u)
+    for (const Span& b : v)
+      if ((a.write || b.write) && overlap(a.p, a.n, b.p, b.n)) return false;
   return true;
 }
 
@@ -218,6 +224,41 @@ void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const Di
                           const sd_dit_block_io& ib, void* s, void* s2) {
   a.check_io(ia);
   b.check_io(ib);
+  if (s2 && s2 != s) {
+    // Two streams: a's own Linears on s; b's, and a's text k|v and fusion
+    // k|v (which need nothing from a's branch), on s2 (the streams' loads
+    // balance: a is the longer branch). Only when neither side touches what
+    // the other writes.
+    std::vector<Span> on_s = linear_spans(a, ia, true), on_s2 = linear_spans(a, ia, false);
+    for (const Span& x : linear_spans(b, ib, true)) on_s2.push_back(x);
+    for (const Span& x : linear_spans(b, ib, false)) on_s2.push_back(x);
+    if (disjoint(on_s, on_s2)) {
+      check(sdq_stream_wait(s2, s), "pair fork");
+      if (ia.shift_sa && ia.scale_sa) a.qkv_lnmod(ia, s);
+      if (ib.shift_sa && ib.scale_sa) b.qkv_lnmod(ib, s2);
+      std::vector<LinCall> ca, cb, ctx;
+      a.attn_linears(ia, ca);
+      // a's text k|v and fusion k|v move to s2 (they read ctx / tn)
+      for (auto it = ca.begin(); it != ca.end();) {
+        if (it->l == &a.ckv_ || it->l == &a.kvf_) {
+          ctx.push_back(*it);
+          it = ca.erase(it);
+        } else {
+          ++it;
+        }
+      }
+      b.attn_linears(ib, cb);
+      for (const LinCall& c : ctx) cb.push_back(c);
+      run_linears(ca, s);
+      run_linears(cb, s2);
+      run_linears({{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x}}, s);
+      run_linears({{&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}}, s2);
+      a.ffn_linears(ia, s);
+      b.ffn_linears(ib, s2);
+      check(sdq_stream_wait(s, s2), "pair join");
+      return;
+    }
+  }
   if (ia.shift_sa && ia.scale_sa) a.qkv_lnmod(ia, s);
   if (ib.shift_sa && ib.scale_sa) b.qkv_lnmod(ib, s);
   std::vector<LinCall> calls;
@@ -227,16 +268,8 @@ void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const Di
   run_linears({{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x},
                {&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}},
               s);
-  if (s2 && s2 != s && ffns_independent(a, ia, b, ib)) {
-    // neither FFN touches what the other reads or writes: fork b's onto s2
-    check(sdq_stream_wait(s2, s), "pair fork");
-    a.ffn_linears(ia, s);
-    b.ffn_linears(ib, s2);
-    check(sdq_stream_wait(s, s2), "pair join");
-  } else {
-    a.ffn_linears(ia, s);
-    b.ffn_linears(ib, s);
-  }
+  a.ffn_linears(ia, s);
+  b.ffn_linears(ib, s);
 }
 
 void DitBlock::set_norms(const sd_dit_norms& n) {

@@ -127,10 +127,11 @@ int sd_dit_block_forward(const sd_dit_block* b, const sd_dit_block_io* io, void*
 // grouped launch (sdq_qlinear_group) when no output overlaps another input.
 int sd_dit_block_forward_pair(const sd_dit_block* a, const sd_dit_block_io* ia,
                               const sd_dit_block* b, const sd_dit_block_io* ib, void* stream);
-// The same with b's FFN (fc1 then fc2) on stream2, forked from `stream`
-// after the grouped launches and joined back into it (sdq_stream_wait), so
-// the two FFNs run side by side; stream2 NULL or equal to stream: as
-// sd_dit_block_forward_pair. Same results.
+// The same on two streams, forked from `stream` and joined back into it
+// (sdq_stream_wait): a's own Linears on `stream`; b's, and a's text k|v and
+// fusion k|v, on stream2 (a balanced split when a is the longer branch).
+// When the two sides would touch each other's outputs, or stream2 is NULL
+// or equal to stream: as sd_dit_block_forward_pair. Same results.
 int sd_dit_block_forward_pair2(const sd_dit_block* a, const sd_dit_block_io* ia,
                                const sd_dit_block* b, const sd_dit_block_io* ib, void* stream,
                                void* stream2);
@@ -243,7 +244,8 @@ class DitBlock {
 
 // Both blocks' forward_linears (independent inputs), their attention Linears
 // and cross-attention output projections grouped (sd_dit_block_forward_pair);
-// with stream2 (not stream), b's FFN runs there, forked and joined.
+// with stream2 (not stream), b's Linears and a's text / fusion k|v run
+// there, forked and joined (sd_dit_block_forward_pair2).
 void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const DitBlock& b,
                           const sd_dit_block_io& ib, void* stream, void* stream2 = nullptr);
 

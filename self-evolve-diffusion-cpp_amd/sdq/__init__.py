@@ -936,8 +936,9 @@ class DitBlock:
         """forward(**io) on this block and forward(**io_other) on `other` (two
         blocks with independent inputs, e.g. the video and audio blocks of a
         twin layer), their attention Linears grouped (sd_dit_block_forward_pair);
-        with stream2, other's FFN runs there beside this block's
-        (sd_dit_block_forward_pair2, forked from and joined into stream)."""
+        with stream2, `other`'s Linears and this block's text / fusion k|v run
+        there beside this block's own (sd_dit_block_forward_pair2, forked from
+        and joined into stream)."""
         c = _Args()
         a, b = self._block_io(c, io), other._block_io(c, io_other)
         c.done()

@@ -256,8 +256,9 @@ def _outs(torch, dev, M, Mc, Mt, dim, ffn):
 def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc, streams):
     """forward_pair: the video and audio blocks of one twin layer with their
     attention Linears (and the two cross-o projections) grouped; every output
-    of both blocks against the oracle. streams=2: the audio block's FFN on a
-    second stream beside the video block's (forward_pair2)."""
+    of both blocks against the oracle. streams=2: the pair split over two
+    streams (forward_pair2): the video block's own Linears on one, the audio
+    block's and the video block's text / fusion k|v on the other."""
     import torch
 
     import sdq
@@ -283,8 +284,9 @@ def test_block_pair_equals_oracle(sdq_dev, oracle, dim, ffn, Mv, Ma, Mc, streams
 
 def test_block_pair_shared_hidden_buffer_stays_in_order(sdq_dev, oracle):
     """forward_pair with a second stream but one hidden-state buffer shared by
-    both blocks: the FFNs may not run side by side, so they run in order on
-    the first stream; x of both blocks equals the separate-buffer results."""
+    both blocks: the two sides may not run side by side, so the pair runs in
+    order on the first stream; x of both blocks equals the separate-buffer
+    results."""
     import torch
 
     import sdq
