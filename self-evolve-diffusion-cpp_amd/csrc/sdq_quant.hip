@@ -185,9 +185,8 @@ ln_stats_full_kernel(const float* __restrict__ x, int64_t M, int64_t K, float ep
   // rows past M start at the range's end: all their loads return 0
   const int voff = (int)(ok ? (row * K + 4 * (l >> 3)) * 4 : bytes);
   const int nt = (int)(K / 32);
-  float mu = ln_pass_full<0, kLnDepthFull>(rs, voff, nt, l, tb, 0.f);
-  mu = mu / (float)K;
-  mu = __shfl(mu, l & 7);  // lanes 0-7 hold the rows' sums; lane l works on row l & 7
+  // every lane holds the sum of its row (l & 7)
+  const float mu = ln_pass_full<0, kLnDepthFull>(rs, voff, nt, l, tb, 0.f) / (float)K;
   const float var = ln_pass_full<1, kLnDepthFull>(rs, voff, nt, l, tb, mu);
   if (l < 8 && ok) {
     const float den = var / (float)K + eps;

@@ -143,8 +143,9 @@ __device__ __forceinline__ float ln_pass(const float* __restrict__ r, int64_t K,
 // column masks (tiles past the row end are loaded but never summed). Three
 // LDS buffers: iteration t reads tile t+1 (written and waited in iteration
 // t-1), writes tile t+2, adds tile t from registers, then waits, so the LDS
-// latency runs under the adds. D (a multiple of 3) tiles of loads in
-// flight. Same sums, in the same order, as ln_pass.
+// latency runs under the adds. D (a multiple of 6) tiles of loads in
+// flight. Same sums, in the same order, as ln_pass; every lane returns the
+// sum of its row (l & 7).
 typedef float v4f_rs __attribute__((ext_vector_type(4)));
 constexpr int kLnDepthFull = 12;
 // Largest range: voff + (nt + 2D + 2) * 128 stays below 2^31.
@@ -153,7 +154,7 @@ constexpr int64_t kFullMaxBytes = 0x7FFF0000;
 template <int PASS, int D>
 __device__ __forceinline__ float ln_pass_full(__amdgpu_buffer_rsrc_t rs, int voff, int nt, int l,
                                               float4 (&tb)[3][64], float mu) {
-  static_assert(D % 3 == 0, "buffer rotation needs D % 3 == 0");
+  static_assert(D % 6 == 0, "LDS buffers rotate by 3, register sets by 2");
   float acc = 0.f;
   v4f_rs buf[D];
 #pragma unroll
@@ -174,35 +175,33 @@ __device__ __forceinline__ float ln_pass_full(__amdgpu_buffer_rsrc_t rs, int vof
   buf[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + D * 128, 0, 0);
   buf[1] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (D + 1) * 128, 0, 0);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  float4 w[8];
-  if (l < 8) {
+  // Every lane adds the terms of its row (l & 7): the 8 lanes of a row read
+  // the same LDS words (a broadcast) and run the same chain, so no lane
+  // masks; the tile being added and the one being read alternate between
+  // two register sets by tile parity (D is even), so nothing is copied.
+  const int lr = l & 7;
+  float4 w[2][8];
 #pragma unroll
-    for (int q = 0; q < 8; q++) w[q] = tb[0][q * 8 + l];
-  }
+  for (int q = 0; q < 8; q++) w[0][q] = tb[0][q * 8 + lr];
   for (int t0 = 0; t0 < nt; t0 += D) {
     const int vt = voff + t0 * 128;
 #pragma unroll
     for (int u = 0; u < D; u++) {
-      float4 wn[8];
-      if (l < 8) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) wn[q] = tb[(u + 1) % 3][q * 8 + l];
-      }
+      for (int q = 0; q < 8; q++) w[(u + 1) & 1][q] = tb[(u + 1) % 3][q * 8 + lr];
       tb[(u + 2) % 3][l] = prep(buf[(u + 2) % D]);
       buf[(u + 2) % D] = __builtin_amdgcn_raw_buffer_load_b128(rs, vt + (u + 2 + D) * 128, 0, 0);
-      if (l < 8 && t0 + u < nt) {
+      if (t0 + u < nt) {
 #pragma unroll
         for (int q = 0; q < 8; q++) {
-          acc = acc + w[q].x;
-          acc = acc + w[q].y;
-          acc = acc + w[q].z;
-          acc = acc + w[q].w;
+          acc = acc + w[u & 1][q].x;
+          acc = acc + w[u & 1][q].y;
+          acc = acc + w[u & 1][q].z;
+          acc = acc + w[u & 1][q].w;
         }
       }
       // one wave per workgroup: waiting for its own LDS operations suffices
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int q = 0; q < 8; q++) w[q] = wn[q];
     }
   }
   return acc;
