@@ -14,7 +14,9 @@
 // result C^T[n][m] of v_mfma_i32_32x32x32_i8 lands as groups of 4
 // consecutive n of one m per lane: lane l, accumulator register r holds
 // m = l & 31, n = 8(r >> 2) + 4(l >> 5) + (r & 3), i.e. four 16-byte
-// row-contiguous stores of Y[m, n..n+3] per 32x32 block.
+// row-contiguous stores of Y[m, n..n+3] per 32x32 block. The persistent
+// kernels read the same fragments as v_mfma_i32_16x16x64_i8 operands (same
+// roles; their result layout is described at qgemm_persist).
 #include "sdq_internal.h"
 #include "sdq_device.h"
 
@@ -376,13 +378,21 @@ qgemm_tiled(const int8_t* __restrict__ wt, const float* __restrict__ bs,
 // compute, so the epilogue of one tile overlaps the loads of the next.
 //
 // A pipeline stage holds two k-fragments (64 bytes of K) of the tile's
-// weight and activation panels. Each step (one stage) runs in two halves:
-//   half 0: the 8 MFMAs of k-fragment 0 from registers, interleaved with
-//           the LDS reads of k-fragment 1 of the same stage;
+// weight and activation panels: one k-step of v_mfma_i32_16x16x64_i8,
+// whose operands are read straight out of the fragment layout (the lane
+// mapping is at `off16` below). Each step (one stage) runs in two halves:
+//   half 0: the MFMAs of the wave's first half of weight rows against all
+//           its activation columns, interleaved with the LDS reads of the
+//           second half's weight operands;
 //   wait until this wave's loads of the next stage have landed, barrier;
-//   half 1: the 8 MFMAs of k-fragment 1, interleaved with the LDS-DMA of
-//           the stage STAGES ahead (into the buffer this stage used) and
-//           the LDS reads of the next stage's k-fragment 0.
+//   half 1: the MFMAs of the second half of weight rows, interleaved with
+//           the LDS-DMA of the stage STAGES ahead (into the buffer this
+//           stage used) and the LDS reads of the next stage's first-half
+//           weight operands and activation operands.
+// The 16x16x64 form moves the same LDS bytes and holds the same
+// accumulator registers per k as 32x32x32 tiles of the same wave tile, at
+// less power per operation: under the power limit the clock runs ~18%
+// higher (1.67 vs 1.41 GHz on the north star).
 // The steady state is branch-free: past the last stage the issue cursor
 // uses zero-range buffer descriptors, so its loads fetch nothing and land
 // in a buffer no remaining stage reads, and every wait keeps the same
@@ -427,6 +437,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(!SPLITK || EPI == SDQ_EPI_ACC, "split-K partials are raw accumulators");
   static_assert(!(GROUPED && SPLITK), "grouped launches do not split K");
   static_assert(EPI != kEpiMixed || (GROUPED && !BIAS), "mixed epilogues come from a group's table");
+  static_assert(KS == 2, "a 16x16x64 k-step spans the two k-fragments of a stage");
   constexpr int NW = WN * WM;
   constexpr int RBN = BN / 32, RBM = BM / 32;
   constexpr int FN = RBN / WN, FM = RBM / WM;
@@ -436,9 +447,8 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   static_assert(WFR % NW == 0 && AFR % NW == 0, "stage fragments must split evenly over waves");
   static_assert(NW % KS == 0, "waves must be a multiple of k-fragments per stage");
   static_assert(NW >= 4, "four waves load the per-tile operands");
-  static_assert(KS == 2 || KS == 4, "k-fragments alternate between two register sets");
   static_assert(STAGES >= 2 && (STAGES - 1) * LPW < 64, "vmcnt range");
-  static_assert(LPW <= FN * FM && FN + FM <= FN * FM, "memory slots per MFMA");
+  static_assert(LPW <= 2 * FN * FM && FN <= 2 * FN * FM, "memory slots per MFMA");
   static_assert(BN <= 256 && BM <= 256, "one 1 KB DMA per per-tile operand");
   // GELU's epilogue spills SGPRs, and the grouped kernels read their
   // problem table into spilled SGPRs; the reloads can sit next to a DMA
@@ -583,73 +593,71 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     }
   };
 
-  struct Half {
-    v4i a[FN], b[FM];
+  // The stages' LDS image read as v_mfma_i32_16x16x64_i8 operands. Such an
+  // operand holds 16 rows (lane l: row l & 15) and 64 k-bytes, spread over
+  // the lanes the same way for both operands, so one 16-byte read per lane
+  // from the stage's two k-fragments of a 32-row block serves as one: lane
+  // l takes k-fragment l >> 5, fragment lane (l & 15) + 32((l >> 4) & 1),
+  // plus 16 rows for the block's second half. Per stage: XN weight operands
+  // (x: 16 rows), YM activation operands (y: 16 columns), XN x YM
+  // accumulators of 4 registers (result lane l, register r: n = 16x +
+  // 4(l >> 4) + r, m = 16y + (l & 15)).
+  constexpr int XN = 2 * FN, YM = 2 * FM;
+  const uint32_t off16 = (uint32_t)(lane >> 5) * 1024u +
+                         (uint32_t)((lane & 15) + 32 * ((lane >> 4) & 1)) * 16u;
+  struct Ops16 {
+    v4i a[XN], b[YM];
   };
-  // Fragment f (0..FN+FM-1: FN weight, then FM activation) of k-fragment
-  // kk of the stage held in LDS buffer `buf`.
-  auto read_frag = [&](const char* cb, int kk, int f, Half& h) {
-    if (f < FN)
-      h.a[f] = *reinterpret_cast<const v4i*>(cb + ((wn * FN + f) * KS + kk) * 1024 + lane_off);
+  Ops16 o16;
+  v4i acc16[XN][YM];
+  // Operand f of the stage in buffer cb: weight operands 0..XN-1, then
+  // activation operands.
+  auto read16 = [&](const char* cb, int f) {
+    if (f < XN)
+      o16.a[f] = *reinterpret_cast<const v4i*>(cb + (wn * FN + (f >> 1)) * KS * 1024 + off16 +
+                                               (f & 1) * 256);
     else
-      h.b[f - FN] = *reinterpret_cast<const v4i*>(
-          cb + WFR * 1024 + ((wm * FM + (f - FN)) * KS + kk) * 1024 + lane_off);
+      o16.b[f - XN] = *reinterpret_cast<const v4i*>(
+          cb + WFR * 1024 + (wm * FM + ((f - XN) >> 1)) * KS * 1024 + off16 + ((f - XN) & 1) * 256);
   };
-  v16i acc[FN][FM];
-  auto mfma = [&](const Half& h, int i) {
-    const int a = i / FM, b = i % FM;
-    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], acc[a][b], 0, 0, 0);
+  // A tile's first stage starts from zero (no separate clearing pass).
+  auto mma16 = [&](int x, int y, bool first) {
+    acc16[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(o16.a[x], o16.b[y],
+                                                        first ? v4i{} : acc16[x][y], 0, 0, 0);
   };
-  // A tile's first k-fragment starts from zero (no separate clearing pass).
-  auto mfma0 = [&](const Half& h, int i) {
-    const int a = i / FM, b = i % FM;
-    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(h.a[a], h.b[b], v16i{}, 0, 0, 0);
-  };
-  // One pipeline step (stage gs) in KS sub-steps: sub-step j runs the MFMAs
-  // of k-fragment j from register set h0 / h1 (alternating), interleaved
-  // with the LDS reads of k-fragment j + 1 into the other set; the last
-  // sub-step reads the next stage's k-fragment 0 (into h0, as KS is even). Before the
-  // last sub-step: this wave's loads of stage gs+1 landed (vmcnt), every
-  // wave finished reading buffer gs (lgkmcnt 0 + barrier), so the last
-  // sub-step also refills buffer gs with the stage STAGES ahead. Each MFMA
-  // slot is fenced with the memory instructions issued behind it. Without
-  // `Dma`, the refill is left to the caller (a tile's last step, whose
-  // buffer serves the epilogue first).
-  Half h0, h1;
-  auto sub = [&](auto dma_tag, auto j_tag, auto first_tag, int gs, const Half& cur, Half& nxt) {
+  // One pipeline step (stage gs) in two halves:
+  //   half 0: weight operands 0..FN-1 against every activation operand,
+  //           interleaved with the LDS reads of weight operands FN..XN-1;
+  //   wait until this wave's loads of the next stage landed and every
+  //   wave read buffer gs (vmcnt, lgkmcnt 0, barrier);
+  //   half 1: weight operands FN..XN-1, activation-operand major (each
+  //           activation register is free after its last use), interleaved
+  //           with the LDS-DMA of the stage STAGES ahead into buffer gs and
+  //           the reads of the next stage's weight operands 0..FN-1 and
+  //           activation operands.
+  auto step16 = [&](auto dma_tag, int gs, auto first_tag) {
     constexpr bool Dma = decltype(dma_tag)::value;
-    constexpr int j = decltype(j_tag)::value;
-    if constexpr (j == KS - 1) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW) & ~(15 << 8));
-      asm volatile("s_barrier" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    const char* cb = lds + ((unsigned)(j == KS - 1 ? gs + 1 : gs) % STAGES) * STAGE;
+    constexpr bool First = decltype(first_tag)::value;
+    const char* cb = lds + ((unsigned)gs % STAGES) * STAGE;
 #pragma unroll
-    for (int i = 0; i < FN * FM; i++) {
-      if constexpr (decltype(first_tag)::value && j == 0)
-        mfma0(cur, i);
-      else
-        mfma(cur, i);
-      if constexpr (j == KS - 1) {
-        if (Dma && i < LPW) dma_stage(i);
-        if (i < FN + FM) read_frag(cb, 0, i, nxt);
-      } else {
-        if (i < FN + FM) read_frag(cb, j + 1, i, nxt);
-      }
+    for (int i = 0; i < FN * YM; i++) {
+      mma16(i / YM, i % YM, First);
+      if (i < FN) read16(cb, FN + i);
       __builtin_amdgcn_sched_barrier(0);
     }
-  };
-  // first_tag: the tile's first stage (its k-fragment 0 starts from zero)
-  auto step = [&](auto dma_tag, int gs, auto first_tag) {
-    const std::false_type later;
-    sub(dma_tag, std::integral_constant<int, 0>{}, first_tag, gs, h0, h1);
-    sub(dma_tag, std::integral_constant<int, 1>{}, later, gs, h1, h0);
-    if constexpr (KS == 4) {
-      sub(dma_tag, std::integral_constant<int, 2>{}, later, gs, h0, h1);
-      sub(dma_tag, std::integral_constant<int, 3>{}, later, gs, h1, h0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LPW) & ~(15 << 8));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const char* nb = lds + ((unsigned)(gs + 1) % STAGES) * STAGE;
+#pragma unroll
+    for (int i = 0; i < FN * YM; i++) {
+      mma16(FN + i % FN, i / FN, First);
+      if (Dma && i < LPW) dma_stage(i);
+      if (i < FN) read16(nb, i);
+      if (i % FN == FN - 1) read16(nb, XN + i / FN);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (decltype(dma_tag)::value) advance();
+    if (Dma) advance();
   };
   const std::true_type with_dma, first_stage;
   const std::false_type defer_dma, next_stage;
@@ -664,7 +672,9 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LPW));
   asm volatile("s_barrier" ::: "memory");
 #pragma unroll
-  for (int f = 0; f < FN + FM; f++) read_frag(lds, 0, f, h0);
+  for (int f = 0; f < FN; f++) read16(lds, f);
+#pragma unroll
+  for (int f = 0; f < YM; f++) read16(lds, XN + f);
 
   // Epilogue memory goes through buffer descriptors too: masked lanes
   // (outside M x N) get an offset beyond the descriptor's range, which the
@@ -674,11 +684,10 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   // Output rows are written once, in whole 128-byte segments: streaming
   // (non-temporal) stores keep them from displacing the operand panels in L2.
   constexpr int kStreamStore = 2;
-  // Epilogue lane roles. MFMA layout: lane holds row lr of a 32x32 block,
-  // 4-column chunks 2g + lh (g = 0..3). Row layout, after the transpose
-  // through LDS: lane holds rows rr + 8i (i = 0..3), chunk rc, so eight
-  // consecutive lanes store one 128-byte row segment.
-  const int lr = lane & 31, lh = lane >> 5;
+  // Epilogue lane roles. Each 32x32 output block goes through LDS: from
+  // the MFMA layout (four 16x16 quarters) to the row layout, where a lane
+  // holds rows rr + 8i (i = 0..3), chunk rc, so eight consecutive lanes
+  // store one 128-byte row segment.
   const int rr = lane >> 3, rc = lane & 7;
   const int ldy4 = (int)N * 4;
   const int wrow = wm * FM * 32, wcol = wn * FN * 32;  // this wave's block in the tile
@@ -695,13 +704,13 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
     // wave writes these slots, now and in the deferred refill.
     char* scr;
     if constexpr (kOwnScratch) {
-      step(with_dma, gs++, first_stage);
-      for (int q = 1; q < nst; q++) step(with_dma, gs++, next_stage);
+      step16(with_dma, gs++, first_stage);
+      for (int q = 1; q < nst; q++) step16(with_dma, gs++, next_stage);
       scr = escr + w * 4096;
     } else {
-      step(with_dma, gs++, first_stage);
-      for (int q = 2; q < nst; q++) step(with_dma, gs++, next_stage);
-      step(defer_dma, gs, next_stage);
+      step16(with_dma, gs++, first_stage);
+      for (int q = 2; q < nst; q++) step16(with_dma, gs++, next_stage);
+      step16(defer_dma, gs, next_stage);
       scr = lds + ((unsigned)gs % STAGES) * STAGE + w * 1024;
       gs++;
     }
@@ -771,13 +780,15 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
       }
 #pragma unroll
       for (int b = 0; b < FM; b++) {
-        const v16i& c = acc[a][b];
-        // transpose the block: MFMA layout -> scratch -> row layout
+        // transpose the block: MFMA layout -> scratch -> row layout. Its
+        // four 16x16 quarters: lane holds block row 16hb + (l & 15), 4-column
+        // chunk 4ha + (l >> 4).
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const v4i c4 = {c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-          *reinterpret_cast<v4i*>(scr + (lr >> 3) * kSlot + (lr & 7) * 128 +
-                                  (((2 * g + lh) ^ (lr & 7)) * 16)) = c4;
+        for (int q = 0; q < 4; q++) {
+          const int ha = q >> 1, hb = q & 1;
+          const int row = 16 * hb + (lane & 15), chunk = 4 * ha + (lane >> 4);
+          *reinterpret_cast<v4i*>(scr + (row >> 3) * kSlot + (row & 7) * 128 +
+                                  ((chunk ^ (row & 7)) * 16)) = acc16[2 * a + ha][2 * b + hb];
         }
         v4i t4[4];
 #pragma unroll
@@ -1477,8 +1488,7 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
         // maxima (the two tile widths write different column chunks).
         const int64_t Ma = epi_r.rmax ? 0 : tail_split_rows(M, N, aux.cu_count);
         if (Ma > 0) {
-          hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r,
-                                                              Y, aux.cu_count, s);
+          hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r, Y, aux.cu_count, s);
           if (e != hipSuccess) return e;
           if (aux.tail) *aux.tail = 1;
           if (aux.mid && (e = hipEventRecord(aux.mid, s)) != hipSuccess) return e;
@@ -1488,8 +1498,7 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
               wt, cols, at + (Ma / kFragRows) * KFp * kFragBytes, as + Ma, M - Ma, N, KFp, et,
               static_cast<char*>(Y) + Ma * N * 4, 2 * aux.cu_count, s);
         }
-        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y,
-                                                    aux.cu_count, s);
+        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y, aux.cu_count, s);
       }
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;

@@ -1,6 +1,6 @@
 // Practical ceiling of the int8 MFMA pipe on this GPU (gfx950), for the
-// roofline of the qGEMM: v_mfma_i32_32x32x32_i8 back to back in every SIMD,
-// one workgroup per CU, operands
+// roofline of the qGEMM: v_mfma_i32_32x32x32_i8 or v_mfma_i32_16x16x64_i8
+// back to back in every SIMD, one workgroup per CU, operands
 //   * random bytes held in registers (no memory traffic), or
 //   * random bytes re-read from LDS every k-step with the qGEMM's register
 //     double buffering (the operand pattern of its 128n x 64m wave tiles),
@@ -10,7 +10,10 @@
 // same instruction stream runs on random and on zero operands: the gap
 // between the two is the power limit (the clock drops when the operands
 // switch), which bounds the GEMM below the 5.0 POPS nominal peak (a
-// 32x32x32 i8 MFMA is 65536 ops, 32 cycles per SIMD: 8192 ops/clk/CU).
+// 32x32x32 i8 MFMA is 65536 ops, 32 cycles per SIMD: 8192 ops/clk/CU; a
+// 16x16x64 one is 32768 ops in 16 cycles, the same rate per clock). Two
+// forms with the same wave tile and the same LDS bytes per k are compared:
+// the 16x16x64 one switches fewer accumulator registers per operation.
 // Each kernel also reads s_memtime and s_memrealtime around its loop; their
 // ratio is printed as a relative clock reading (higher = faster clock).
 //
@@ -101,6 +104,66 @@ mfma_loop(int iters, const int* __restrict__ bytes, int* out, Clocks* clk) {
   if (threadIdx.x == 0) clk[blockIdx.x] = Clocks{s1 - s0, r1 - r0};
 }
 
+// The same with v_mfma_i32_16x16x64_i8: FN x FM blocks of 16x16 per wave
+// (a 32x32 block of the loop above is 2 x 2 of these, so FN x FM here is
+// 2FN x 2FM there for the same wave tile).
+template <int FN, int FM, bool READS, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64, 1)
+mfma16_loop(int iters, const int* __restrict__ bytes, int* out, Clocks* clk) {
+  __shared__ v4i lds[kLdsVec];
+  for (int i = threadIdx.x; i < kLdsVec; i += blockDim.x) {
+    const int* r = bytes + ((size_t)blockIdx.x * kLdsVec + i) % (1 << 20) * 4;
+    lds[i] = v4i{r[0], r[1], r[2], r[3]};
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v4i acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; a++)
+#pragma unroll
+    for (int b = 0; b < FM; b++) acc[a][b] = v4i{0, 0, 0, 0};
+  v4i a0[FN], b0[FM], a1[FN], b1[FM];
+#pragma unroll
+  for (int a = 0; a < FN; a++) a0[a] = a1[a] = lds[(lane + (a + w * 16) * 64) & (kLdsVec - 1)];
+#pragma unroll
+  for (int b = 0; b < FM; b++) b0[b] = b1[b] = lds[(lane + (b + 8 + w * 16) * 64) & (kLdsVec - 1)];
+  const unsigned long long s0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < FN * FM; i++) {
+      acc[i / FM][i % FM] =
+          __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[i / FM], b0[i % FM], acc[i / FM][i % FM], 0, 0, 0);
+      if (READS && i < FN)
+        a1[i] = lds[(lane + (i + w * 16 + it * 2) * 64) & (kLdsVec - 1)];
+      else if (READS && i < FN + FM)
+        b1[i - FN] = lds[(lane + (i + w * 16 + it * 2 + 64) * 64) & (kLdsVec - 1)];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < FN * FM; i++) {
+      acc[i / FM][i % FM] =
+          __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[i / FM], b1[i % FM], acc[i / FM][i % FM], 0, 0, 0);
+      if (READS && i < FN)
+        a0[i] = lds[(lane + (i + w * 16 + it * 2 + 1) * 64) & (kLdsVec - 1)];
+      else if (READS && i < FN + FM)
+        b0[i - FN] = lds[(lane + (i + w * 16 + it * 2 + 65) * 64) & (kLdsVec - 1)];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const unsigned long long s1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  int sum = 0;
+#pragma unroll
+  for (int a = 0; a < FN; a++)
+#pragma unroll
+    for (int b = 0; b < FM; b++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) sum += acc[a][b][r];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
+  if (threadIdx.x == 0) clk[blockIdx.x] = Clocks{s1 - s0, r1 - r0};
+}
+
 // 16-byte LDS reads, 16 per wave per iteration, conflict free.
 template <int WAVES>
 __global__ void __launch_bounds__(WAVES * 64, 1)
@@ -181,11 +244,30 @@ int main() {
         ops, NAME, "ops");                                                                         \
     std::printf("  %6.0f TOPS = %.3f of 5.0 POPS\n", r.second / 1e12, r.second / 5.0e15);        \
   }
-  MFMA(4, 2, false, 8, rnd, "8 waves, 4x2 blocks, random, registers")
-  MFMA(4, 2, true, 8, rnd, "8 waves, 4x2 blocks, random, LDS reads")
-  MFMA(4, 4, false, 4, rnd, "4 waves, 4x4 blocks, random, registers")
-  MFMA(4, 4, true, 4, rnd, "4 waves, 4x4 blocks, random, LDS reads")
-  MFMA(4, 2, true, 8, zero, "8 waves, 4x2 blocks, zeros, LDS reads")
+#define MFMA16(FN, FM, READS, WAVES, SRC, NAME)                                                    \
+  {                                                                                                \
+    const int iters = 4000;                                                                        \
+    const double ops = (double)WAVES * iters * 2 * FN * FM * 32768.0;                              \
+    auto r = timed(                                                                                \
+        [&] {                                                                                      \
+          hipLaunchKernelGGL((mfma16_loop<FN, FM, READS, WAVES>), dim3(cus), dim3(WAVES * 64), 0,  \
+                             0, iters, SRC, out, clk);                                             \
+        },                                                                                         \
+        ops, NAME, "ops");                                                                         \
+    std::printf("  %6.0f TOPS = %.3f of 5.0 POPS\n", r.second / 1e12, r.second / 5.0e15);        \
+  }
+  // the first launch on a cold GPU runs at a lower clock: one untimed pass
+  MFMA(4, 2, true, 8, rnd, "(warm-up) 32x32x32, 8 waves, 4x2 blocks")
+  MFMA(4, 2, false, 8, rnd, "32x32x32, 8 waves, 4x2 blocks, random, registers")
+  MFMA16(8, 4, false, 8, rnd, "16x16x64, 8 waves, 8x4 blocks, random, registers")
+  MFMA(4, 2, true, 8, rnd, "32x32x32, 8 waves, 4x2 blocks, random, LDS reads")
+  MFMA16(8, 4, true, 8, rnd, "16x16x64, 8 waves, 8x4 blocks, random, LDS reads")
+  MFMA(2, 2, true, 8, rnd, "32x32x32, 8 waves, 2x2 blocks, random, LDS reads")
+  MFMA16(4, 4, true, 8, rnd, "16x16x64, 8 waves, 4x4 blocks, random, LDS reads")
+  MFMA(4, 4, false, 4, rnd, "32x32x32, 4 waves, 4x4 blocks, random, registers")
+  MFMA(4, 4, true, 4, rnd, "32x32x32, 4 waves, 4x4 blocks, random, LDS reads")
+  MFMA(4, 2, true, 8, zero, "32x32x32, 8 waves, 4x2 blocks, zeros, LDS reads")
+  MFMA16(8, 4, true, 8, zero, "16x16x64, 8 waves, 8x4 blocks, zeros, LDS reads")
 #define LDS(WAVES)                                                                                 \
   {                                                                                                \
     const int iters = 4000;                                                                        \

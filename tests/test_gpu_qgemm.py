@@ -192,6 +192,35 @@ def test_core_3072x5120x5120_matches_reference_hash(sdq_dev, oracle):
     assert hashlib.sha256(got.tobytes()).digest() == r["core_3072x5120x5120_sha256"].tobytes()
 
 
+@pytest.mark.parametrize("M,K,N", [(300, 257, 129), (700, 3072, 1000), (513, 1024, 520)])
+def test_256_tiles_forced_bitexact(sdq_dev, oracle, monkeypatch, M, K, N):
+    """The 256x256 persistent kernel (chosen by itself only for large grids)
+    forced onto ragged shapes, with every epilogue form: partial tiles in
+    both dimensions, K not a multiple of the 64-byte k-step."""
+    import sdq
+
+    monkeypatch.setenv("SDQ_FORCE_CFG", "2")  # kCfg256x256
+    monkeypatch.setenv("SDQ_NO_TAIL", "1")
+    print(f"[256-forced] M={M} K={K} N={N}", flush=True)
+    A, q, s, bias = _inputs(M, K, N, seed=11 * M + K + N)
+    w = sdq.Weight.from_host(q, s)
+    aq, _ = oracle.act_quant(A)
+    assert_bitexact(_run(sdq_dev, w, A, kind="acc"), oracle.qgemm_acc(aq, q), "256 acc")
+    assert_bitexact(_run(sdq_dev, w, A), oracle.qgemm(A, q, s), "256 qgemm")
+    assert_bitexact(_run(sdq_dev, w, A, bias=bias), oracle.linear(A, q, s, bias=bias), "256 mlin")
+    gate = oracle.randn(N, 96)
+    x = oracle.randn(M * N, 95).reshape(M, N)
+    got = _run(sdq_dev, w, A, kind="gated", bias=bias, gate=gate, resid=x)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gated", gate=gate, resid=x)
+    assert_bitexact(got, want, "256 gated")
+    got = _run(sdq_dev, w, A, kind="resid", bias=bias, resid=x)
+    assert_bitexact(got, oracle.linear(A, q, s, bias=bias, epilogue="resid", resid=x), "256 resid")
+    got = _run(sdq_dev, w, A, kind="gelu", bias=bias)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gelu")
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-6 * (1.0 + np.abs(want))), float(err.max())
+
+
 # ---------------------------------------------------------------- epilogues
 @pytest.mark.parametrize("M,K,N", [(40, 3072, 3072), (300, 1024, 3072), (5, 14336, 3072)])
 @pytest.mark.parametrize("fma", [True, False])
