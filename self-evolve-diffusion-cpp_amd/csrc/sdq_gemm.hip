@@ -1488,7 +1488,8 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
         // maxima (the two tile widths write different column chunks).
         const int64_t Ma = epi_r.rmax ? 0 : tail_split_rows(M, N, aux.cu_count);
         if (Ma > 0) {
-          hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r, Y, aux.cu_count, s);
+          hipError_t e = run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, Ma, N, KFp, epi_r,
+                                                              Y, aux.cu_count, s);
           if (e != hipSuccess) return e;
           if (aux.tail) *aux.tail = 1;
           if (aux.mid && (e = hipEventRecord(aux.mid, s)) != hipSuccess) return e;
@@ -1498,7 +1499,8 @@ hipError_t launch_qgemm(int cfg, const int8_t* wt, const float* bs, const int8_t
               wt, cols, at + (Ma / kFragRows) * KFp * kFragBytes, as + Ma, M - Ma, N, KFp, et,
               static_cast<char*>(Y) + Ma * N * 4, 2 * aux.cu_count, s);
         }
-        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y, aux.cu_count, s);
+        return run_persist<256, 256, 2, 4, 2, 4, 1>(wt, cols, at, as, M, N, KFp, epi_r, Y,
+                                                    aux.cu_count, s);
       }
       return run_tiled<256, 256, 2, 4, 2, 4>(wt, bs, at, as, M, N, KFp, epi, Y, vec, s);
     default: return hipErrorInvalidValue;
