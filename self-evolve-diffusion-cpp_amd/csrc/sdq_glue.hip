@@ -233,8 +233,12 @@ hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Scaled dot-product attention (src/model/blocks.cpp:112-199, non-causal):
 // out[i, head] = softmax_j(q_i . k_j / sqrt(hd)) v_j, head_dim 128: the
-// scores in fp32 (v_mfma_f32_32x32x2_f32; the softmax's exponential would
-// amplify any error in them), P.V as three bf16 products per fp32 product on
+// scores as three fp16 products per fp32 product on v_mfma_f32_32x32x16_f16
+// (the softmax's exponential would amplify any error in them: each q and k
+// row is scaled by a power of two into [0.5, 1) of its largest element, then
+// split as x = hi + lo, hi = fp16(x), lo = fp16(x - hi), and q.k taken as
+// hi.hi + hi.lo + lo.hi, ~2^-22 relative per product; the powers of two come
+// back out exactly in fp32), P.V as three bf16 products per fp32 product on
 // v_mfma_f32_32x32x16_bf16 (~2^-17 relative, P in [0, 1]), an online softmax
 // (running max and sum per query, the accumulator rescaled when the max
 // moves), fp32 accumulation. The reference sums in a fixed serial order, so
@@ -246,8 +250,11 @@ hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
 //   S^T = K . Q^T    32 keys x 32 queries: lane (query j = l & 31, half
 //                    h = l >> 5) holds 16 keys of its query, so the softmax
 //                    of a query is one lane plus its partner lane l ^ 32;
-//                    MFMA step s takes dim 64h + s in both operands (Q stays
-//                    in 64 VGPRs, K is read 16 bytes at a time).
+//                    MFMA step s takes dims 64h + 8s .. +7 in both operands
+//                    (Q's fp16 parts stay in 64 VGPRs, K's are read 16 bytes
+//                    at a time); each key's score is then multiplied by its
+//                    row's power of two, the query's goes into the softmax's
+//                    scale.
 //   O^T += V^T . P^T 128 dims x 32 queries in four 32 x 32 tiles; step t's
 //                    key in half h is 8(t/4) + 4h + t%4, exactly the key of
 //                    the lane's S^T register t, so P feeds the MFMA with no
@@ -261,9 +268,11 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 constexpr int kHd = 128;      // head dim
 constexpr int kKB = 32;       // keys per block
-constexpr int kKPad = 132;    // LDS row of K (floats): conflict-free 16-byte reads
+constexpr int kKPadH = 136;   // LDS row of K's fp16 parts (halves): conflict-free 16-byte reads
 constexpr int kVPd = 20;      // LDS row of V^T (dwords: 32 bf16 + pad; conflict-free stash)
 
 // Key split (SPLIT): workgroup z of the grid takes key blocks [z*kbs,
@@ -277,6 +286,21 @@ struct SdpaPart {
   int kbs;     // key blocks per split
 };
 
+// Exponent e with x * 2^-e in [0.5, 1) for a row's largest magnitude x
+// (0 for a zero row, so its factor is 1).
+__device__ __forceinline__ int row_exp(float x) {
+  return x > 0.f && x <= 3.4e38f ? __builtin_amdgcn_frexp_expf(x) : 0;
+}
+
+// x = hi + lo + O(2^-22 |x|) in fp16 (|x| < 1 here: no overflow)
+struct HalfPair {
+  _Float16 hi, lo;
+};
+__device__ __forceinline__ HalfPair split_f16(float x) {
+  const _Float16 hi = (_Float16)x;
+  return HalfPair{hi, (_Float16)(x - (float)hi)};
+}
+
 template <int NW, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64)
 sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
@@ -288,7 +312,12 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   O += (int64_t)blockIdx.y * Lq * ldo;
   K += (int64_t)blockIdx.y * Lk * ldk;
   V += (int64_t)blockIdx.y * Lk * ldv;
-  __shared__ __attribute__((aligned(16))) float ks[2][kKB][kKPad];
+  // K as fp16 hi and lo parts of each row scaled by 2^-e (its largest
+  // element in [0.5, 1)); 2^e per key in a ring of three blocks (a block's
+  // factors are read in the iteration after its K buffer was refilled)
+  __shared__ __attribute__((aligned(16))) _Float16 ksh[2][kKB][kKPadH];
+  __shared__ __attribute__((aligned(16))) _Float16 ksl[2][kKB][kKPadH];
+  __shared__ __attribute__((aligned(16))) float kexp[3][kKB];
   // V^T as bf16 hi and lo parts, two keys per dword, keys of each 16-key
   // group stored in the order 0-3, 8-11, 4-7, 12-15 (lane half h then reads
   // its 8 keys of a PV step as one 16-byte run)
@@ -304,11 +333,16 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   int64_t kb0 = 0;
   if constexpr (SPLIT) kb0 = (int64_t)blockIdx.z * part.kbs;
 
-  // this lane's query row, dims 64h .. 64h+63
-  float qr[64];
+  // this lane's query row, dims 64h .. 64h+63, scaled by 2^-e (the row's
+  // largest element in [0.5, 1)) and split into fp16 parts for the 8 MFMA
+  // steps; sq = scale * log2(e) * 2^e puts the factor back in the softmax
+  v8h qh[8], ql[8];
+  float sq;
   {
     const int64_t qi = q0 + j;
     const float* src = Q + (qi < Lq ? qi : 0) * ldq + col + 64 * h;
+    float qr[64];
+    float mq = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; c++) {
       const float4 v = qi < Lq ? reinterpret_cast<const float4*>(src)[c] : float4{0.f, 0.f, 0.f, 0.f};
@@ -316,7 +350,19 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       qr[4 * c + 1] = v.y;
       qr[4 * c + 2] = v.z;
       qr[4 * c + 3] = v.w;
+      mq = fmaxf(mq, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
+    mq = fmaxf(mq, __shfl_xor(mq, 32));
+    const int eq = row_exp(mq);
+    sq = ldexpf(scale_log2e, eq);
+#pragma unroll
+    for (int st8 = 0; st8 < 8; st8++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const HalfPair p = split_f16(ldexpf(qr[8 * st8 + e], -eq));
+        qh[st8][e] = p.hi;
+        ql[st8][e] = p.lo;
+      }
   }
   // Cooperative block loads. K: 32 keys x 32 float4, element f is (key
   // f >> 5, float4 f & 31), whole rows per half-wave. V: 16 key pairs x 32
@@ -357,11 +403,24 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
                               : float4{0.f, 0.f, 0.f, 0.f};
     }
   };
-  auto stash_k = [&](int b) {
+  // K block into buffer b, its keys' factors into ring slot `slot`: the 32
+  // lanes of a half-wave hold one key row (PER * NT = 32 * 32 float4s), so
+  // the row's largest element is a 32-lane reduction
+  auto stash_k = [&](int b, int slot) {
 #pragma unroll
     for (int c = 0; c < PER; c++) {
       const int f = tid + c * NT;
-      if (f < kKB * kHd / 4) *reinterpret_cast<float4*>(&ks[b][f >> 5][4 * (f & 31)]) = pk[c];
+      const float4 v = pk[c];
+      float mk = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+      for (int d = 1; d < 32; d *= 2) mk = fmaxf(mk, __shfl_xor(mk, d));
+      const int ek = row_exp(mk);
+      const HalfPair px = split_f16(ldexpf(v.x, -ek)), py = split_f16(ldexpf(v.y, -ek));
+      const HalfPair pz = split_f16(ldexpf(v.z, -ek)), pw = split_f16(ldexpf(v.w, -ek));
+      const v4h hi = {px.hi, py.hi, pz.hi, pw.hi}, lo = {px.lo, py.lo, pz.lo, pw.lo};
+      *reinterpret_cast<v4h*>(&ksh[b][f >> 5][4 * (f & 31)]) = hi;
+      *reinterpret_cast<v4h*>(&ksl[b][f >> 5][4 * (f & 31)]) = lo;
+      if ((f & 31) == 0) kexp[slot][f >> 5] = ldexpf(1.f, ek);
     }
   };
   // x -> (bf16(x), bf16(x - bf16(x))) for the two keys of a dword
@@ -389,17 +448,19 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       }
     }
   };
-  // S^T = K . Q^T (keys x queries) from K buffer b
+  // S^T = K . Q^T (keys x queries, both scaled) from K buffer b: per step
+  // hi.hi + hi.lo + lo.hi
   auto scores = [&](int b) {
     v16f st = v16f{};
-    const float* krow = &ks[b][j][64 * h];
+    const _Float16* khrow = &ksh[b][j][64 * h];
+    const _Float16* klrow = &ksl[b][j][64 * h];
 #pragma unroll
-    for (int s4 = 0; s4 < 16; s4++) {
-      const float4 kv = *reinterpret_cast<const float4*>(krow + 4 * s4);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qr[4 * s4], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qr[4 * s4 + 1], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qr[4 * s4 + 2], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qr[4 * s4 + 3], st, 0, 0, 0);
+    for (int s8 = 0; s8 < 8; s8++) {
+      const v8h kh = *reinterpret_cast<const v8h*>(khrow + 8 * s8);
+      const v8h kl = *reinterpret_cast<const v8h*>(klrow + 8 * s8);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[s8], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[s8], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[s8], st, 0, 0, 0);
     }
     return st;
   };
@@ -412,12 +473,12 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   if constexpr (SPLIT) nkb = (nkb - kb0) < part.kbs ? (nkb - kb0) : part.kbs;
   // prologue: K(0) -> scores; then K(1) and V(0) staged
   fetch_k(0);
-  stash_k(0);
+  stash_k(0, 0);
   fetch_k(1);
   fetch_v(0);
   __syncthreads();
   v16f st = scores(0);
-  stash_k(1);
+  stash_k(1, 1);
   stash_v(0);
   __syncthreads();
   for (int64_t kb = 0; kb < nkb; kb++) {
@@ -427,25 +488,32 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     // scores of the next block (discarded after the last block)
     const v16f sn = scores(b ^ 1);
     // online softmax (base 2, m in units of scale*log2 e) of this block:
-    // register r holds key kb*32 + 8(r/4) + 4h + r%4; keys past Lk are -inf.
+    // register r holds key kb*32 + 8(r/4) + 4h + r%4 (times its row factor
+    // 2^-e_k, put back here); keys past Lk are -inf.
     // v_exp_f32 flushes results below 2^-126 to 0, which moves a row sum
     // that holds a 1 (the max) by less than 2^-121.
     const int64_t kba = SPLIT ? kb0 + kb : kb;  // the block's index among all keys
     const int rem = Lk - kba * kKB < kKB ? (int)(Lk - kba * kKB) : kKB;
     float t[16];
     float mloc = -INFINITY;
+    const float* kf = kexp[(int)(kb % 3)];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      t[r] = 8 * (r >> 2) + 4 * h + (r & 3) < rem ? st[r] : -INFINITY;
-      mloc = fmaxf(mloc, t[r]);
+    for (int g = 0; g < 4; g++) {
+      const float4 f4 = *reinterpret_cast<const float4*>(kf + 8 * g + 4 * h);
+      const float fg[4] = {f4.x, f4.y, f4.z, f4.w};
+#pragma unroll
+      for (int r = 4 * g; r < 4 * g + 4; r++) {
+        t[r] = 8 * (r >> 2) + 4 * h + (r & 3) < rem ? st[r] * fg[r & 3] : -INFINITY;
+        mloc = fmaxf(mloc, t[r]);
+      }
     }
     const float mo = __shfl_xor(mloc, 32);
-    const float mnew = fmaxf(m, fmaxf(mloc, mo) * scale_log2e);
+    const float mnew = fmaxf(m, fmaxf(mloc, mo) * sq);
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // m = -inf at the first block: 0
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      t[r] = __builtin_amdgcn_exp2f(fmaf(t[r], scale_log2e, -mnew));
+      t[r] = __builtin_amdgcn_exp2f(fmaf(t[r], sq, -mnew));
       ps += t[r];
     }
     lsum = lsum * alpha + ps;
@@ -484,7 +552,7 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     }
     // K(kb+2) into the buffer K(kb) left before the last barrier; V(kb+1)
     // into the one V(kb-1) left
-    stash_k(b);
+    stash_k(b, (int)((kb + 2) % 3));
     stash_v(b ^ 1);
     st = sn;
     __syncthreads();

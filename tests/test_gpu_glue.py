@@ -68,8 +68,9 @@ def test_rmsnorm_rope_errors(sdq_dev):
 def test_sdpa_matches_oracle(sdq_dev, oracle, Lq, Lk, heads):
     """Attention on q|k|v-style strided inputs against the oracle (bit-exact
     with the reference build's sdpa): within 2e-5 of the output scale (QK^T
-    on the fp32 MFMA, PV as three bf16 MFMA products per fp32 product, and an
-    online softmax sum in another order). Few queries run as key splits
+    as three fp16 MFMA products per fp32 product of power-of-two-scaled rows,
+    PV as three bf16 MFMA products, and an online softmax sum in another
+    order). Few queries run as key splits
     merged afterwards (here 300x300, 157x512, and the twin backbone's audio
     fusion and video self-attention shapes)."""
     import torch
@@ -82,6 +83,42 @@ def test_sdpa_matches_oracle(sdq_dev, oracle, Lq, Lk, heads):
     q = (rng.standard_normal((Lq, C)) * 0.6).astype(np.float32)
     kv = rng.standard_normal((Lk, 2 * C)).astype(np.float32)
     kv[:, :C] *= np.float32(0.6)
+    want = oracle.sdpa(q, kv[:, :C], kv[:, C:], heads)
+    qd = torch.from_numpy(q).to(sdq_dev)
+    kvd = torch.from_numpy(kv).to(sdq_dev)
+    out = torch.full((Lq, C), float("nan"), device=sdq_dev)
+    sdq.sdpa(qd, kvd, kvd, out, heads, kcol=0, vcol=C)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    err = np.abs(got.astype(np.float64) - want) / (np.abs(want).max() + 1e-30)
+    print(f"  max rel err {err.max():.3e}", flush=True)
+    assert err.max() <= 2e-5, float(err.max())
+
+
+@pytest.mark.parametrize("qs,ks", [(3e4, 1e-4), (1e-6, 1e6), (1.0, 1.0)])
+def test_sdpa_element_range(sdq_dev, oracle, qs, ks):
+    """q and k elements far outside the fp16 range (up to ~1e5, down to
+    ~1e-6), with logits of ordinary size, and rows whose magnitudes differ by
+    2^-12..2^12 inside one key block: the scores' fp16 parts are taken of
+    rows scaled by powers of two, which come back out exactly."""
+    import torch
+
+    import sdq
+
+    Lq, Lk, heads = 100, 300, 2
+    C = heads * 128
+    print(f"[sdpa-range] q*{qs} k*{ks}", flush=True)
+    rng = np.random.default_rng(17)
+    q = (rng.standard_normal((Lq, C)) * 0.6 * qs).astype(np.float32)
+    kv = rng.standard_normal((Lk, 2 * C)).astype(np.float32)
+    kv[:, :C] *= np.float32(0.6 * ks)
+    if qs == 1.0:
+        # key rows 2^-12..2^12; q small enough that the largest rows' logits
+        # stay ordinary (std ~6)
+        rs = np.exp2(rng.integers(-12, 13, Lk)).astype(np.float32)
+        kv[:, :C] *= rs[:, None]
+        q *= np.float32(2.0 ** -8)
     want = oracle.sdpa(q, kv[:, :C], kv[:, C:], heads)
     qd = torch.from_numpy(q).to(sdq_dev)
     kvd = torch.from_numpy(kv).to(sdq_dev)
