@@ -159,7 +159,7 @@ int sd_dit_blocks_from_pack(const char* path, const char* prefix, const int* lay
 // Device workspace bytes that sd_dit_block_step_forward needs for these rows.
 size_t sd_dit_block_workspace_bytes(const sd_dit_block* b, int64_t M, int64_t Mc, int64_t Mt);
 // The whole block on the GPU, stream-ordered, bit-exact with the reference
-// build except the attention (fp32 scores, split-bf16 P.V, an online softmax:
+// build except the attention (split-fp16 scores, split-bf16 P.V, an online softmax:
 // within 2e-5 of the reference's sdpa); phases = SD_DIT_SELF | SD_DIT_CROSS_FFN. A fusion
 // layer (ovi_dit.cpp:726-734) runs SELF on both branches, then CROSS_FFN of
 // the audio branch (target = video x), then of the video branch with target =

@@ -4,8 +4,8 @@ restatement of the reference's block (ovi_dit.cpp:205-268): block_self_fwd,
 then block_vanilla_fwd's cross attention + FFN, or fusion_cross_ffn.
 
 Every step of the oracle chain is pinned to the reference build; the GPU's
-steps are each bit-exact with it except the attention (fp32 scores, split
-bf16 P.V, online softmax: within 2e-5 of the output scale) and GELU's tanhf, both tested on
+steps are each bit-exact with it except the attention (split-fp16 scores,
+split bf16 P.V, online softmax: within 2e-5 of the output scale) and GELU's tanhf, both tested on
 their own against the oracle. Two checks per case:
   * bit-exact: the oracle chain with its sdpa and fc1+GELU steps replaced by
     the GPU's own kernels (sdq.sdpa, sdq.qlinear_host with the GELU
