@@ -301,6 +301,37 @@ __device__ __forceinline__ HalfPair split_f16(float x) {
   return HalfPair{hi, (_Float16)(x - (float)hi)};
 }
 
+// max / sum of a lane's value and lane l ^ 32's, in both lanes (one VALU
+// lane swap instead of an LDS permute)
+__device__ __forceinline__ float pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// max over the 32 lanes of each half-wave, in all of them: DPP within rows of
+// 16 (xor 1, xor 2, then the half-row and row mirrors pair the reduced
+// groups), then a row swap pairs rows 0-1 and 2-3
+__device__ __forceinline__ float half_wave_max(float v) {
+  auto dpp = [](float x, auto ctrl_tag) {
+    constexpr int ctrl = decltype(ctrl_tag)::value;
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), ctrl, 0xF, 0xF,
+                                                       false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm 1,0,3,2
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm 2,3,0,1
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <int NW, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64)
 sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
@@ -352,7 +383,7 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       qr[4 * c + 3] = v.w;
       mq = fmaxf(mq, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    mq = fmaxf(mq, __shfl_xor(mq, 32));
+    mq = pair32_max(mq);
     const int eq = row_exp(mq);
     sq = ldexpf(scale_log2e, eq);
 #pragma unroll
@@ -411,9 +442,8 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
     for (int c = 0; c < PER; c++) {
       const int f = tid + c * NT;
       const float4 v = pk[c];
-      float mk = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-      for (int d = 1; d < 32; d *= 2) mk = fmaxf(mk, __shfl_xor(mk, d));
+      const float mk =
+          half_wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
       const int ek = row_exp(mk);
       const HalfPair px = split_f16(ldexpf(v.x, -ek)), py = split_f16(ldexpf(v.y, -ek));
       const HalfPair pz = split_f16(ldexpf(v.z, -ek)), pw = split_f16(ldexpf(v.w, -ek));
@@ -502,13 +532,17 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       const float4 f4 = *reinterpret_cast<const float4*>(kf + 8 * g + 4 * h);
       const float fg[4] = {f4.x, f4.y, f4.z, f4.w};
 #pragma unroll
-      for (int r = 4 * g; r < 4 * g + 4; r++) {
-        t[r] = 8 * (r >> 2) + 4 * h + (r & 3) < rem ? st[r] * fg[r & 3] : -INFINITY;
-        mloc = fmaxf(mloc, t[r]);
-      }
+      for (int r = 4 * g; r < 4 * g + 4; r++) t[r] = st[r] * fg[r & 3];
     }
-    const float mo = __shfl_xor(mloc, 32);
-    const float mnew = fmaxf(m, fmaxf(mloc, mo) * sq);
+    // only a last, partial block has keys to mask (a uniform branch)
+    if (rem < kKB) {
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        if (8 * (r >> 2) + 4 * h + (r & 3) >= rem) t[r] = -INFINITY;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, t[r]);
+    const float mnew = fmaxf(m, pair32_max(mloc) * sq);
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // m = -inf at the first block: 0
     float ps = 0.f;
 #pragma unroll
@@ -551,14 +585,16 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
       }
     }
     // K(kb+2) into the buffer K(kb) left before the last barrier; V(kb+1)
-    // into the one V(kb-1) left
+    // into the one V(kb-1) left. Kept after the P.V MFMAs: hoisted into the
+    // softmax, the stash's work would wait there for this iteration's loads.
+    __builtin_amdgcn_sched_barrier(0);
     stash_k(b, (int)((kb + 2) % 3));
     stash_v(b ^ 1);
     st = sn;
     __syncthreads();
   }
   // out[query][dim]: lane holds dims 32tt + 8(r/4) + 4h + r%4 of query j
-  const float ltot = lsum + __shfl_xor(lsum, 32);
+  const float ltot = pair32_sum(lsum);
   const int64_t qi = q0 + j;
   if constexpr (SPLIT) {
     if (qi < Lq) {
