@@ -271,10 +271,11 @@ int sdq_add(float* x, const float* y, int64_t n, void* stream);
  *   out[i, h] = sum_j softmax_j(q[i, h] . k[j, h] / sqrt(head_dim)) v[j, h]
  * with q [Lq, ldq], k, v [Lk, ldk / ldv], out [Lq, ldo] row-major (e.g. the
  * q, k, v column blocks of a q|k|v tensor), head h in columns
- * h*head_dim .. h*head_dim+head_dim-1; head_dim = 128. Scores on the fp32
- * MFMA, P.V as three split bf16 MFMA products per fp32 product, an online
- * softmax: within 2e-5 of the reference's output scale (its serial sums are
- * not reproduced). 16-byte aligned rows. Stream-ordered. */
+ * h*head_dim .. h*head_dim+head_dim-1; head_dim = 128. Scores as three
+ * split fp16 MFMA products per fp32 product (each q and k row scaled by a
+ * power of two first, taken back out exactly), P.V as three split bf16 MFMA
+ * products, an online softmax: within 2e-5 of the reference's output scale
+ * (its serial sums are not reproduced). 16-byte aligned rows. Stream-ordered. */
 int sdq_sdpa(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v, int64_t ldv,
              float* out, int64_t ldo, int64_t Lq, int64_t Lk, int heads, int head_dim,
              void* stream);

@@ -10,7 +10,9 @@
 //   the same k placement, so the exact int32 sum does not depend on which
 //   k the hardware assigns to a byte), so a 1 KB fragment moves
 //   global -> LDS -> VGPRs as one linear, conflict-free 16-byte-per-lane
-//   copy. Rows are padded to a multiple of the largest GEMM tile and KFp to
+//   copy; the persistent kernels read the two fragments of a 64-byte stage
+//   as v_mfma_i32_16x16x64_i8 operands instead (16 rows each, one 16-byte
+//   read per lane). Rows are padded to a multiple of the largest GEMM tile and KFp to
 //   a multiple of 8 fragments (256 bytes of K) with zeros.
 #pragma once
 
