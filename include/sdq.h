@@ -21,7 +21,7 @@
  *   acc[i,j] = sum_k aq[i,k] * Bq[j,k]             (exact int32)
  *   y[i,j]   = fl( fl((float)acc) * fl(sc_i * bs[j]) )
  *   bias:      y = fl(y + bias[j])
- *   epilogue:  GELU  y = gelu_tanh(y)               (tolerance, libm tanh)
+ *   epilogue:  GELU  y = gelu_tanh(y)               (tolerance: the reference uses libm tanh)
  *              GATED x[i,j] = fma(y, gate[j], x[i,j]) (or x + fl(y*gate))
  *              RESID x[i,j] = fl(x[i,j] + y)
  *

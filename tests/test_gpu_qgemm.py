@@ -270,8 +270,9 @@ def test_gated_residual_in_place(sdq_dev, oracle):
 
 @pytest.mark.parametrize("M,K,N", [(30, 3072, 14336), (200, 3072, 1000)])
 def test_gelu_epilogue_tolerance(sdq_dev, oracle, M, K, N):
-    """GELU uses the device tanhf; the reference uses libm tanh, so this one
-    is a tolerance check: max abs err <= 1e-6 * (1 + |y|)."""
+    """GELU runs as x / (1 + e^(-2u)) on the GPU's exp2 and reciprocal; the
+    reference uses libm tanh, so this one is a tolerance check:
+    max abs err <= 1e-6 * (1 + |y|)."""
     import sdq
 
     A, q, s, bias = _inputs(M, K, N, seed=M * 3 + N)
