@@ -402,6 +402,7 @@ sdpa_kernel(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ 
   // stash writes packed bf16x2 dwords, 32 distinct banks per half-wave.
   // Blocks past the end load zeros.
   constexpr int PER = (kKB * kHd / 4 + NT - 1) / NT;
+  static_assert(PER * NT == kKB * kHd / 4, "every lane stashes whole K row slots (half-wave rows)");
   constexpr int PERV = (kKB / 2 * kHd / 4 + NT - 1) / NT;
   float4 pk[PER], pv0[PERV], pv1[PERV];
   // stored position p (0..31) -> key: quads 1 and 2 of each 16 swapped
