@@ -286,6 +286,30 @@ def test_gelu_epilogue_tolerance(sdq_dev, oracle, M, K, N):
     assert_bitexact(pre, oracle.linear(A, q, s, bias=bias), "pre-gelu")
 
 
+@pytest.mark.parametrize("M,K,N", [(40, 3072, 1024), (300, 1024, 1024)])
+def test_gelu_epilogue_saturation(sdq_dev, oracle, M, K, N):
+    """GELU inputs driven into both saturations by large biases (|b| up to
+    1e6): within the tolerance of the reference's 0.5 x (1 + tanh(u)), with
+    the same sign of zero where that underflows (x < 0: -0.0), and y = x for
+    large x."""
+    import sdq
+
+    A, q, s, _ = _inputs(M, K, N, seed=4 * M + N)
+    levels = np.array([-1e6, -30.0, -8.0, -3.0, -1.0, 0.0, 1.0, 3.0, 8.0, 30.0, 1e6], np.float32)
+    bias = levels[np.arange(N) % levels.size]
+    w = sdq.Weight.from_host(q, s)
+    got = _run(sdq_dev, w, A, kind="gelu", bias=bias)
+    want = oracle.linear(A, q, s, bias=bias, epilogue="gelu")
+    assert np.isfinite(got).all()
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= 1e-6 * (1.0 + np.abs(want))), float(err.max())
+    zero = want == 0
+    assert np.array_equal(np.signbit(got[zero]), np.signbit(want[zero])), "sign of zero"
+    big = bias >= 30.0
+    pre = oracle.linear(A, q, s, bias=bias)
+    assert_bitexact(got[:, big], pre[:, big], "GELU(x) = x for large x")
+
+
 def test_k_zero_and_m_zero(sdq_dev, oracle):
     """K == 0 gives the reference's zero-filled out (+bias); M == 0 is a no-op."""
     import torch
