@@ -177,9 +177,9 @@ typedef struct sdq_group_item {
 #define SDQ_MAX_GROUP 16
 int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream);
 
-/* sdq_qlinear for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * No counterpart in the reference. The same results as sdq_qlinear, bit for
+/* sdq_qlinear for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Capturing it into a HIP graph is untested and unsupported. The same results as sdq_qlinear, bit for
  * bit, with no hipMalloc / hipFree or other allocation on any call: the
  * quantized activations and the GEMM's other scratch live in a static device
  * array of SDQ_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).

@@ -709,6 +709,96 @@ bool read_spans(int fd, const std::vector<ReadSpan>& spans, int threads) {
 
 namespace {
 
+// sdq_qlinear_host's staging, per host thread and device, grown and never
+// shrunk (held until the process ends): a device block for the call's
+// arrays, a stream of its own, and two pinned host buffers through which
+// host arrays move in chunks (the copy of one chunk into pinned memory
+// overlaps the DMA of the previous one).
+constexpr size_t kHostBounce = size_t(16) << 20;  // bytes per pinned buffer
+struct HostStage {
+  hipStream_t stream = nullptr;
+  char* dbuf = nullptr;
+  size_t dbytes = 0;
+  char* pin[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+};
+thread_local HostStage t_host_stage[kMaxDev];
+
+int host_stage_ready(HostStage& hs) {
+  hipError_t e = hipSuccess;
+  if (!hs.stream) {
+    e = hipStreamCreateWithFlags(&hs.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      hs.stream = nullptr;
+      return hip_error(e, "hipStreamCreate (host calls)");
+    }
+  }
+  for (int i = 0; i < 2; i++) {
+    if (!hs.pin[i]) {
+      void* p = nullptr;
+      e = hipHostMalloc(&p, kHostBounce, hipHostMallocDefault);
+      if (e != hipSuccess) return hip_error(e, "hipHostMalloc (host-call bounce)");
+      hs.pin[i] = static_cast<char*>(p);
+    }
+    if (!hs.done[i]) {
+      e = hipEventCreateWithFlags(&hs.done[i], hipEventDisableTiming);
+      if (e != hipSuccess) {
+        hs.done[i] = nullptr;
+        return hip_error(e, "hipEventCreate (host calls)");
+      }
+    }
+  }
+  return SDQ_OK;
+}
+
+// Host -> device through the pinned buffers. A buffer is refilled only
+// after the DMA that read it finished.
+int host_stage_h2d(HostStage& hs, char* dst, const void* src, size_t bytes) {
+  const char* p = static_cast<const char*>(src);
+  for (size_t off = 0, c = 0; off < bytes; off += kHostBounce, c++) {
+    const size_t len = bytes - off < kHostBounce ? bytes - off : kHostBounce;
+    const int b = (int)(c & 1);
+    hipError_t e = hipEventSynchronize(hs.done[b]);
+    if (e == hipSuccess) {
+      std::memcpy(hs.pin[b], p + off, len);
+      e = hipMemcpyAsync(dst + off, hs.pin[b], len, hipMemcpyHostToDevice, hs.stream);
+    }
+    if (e == hipSuccess) e = hipEventRecord(hs.done[b], hs.stream);
+    if (e != hipSuccess) return hip_error(e, "host-call H2D");
+  }
+  return SDQ_OK;
+}
+
+// Device -> host through the pinned buffers: chunk c's DMA is queued before
+// chunk c-1 is copied out of its pinned buffer.
+int host_stage_d2h(HostStage& hs, void* dst, const char* src, size_t bytes) {
+  char* q = static_cast<char*>(dst);
+  size_t prev_off = 0, prev_len = 0;
+  int prev_b = -1;
+  auto drain = [&]() {
+    if (prev_b < 0) return hipSuccess;
+    hipError_t e = hipEventSynchronize(hs.done[prev_b]);
+    if (e == hipSuccess) std::memcpy(q + prev_off, hs.pin[prev_b], prev_len);
+    prev_b = -1;
+    return e;
+  };
+  for (size_t off = 0, c = 0; off < bytes; off += kHostBounce, c++) {
+    const size_t len = bytes - off < kHostBounce ? bytes - off : kHostBounce;
+    const int b = (int)(c & 1);
+    // buffer b last held chunk c-2, copied out when chunk c-1 was queued
+    hipError_t e = hipMemcpyAsync(hs.pin[b], src + off, len, hipMemcpyDeviceToHost, hs.stream);
+    if (e == hipSuccess) e = hipEventRecord(hs.done[b], hs.stream);
+    if (e == hipSuccess) e = drain();
+    if (e != hipSuccess) return hip_error(e, "host-call D2H");
+    prev_off = off;
+    prev_len = len;
+    prev_b = b;
+  }
+  const hipError_t e = drain();
+  if (e != hipSuccess) return hip_error(e, "host-call D2H");
+  return SDQ_OK;
+}
+
 // Whether item `it` takes sdq_qlinear_group's shared launches: the plain
 // quantizer's single-kernel form and the 128x128 persistent GEMM without
 // split-K, the path sdq_qlinear itself would take for it.
@@ -932,6 +1022,35 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
     if (it.M < 0) return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": negative M");
     if (it.M > 0 && it.w->N > 0 && ((!it.A && it.w->K > 0) || !it.Y))
       return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": null A or Y");
+  }
+  // The items run in any order (the shared path quantizes every input before
+  // any GEMM), so no item's output may overlap another item's input,
+  // residual or output.
+  {
+    struct Span {
+      uintptr_t lo, hi;
+    };
+    auto span = [](const void* p, int64_t bytes) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+      return Span{a, a + (uintptr_t)(bytes > 0 ? bytes : 0)};
+    };
+    auto meet = [](Span a, Span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; };
+    for (int i = 0; i < n; i++) {
+      const sdq_group_item& a = items[i];
+      if (a.M == 0 || a.w->N == 0) continue;
+      const Span ya = span(a.Y, a.M * a.w->N * 4);
+      for (int j = 0; j < n; j++) {
+        const sdq_group_item& b = items[j];
+        if (j == i || b.M == 0 || b.w->N == 0) continue;
+        const bool clash = meet(ya, span(b.A, b.M * b.w->K * 4)) ||
+                           meet(ya, span(b.Y, b.M * b.w->N * 4)) ||
+                           (b.epi.resid && meet(ya, span(b.epi.resid, b.M * b.w->N * 4)));
+        if (clash)
+          return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) +
+                                                ": Y overlaps the input, residual or output of item " +
+                                                std::to_string(j));
+      }
+    }
   }
   if ((rc = ensure_device(dev))) return rc;
   const int cu_count = g_dev[dev].cu_count;
@@ -1263,41 +1382,52 @@ int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
   const int64_t N = w->N;
   if (M == 0 || N == 0) return SDQ_OK;
+  int dev = -1;
+  if ((rc = current_device(&dev))) return rc;
+  if ((rc = ensure_device(dev))) return rc;
+  HostStage& hs = t_host_stage[dev];
+  if ((rc = host_stage_ready(hs))) return rc;
   const size_t abytes = (size_t)(M * K) * 4, ybytes = (size_t)(M * N) * 4;
-  char* buf = nullptr;
-  // one block: A | Y | resid | bias | gate, each 256-byte aligned
+  // one device block: A | Y | resid | bias | gate, each 256-byte aligned
   auto al = [](size_t x) { return (x + 255) & ~size_t(255); };
   const bool has_resid = epi && epi->resid;
   const size_t o_y = al(abytes), o_r = o_y + al(ybytes), o_b = o_r + (has_resid ? al(ybytes) : 0);
   const size_t o_g = o_b + al((size_t)N * 4), total = o_g + al((size_t)N * 4);
-  hipError_t e = hipMalloc(&buf, total);
-  if (e != hipSuccess) return hip_error(e, "hipMalloc (host-call buffers)");
+  if (total > hs.dbytes) {
+    // the stage's stream is idle here (every call ends synchronized)
+    if (hs.dbuf) (void)hipFree(hs.dbuf);
+    hs.dbuf = nullptr;
+    hs.dbytes = 0;
+    hipError_t e = hipMalloc(&hs.dbuf, total);
+    if (e != hipSuccess) {
+      hs.dbuf = nullptr;
+      return hip_error(e, "hipMalloc (host-call buffers)");
+    }
+    hs.dbytes = total;
+  }
+  char* buf = hs.dbuf;
   sdq_epilogue de{};
   if (epi) de = *epi;
-  if (abytes) e = hipMemcpy(buf, A, abytes, hipMemcpyHostToDevice);
-  if (e == hipSuccess && has_resid) {
-    e = hipMemcpy(buf + o_r, epi->resid, ybytes, hipMemcpyHostToDevice);
+  rc = host_stage_h2d(hs, buf, A, abytes);
+  if (!rc && has_resid) {
+    rc = host_stage_h2d(hs, buf + o_r, epi->resid, ybytes);
     de.resid = reinterpret_cast<float*>(buf + o_r);
   }
-  if (e == hipSuccess && epi && epi->bias) {
-    e = hipMemcpy(buf + o_b, epi->bias, (size_t)N * 4, hipMemcpyHostToDevice);
+  if (!rc && epi && epi->bias) {
+    rc = host_stage_h2d(hs, buf + o_b, epi->bias, (size_t)N * 4);
     de.bias = reinterpret_cast<float*>(buf + o_b);
   }
-  if (e == hipSuccess && epi && epi->gate) {
-    e = hipMemcpy(buf + o_g, epi->gate, (size_t)N * 4, hipMemcpyHostToDevice);
+  if (!rc && epi && epi->gate) {
+    rc = host_stage_h2d(hs, buf + o_g, epi->gate, (size_t)N * 4);
     de.gate = reinterpret_cast<float*>(buf + o_g);
   }
-  if (e != hipSuccess) {
-    (void)hipFree(buf);
-    return hip_error(e, "hipMemcpy H2D");
-  }
-  rc = qlinear_device(w, reinterpret_cast<float*>(buf), M, K, epi ? &de : nullptr, buf + o_y,
-                      nullptr);
-  if (rc == SDQ_OK) {
-    e = hipMemcpy(Y, buf + o_y, ybytes, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) rc = hip_error(e, "hipMemcpy D2H");
-  }
-  (void)hipFree(buf);
+  if (!rc)
+    rc = qlinear_device(w, reinterpret_cast<float*>(buf), M, K, epi ? &de : nullptr, buf + o_y,
+                        hs.stream);
+  if (!rc) rc = host_stage_d2h(hs, Y, buf + o_y, ybytes);
+  // leave the stage idle whatever happened
+  const hipError_t e = hipStreamSynchronize(hs.stream);
+  if (!rc && e != hipSuccess) rc = hip_error(e, "hipStreamSynchronize (host call)");
   return rc;
 }
 

@@ -590,7 +590,10 @@ FilePart file_part(const PackIndex& ix, const std::string& base, int64_t in, int
   bool from_int8 = false;
   const PackEntry* sc = ix.f32_view(wn + ".scale", &from_int8);
   if (!sc) throw std::runtime_error("ovi_dit: missing tensor " + wn + ".scale");
-  if (!from_int8 || sc != w) throw std::runtime_error("ovi_dit: scale not packed after i8 for " + base);
+  // where the view's floats start, checked as lin() checks its pointers
+  const uint64_t sc_at = from_int8 ? sc->scale : sc->data;
+  if (sc_at != w->data + (uint64_t)w->numel)
+    throw std::runtime_error("ovi_dit: scale not packed after i8 for " + base);
   bool bias_scale = false;
   const PackEntry* b = ix.f32_view(base + ".bias", &bias_scale);
   if (!b) throw std::runtime_error("ovi_dit: missing tensor " + base + ".bias");

@@ -139,11 +139,15 @@ PackIndex PackIndex::read(const std::string& path) {
   const uint64_t base = in.offset(), avail = ix.size_ - base;
   for (const Row& r : rows)
     if (r.rel > avail || r.e.bytes > avail - r.rel) fail("data out of bounds");
+  ix.table_.reserve(rows.size());
   for (Row& r : rows) {
     r.e.data = base + r.rel;
     r.e.scale = r.e.kind == PackEntry::kInt8Rows ? r.e.data + (uint64_t)r.e.numel : 0;
-    if (ix.map_.emplace(r.name, std::move(r.e)).second)  // first of a repeated name wins
-      ix.order_.push_back(std::move(r.name));
+    if (r.e.kind == PackEntry::kInt8Rows)
+      ix.int8_first_.emplace(r.name, (uint32_t)ix.table_.size());
+    if (ix.map_.emplace(r.name, r.e).second)  // first of a repeated name wins
+      ix.order_.push_back(r.name);
+    ix.table_.emplace_back(std::move(r.name), std::move(r.e));
   }
   return ix;
 }
@@ -155,18 +159,18 @@ const PackEntry* PackIndex::find(const std::string& name) const {
 
 const PackEntry* PackIndex::f32_view(const std::string& name, bool* scale_of_int8) const {
   const PackEntry* raw = find(name);
-  if (raw && raw->kind != PackEntry::kF32) raw = nullptr;
   const PackEntry* q = nullptr;
   const std::string suffix = ".scale";
   if (name.size() > suffix.size() &&
       name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0) {
-    q = find(name.substr(0, name.size() - suffix.size()));
-    if (q && q->kind != PackEntry::kInt8Rows) q = nullptr;
+    auto it = int8_first_.find(name.substr(0, name.size() - suffix.size()));
+    if (it != int8_first_.end()) q = &table_[it->second].second;
   }
   // load_sdcpp emplaces views in table order: the earlier entry owns the name
   const bool use_q = q && (!raw || q->position < raw->position);
   if (scale_of_int8) *scale_of_int8 = use_q;
-  return use_q ? q : raw;
+  if (use_q) return q;
+  return raw && raw->kind == PackEntry::kF32 ? raw : nullptr;
 }
 
 std::vector<float> PackIndex::read_f32(const PackEntry& e, bool scales) const {
@@ -212,8 +216,7 @@ std::unordered_map<std::string, Tensor> load_sdcpp(const std::string& path,
     t.owning = false;
     return t;
   };
-  for (const std::string& name : ix.order()) {  // table order: the first view of a name wins
-    const PackEntry& e = *ix.find(name);
+  for (const auto& [name, e] : ix.table()) {  // table order: the first view of a name wins
     if (e.kind == PackEntry::kInt8Rows) {
       views.emplace(name, view(e.data, e.dims, DType::I8, (size_t)e.numel));
       views.emplace(name + ".scale", view(e.scale, {e.rows}, DType::F32, (size_t)e.rows * 4));

@@ -23,7 +23,11 @@ void check_rc(int rc, const char* what) {
   if (rc != SDQ_OK) throw std::runtime_error(std::string(what) + ": " + sdq_last_error());
 }
 
-// Device copies of (Bq, bs), keyed by the host views' addresses.
+// Device copies of (Bq, bs), keyed by the host views' addresses. A view's
+// address can be reused for other contents (a pack unmapped and another
+// mapped in its place, weights rewritten in place), so each entry also keeps
+// a fingerprint of the contents: all of bs and the first and last rows of
+// Bq. A changed fingerprint replaces the device copy.
 struct WeightKey {
   const void* q;
   const void* s;
@@ -32,22 +36,45 @@ struct WeightKey {
     return std::tie(q, s, N, K) < std::tie(o.q, o.s, o.N, o.K);
   }
 };
+struct CachedWeight {
+  sdq_weight* w;
+  uint64_t print;
+};
+
+uint64_t fnv1a(uint64_t h, const void* p, size_t n) {
+  const unsigned char* b = static_cast<const unsigned char*>(p);
+  for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 0x100000001b3ull;
+  return h;
+}
+
+uint64_t fingerprint(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t K) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  h = fnv1a(h, bs.data, (size_t)N * sizeof(float));
+  const int8_t* q = Bq.ptr<int8_t>();
+  h = fnv1a(h, q, (size_t)K);
+  return fnv1a(h, q + (N - 1) * K, (size_t)K);
+}
 
 std::mutex g_cache_mu;
-std::map<WeightKey, sdq_weight*>& cache() {
-  static std::map<WeightKey, sdq_weight*> m;
+std::map<WeightKey, CachedWeight>& cache() {
+  static std::map<WeightKey, CachedWeight> m;
   return m;
 }
 
 sdq_weight* cached_weight(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t K) {
+  const uint64_t print = fingerprint(Bq, bs, N, K);
   std::lock_guard<std::mutex> lk(g_cache_mu);
   WeightKey key{Bq.data, bs.data, N, K};
   auto it = cache().find(key);
-  if (it != cache().end()) return it->second;
+  if (it != cache().end()) {
+    if (it->second.print == print) return it->second.w;
+    sdq_weight_free(it->second.w);
+    cache().erase(it);
+  }
   sdq_weight* w = nullptr;
   check_rc(sdq_weight_upload(Bq.ptr<int8_t>(), bs.ptr<float>(), N, K, nullptr, &w),
            "qgemm: weight upload");
-  cache().emplace(key, w);
+  cache().emplace(key, CachedWeight{w, print});
   return w;
 }
 
@@ -55,7 +82,7 @@ sdq_weight* cached_weight(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t
 
 void qgemm_cache_clear() {
   std::lock_guard<std::mutex> lk(g_cache_mu);
-  for (auto& kv : cache()) sdq_weight_free(kv.second);
+  for (auto& kv : cache()) sdq_weight_free(kv.second.w);
   cache().clear();
 }
 

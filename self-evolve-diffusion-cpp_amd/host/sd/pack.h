@@ -44,10 +44,14 @@ class PackIndex {
   const std::unordered_map<std::string, PackEntry>& entries() const { return map_; }
   // Names in table order (a repeated name is listed once, at its first entry).
   const std::vector<std::string>& order() const { return order_; }
+  // Every entry in table order, repeated names included.
+  const std::vector<std::pair<std::string, PackEntry>>& table() const { return table_; }
   uint64_t file_size() const { return size_; }
-  // The F32 view load_sdcpp gives `name`: the raw entry, or the scales of the
-  // int8 entry `name` minus ".scale" (whichever comes first in the table);
-  // nullptr when neither exists. *scale_of_int8 tells which.
+  // The view load_sdcpp gives `name`, when it is an F32 one: the first entry
+  // called `name`, or the scales of the first int8 entry called `name` minus
+  // ".scale", whichever comes first in the table (the loader emplaces views in
+  // table order and the first view of a name wins); nullptr when neither
+  // exists or the winner is an int8 tensor. *scale_of_int8 tells which.
   const PackEntry* f32_view(const std::string& name, bool* scale_of_int8) const;
   // Reads a raw F32 entry's values (or an int8 entry's scales) from the file.
   std::vector<float> read_f32(const PackEntry& e, bool scales) const;
@@ -56,8 +60,10 @@ class PackIndex {
  private:
   std::string path_;
   uint64_t size_ = 0;
-  std::unordered_map<std::string, PackEntry> map_;
+  std::unordered_map<std::string, PackEntry> map_;       // first entry of each name
+  std::unordered_map<std::string, uint32_t> int8_first_;  // name -> table_ index
   std::vector<std::string> order_;
+  std::vector<std::pair<std::string, PackEntry>> table_;
 };
 
 // The reference's loader contract (src/serde/sdcpp.h:18-19): the file mapped

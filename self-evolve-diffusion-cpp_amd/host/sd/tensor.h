@@ -45,9 +45,12 @@ struct Tensor {
 //   out[i,j] = (float)(sum_k aq[i,k]*Bq[j,k]) * (as[i]*bs[j]) with the
 //   reference's per-row dynamic activation quantization — bit-identical.
 // Runs on the current HIP device (sdq_init). The device copy of (Bq, bs) is
-// uploaded and repacked once and cached by Bq.data: like the reference's
-// mmap views (src/model/ovi_dit.cpp:397-415) the weight bytes must not change
-// while cached (qgemm_cache_clear() drops the cache).
+// uploaded and repacked once and cached by (Bq.data, bs.data, N, K) plus a
+// fingerprint of the contents (all of bs, the first and last rows of Bq),
+// checked on every call: new contents at a cached address are uploaded
+// again. A change confined to Bq's middle rows is not seen, so a caller that
+// rewrites weights in place or releases a pack calls qgemm_cache_clear(),
+// which also frees the device copies.
 // Unlike the reference, shape mismatches throw std::runtime_error("qgemm: …")
 // instead of reading out of bounds; GPU failures throw too.
 void qgemm(const Tensor& A, const Tensor& Bq, const Tensor& bs, Tensor& out);

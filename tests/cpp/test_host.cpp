@@ -56,6 +56,20 @@ static int cmd_sdcpp(const std::string& path) {
   return 0;
 }
 
+// The F32 view PackIndex::f32_view resolves for `name`: its data offset, and
+// whether it is an int8 entry's scales.
+static int cmd_f32view(const std::string& path, const std::string& name) {
+  const PackIndex ix = PackIndex::read(path);
+  bool scales = false;
+  const PackEntry* e = ix.f32_view(name, &scales);
+  if (!e)
+    std::printf("none\n");
+  else
+    std::printf("%s %llu\n", scales ? "scales" : "f32",
+                (unsigned long long)(scales ? e->scale : e->data));
+  return 0;
+}
+
 static int cmd_sdcpp_err(const std::string& path) {
   try {
     std::shared_ptr<void> owner;
@@ -77,6 +91,7 @@ int main(int argc, char** argv) {
   try {
     if (cmd == "sdcpp" && argc == 3) return cmd_sdcpp(argv[2]);
     if (cmd == "sdcpp_err" && argc == 3) return cmd_sdcpp_err(argv[2]);
+    if (cmd == "f32view" && argc == 4) return cmd_f32view(argv[2], argv[3]);
     if (cmd == "qgemm" && argc == 9) {
       gpu::check(sdq_init(0), "sdq_init");
       const int64_t M = std::atoll(argv[2]), K = std::atoll(argv[3]), N = std::atoll(argv[4]);
@@ -93,8 +108,18 @@ int main(int argc, char** argv) {
         return 1;
       }
       std::printf("cache entries %zu\n", qgemm_cache_size());
+      // new contents at the same addresses (a pack mapped again in place):
+      // the cached device copy must be replaced, not reused
+      int8_t* q = Bq.ptr<int8_t>();
+      float* s = bs.ptr<float>();
+      for (int64_t i = 0; i < N * K; i++) q[i] = (int8_t)(-q[i]);
+      for (int64_t j = 0; j < N; j++) s[j] = 2.f * s[j];
+      Tensor out3;
+      qgemm(A, Bq, bs, out3);
+      std::printf("cache entries after rewrite %zu\n", qgemm_cache_size());
       qgemm_cache_clear();
       write_file(argv[8], out.data, out.nbytes);
+      write_file(std::string(argv[8]) + ".rewritten", out3.data, out3.nbytes);
       return 0;
     }
     if (cmd == "linear" && argc == 12) {

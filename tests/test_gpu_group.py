@@ -138,3 +138,33 @@ def test_group_raw_abi_errors(sdq_dev, oracle):
     arr[0].A = arr[0].Y = ctypes.c_void_p(16)
     assert lib.sdq_qlinear_group(arr, 1, None) == sdq.ERR_INVALID
     w.free()
+
+
+def test_group_rejects_overlapping_items(sdq_dev, oracle):
+    """One item's output over another item's input, residual or output is
+    refused before anything runs (the items run in any order); an item's own
+    residual may be its own output."""
+    import torch
+
+    import sdq
+
+    specs = [(96, 512, 512, "none", True), (96, 512, 256, "resid", True)]
+    items, host = _items(sdq, torch, oracle, sdq_dev, specs, 900)
+    before = [it["out"].clone() for it in items]
+    buf = torch.zeros((96, 512), device=sdq_dev)
+    # item 0 writes the buffer that item 1 reads as its input
+    items[0]["out"] = buf
+    items[1]["A"] = buf
+    with pytest.raises(sdq.SdqError) as ei:
+        sdq.qlinear_group(items)
+    assert "overlaps" in str(ei.value)
+    # item 1 writes into item 0's output (a view of the same storage)
+    items[0]["out"] = before[0].clone()
+    items[1]["A"] = torch.from_numpy(host[1]["A"]).to(sdq_dev)
+    items[1]["out"] = items[1]["resid"] = items[0]["out"].view(-1)[: 96 * 256].view(96, 256)
+    with pytest.raises(sdq.SdqError) as ei:
+        sdq.qlinear_group(items)
+    assert "overlaps" in str(ei.value)
+    torch.cuda.synchronize()
+    for it in items:
+        it["w"].free()

@@ -85,6 +85,58 @@ def test_sdcpp_reader_agrees_with_reference_loader(tmp_path, oracle, ref):
         assert r["count"] == len(got)
 
 
+def _raw_pack(path, entries):
+    """A .sdcpp v1 file from (name, code, array) in table order, repeated
+    names allowed (the format does not forbid them): code 0 = int8 rows
+    followed by one f32 scale per row, code 1 = f32."""
+    blobs, table, off = [], [], 0
+    for name, code, a in entries:
+        if code == 0:
+            rows = int(np.prod(a.shape[:-1]))
+            blob = a.astype(np.int8).tobytes() + np.arange(1, rows + 1, dtype=np.float32).tobytes()
+        else:
+            blob = a.astype(np.float32).tobytes()
+        nb = name.encode()
+        table.append(struct.pack("<I", len(nb)) + nb + struct.pack("<BI", code, a.ndim) +
+                     b"".join(struct.pack("<q", d) for d in a.shape) + struct.pack("<Q", off))
+        blobs.append(blob)
+        off += len(blob)
+    with open(path, "wb") as f:
+        f.write(b"SDCP" + struct.pack("<II", 1, len(entries)) + b"".join(table) + b"".join(blobs))
+
+
+def test_sdcpp_repeated_names_follow_reference_loader(tmp_path, ref):
+    """Repeated names: the reference's loader emplaces each entry's view and,
+    for int8 entries, its ".scale" view in table order, the first view of a
+    name winning (src/serde/sdcpp.cpp:107-131). The mirror's load_sdcpp and
+    PackIndex::f32_view must give the same view for every name."""
+    i8 = lambda *sh: (np.arange(int(np.prod(sh))) % 200 - 100).astype(np.int8).reshape(sh)  # noqa
+    f32 = lambda *sh: np.linspace(-1, 1, int(np.prod(sh)), dtype=np.float32).reshape(sh)  # noqa
+    entries = [
+        ("X", 1, f32(4)), ("X", 0, i8(3, 8)),              # X: the f32; X.scale: the int8's scales
+        ("Y.scale", 1, f32(2)), ("Y", 0, i8(2, 8)),        # Y.scale: the raw f32 (first)
+        ("Z", 0, i8(2, 8)), ("Z.scale", 1, f32(2)), ("Z", 1, f32(5)),  # Z: int8; Z.scale: scales
+        ("W.scale", 0, i8(2, 8)), ("W", 0, i8(2, 8)),      # W.scale: an int8 tensor
+        ("V", 0, i8(4, 8)), ("V", 0, i8(5, 8)),            # V and V.scale: the first int8
+    ]
+    p = str(tmp_path / "rep.sdcpp")
+    _raw_pack(p, entries)
+    got = listing(p)
+    names = sorted(got)
+    assert ref.sdcpp_lookup(p, "X")["count"] == len(got)
+    for name in names:
+        r = ref.sdcpp_lookup(p, name)
+        assert r is not None, name
+        assert (r["dtype"], r["dims"], r["data_off"]) == (
+            got[name]["code"], got[name]["dims"], got[name]["off"]), name
+        v = run("f32view", p, name).stdout.split()
+        if r["dtype"] == 0:  # DType::F32: the same bytes, raw or an int8 entry's scales
+            assert v[0] in ("f32", "scales") and int(v[1]) == r["data_off"], (name, v, r)
+        else:
+            assert v == ["none"], (name, v)
+    assert run("f32view", p, "nothing").stdout.split() == ["none"]
+
+
 def _corrupt(tmp_path, oracle, fn, tag):
     p = str(tmp_path / "c.sdcpp")
     make_pack(p, oracle)
@@ -193,6 +245,13 @@ def test_sd_qgemm_host_tensor_api(tmp_path, sdq_dev, oracle):
     assert "cache entries 1" in r.stdout
     got = np.fromfile(tmp_path / "o.bin", np.float32).reshape(M, N)
     assert_bitexact(got, oracle.qgemm(A, q, s), "sd::qgemm")
+    # the driver then rewrote Bq (negated) and bs (doubled) in place: the
+    # cache must notice and upload the new contents
+    assert "cache entries after rewrite 1" in r.stdout
+    got2 = np.fromfile(tmp_path / "o.bin.rewritten", np.float32).reshape(M, N)
+    assert_bitexact(got2, oracle.qgemm(A, (-q.astype(np.int16)).astype(np.int8),
+                                       (np.float32(2) * s).astype(np.float32)),
+                    "sd::qgemm after the weights changed in place")
 
 
 @pytest.mark.gpu
