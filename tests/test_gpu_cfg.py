@@ -8,12 +8,14 @@ run both ways on small widths: two separate passes, and one stacked pass
 (sd_dit_block_step_forward_batched: every Linear, norm and residual on the
 stacked rows, the attention inside each half; the SLG layer on the
 conditional half alone). The stacked pass must reproduce both passes bit for
-bit."""
+bit, and each half must equal the oracle's layer loop for its pass (the
+unconditional one skipping the SLG layer) with the GPU's sdpa and fc1 + GELU
+substituted, the two steps that are not bit-exact by construction."""
 import numpy as np
 import pytest
 
 from conftest import assert_bitexact
-from test_gpu_block_full import _norms, _weights
+from test_gpu_block_full import _gpu_fc1_gelu, _gpu_sdpa, _norms, _ref_block, _weights
 
 pytestmark = pytest.mark.gpu
 
@@ -71,20 +73,25 @@ def test_cfg_stacked_pass_equals_two_passes(sdq_dev, oracle, slg):
     dim, ffn, heads, L = 256, 512, 2, 3
     Mv, Ma, Mc = 64, 20, 16
     print(f"[cfg] layers={L} slg={slg} Mv={Mv} Ma={Ma}", flush=True)
-    layers = []
+    layers, host = [], []
     for i in range(L):
-        pair = []
+        pair, hpair = [], []
         for j in range(2):
-            blk = sdq.DitBlock(_weights(oracle, dim, ffn, 1000 + 100 * i + 50 * j, True), True)
-            blk.set_norms(_norms(oracle, dim, 3000 + 100 * i + 50 * j))
+            lin = _weights(oracle, dim, ffn, 1000 + 100 * i + 50 * j, True)
+            nm = _norms(oracle, dim, 3000 + 100 * i + 50 * j)
+            blk = sdq.DitBlock(lin, True)
+            blk.set_norms(nm)
             pair.append(blk)
+            hpair.append((lin, nm))
         layers.append(tuple(pair))
+        host.append(tuple(hpair))
     dv = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(sdq_dev)  # noqa
     r = lambda n, s: oracle.randn(n * dim, s).reshape(n, dim)  # noqa: E731
     xv0, xa0 = r(Mv, 1), r(Ma, 2)
     ctx = {k: r(Mc, 10 + i) for i, k in enumerate(("v_pos", "a_pos", "v_neg", "a_neg"))}
-    ev = [dv((oracle.randn(6 * dim, 20 + i) * np.float32(0.3)).reshape(6, dim)) for i in range(L)]
-    ea = [dv((oracle.randn(6 * dim, 30 + i) * np.float32(0.3)).reshape(6, dim)) for i in range(L)]
+    hev = [(oracle.randn(6 * dim, 20 + i) * np.float32(0.3)).reshape(6, dim) for i in range(L)]
+    hea = [(oracle.randn(6 * dim, 30 + i) * np.float32(0.3)).reshape(6, dim) for i in range(L)]
+    ev, ea = [dv(e) for e in hev], [dv(e) for e in hea]
     cs_v = sdq.rope_table_3d(1, Mv // 4, 4)
     cs_a = sdq.rope_table_1d(Ma, 128, 10000.0, 0.19676)
 
@@ -109,6 +116,25 @@ def test_cfg_stacked_pass_equals_two_passes(sdq_dev, oracle, slg):
     assert_bitexact(ga[Ma:], sep["neg"][1], "audio, unconditional half")
     # the halves did diverge (different contexts, and SLG when on)
     assert np.abs(sep["pos"][0] - sep["neg"][0]).max() > 1e-2
+    # each half against the oracle's layer loop for its own pass
+    gsd = _gpu_sdpa(sdq_dev)
+    fc1 = [(_gpu_fc1_gelu(lv), _gpu_fc1_gelu(la)) for (lv, _), (la, _) in host]
+    for half, vk, ak, skip in ((0, "v_pos", "a_pos", -1), (1, "v_neg", "a_neg", slg)):
+        xv, xa = xv0, xa0
+        for i, ((lv, nv), (la, na)) in enumerate(host):
+            if i == skip:
+                continue  # skip-layer guidance, ovi_dit.cpp:713
+            kv = dict(sdpa=gsd, fc1_gelu=fc1[i][0])
+            ka = dict(sdpa=gsd, fc1_gelu=fc1[i][1])
+            xa1 = _ref_block(oracle, xa, ctx[ak], hea[i], la, na, heads, cs_a, True, phases=1, **ka)
+            xv1 = _ref_block(oracle, xv, ctx[vk], hev[i], lv, nv, heads, cs_v, True, phases=1, **kv)
+            xa = _ref_block(oracle, xa1, ctx[ak], hea[i], la, na, heads, cs_a, True, xv1, cs_v, 2,
+                            **ka)
+            xv = _ref_block(oracle, xv1, ctx[vk], hev[i], lv, nv, heads, cs_v, True, xa1, cs_a, 2,
+                            **kv)
+        tag = "conditional" if half == 0 else f"unconditional (SLG layer {slg})"
+        assert_bitexact(gv[half * Mv:(half + 1) * Mv], xv, f"video, {tag} half vs the oracle")
+        assert_bitexact(ga[half * Ma:(half + 1) * Ma], xa, f"audio, {tag} half vs the oracle")
     for pair in layers:
         for b in pair:
             b.free()

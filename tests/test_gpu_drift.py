@@ -1,21 +1,26 @@
-"""Drift of the whole twin backbone over several fusion layers at the real
-widths (dim 3072, FFN 14336, 24 heads; video 768 tokens on the 3x16x16 grid,
-audio 157 tokens, text contexts of 512 rows), the layer loop of
-OviDit::forward (ovi_dit.cpp:712-739).
+"""Drift of the whole twin backbone over the model's 30 fusion layers
+(OviDitCfg, ovi_dit.cpp:326-334) at the real widths (dim 3072, FFN 14336,
+24 heads; video 768 tokens on the 3x16x16 grid, audio 157 tokens, text
+contexts of 512 rows), the layer loop of OviDit::forward (ovi_dit.cpp:712-739).
 
 Two chains run beside the GPU's, layer by layer:
-  * the reference chain: every step of the reference block, computed by the
-    reference's own compiled functions (oracle/_ref: sd::qgemm, sdpa,
-    layernorm, mod_rows, rmsnorm; bit-identical to the oracle's restatement,
-    which the CPU suite pins) plus the oracle's elementwise steps;
-  * the same chain with its sdpa and fc1 + GELU steps replaced by the GPU's
-    own kernels (the two steps that are not bit-exact by construction): the
-    GPU must match it bit for bit after every layer, which pins the order
-    and wiring of every other step across layers.
+  * the reference chain, all 30 layers: every step of the reference block,
+    computed by the reference's own compiled functions (oracle/_ref:
+    sd::qgemm, sdpa, layernorm, mod_rows, rmsnorm; bit-identical to the
+    oracle's restatement, which the CPU suite pins) plus the oracle's
+    elementwise steps;
+  * for the first EXACT layers, the same chain with its sdpa and fc1 + GELU
+    steps replaced by the GPU's own kernels (the two steps that are not
+    bit-exact by construction): the GPU must match it bit for bit after each
+    of those layers, which pins the order and wiring of every other step.
 Against the reference chain the GPU is gated like the reference's own int8
-DiT test (tests/test_ovit8.cpp:113-122: cosine > 0.99); the per-layer cosine
-and max relative error are printed and bounded, so their growth over the
-layers is measured."""
+DiT test (tests/test_ovit8.cpp:113-122: cosine > 0.99) and by tighter bounds
+on the per-layer cosine and max relative error, set from the measured 30-layer
+run (recorded in profiles/twin_drift_30_layers.md). Each layer has its own
+modulation rows and norm vectors; the int8 Linear weights come from NSETS
+seeded sets per branch, cycled over the layers (generating 60 blocks of real
+width weights would take minutes). SDQ_DRIFT_REPORT=<path> writes the
+per-layer report as JSON."""
 import numpy as np
 import pytest
 
@@ -67,12 +72,23 @@ def _cos(a, b):
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
 
 
+# Bounds against the reference chain, from the measured 30-layer run: the max
+# relative error (to the chain's max |x|) peaks at 0.024 (layer 1) and then
+# falls to ~0.010 as the residual stream grows (max |x| 43 -> 346); cosine
+# stays >= 0.99994. Both runs are deterministic, so the bounds keep ~1.5x
+# headroom only.
+ERR_BOUND, COS_BOUND = 0.035, 0.9999
+
+
 def test_twin_backbone_drift_real_width(sdq_dev, oracle, ref):
+    import json
+    import os
+
     import torch
 
     import sdq
 
-    dim, ffn, heads, L = 3072, 14336, 24, 4
+    dim, ffn, heads, L, NSETS, EXACT = 3072, 14336, 24, 30, 2, 3
     Mv, Ma, Mc = 768, 157, 512
     print(f"[drift] {L} fusion layers, video {Mv} / audio {Ma} tokens, dim {dim}", flush=True)
     ops = _RefOps(oracle, ref)
@@ -87,14 +103,18 @@ def test_twin_backbone_drift_real_width(sdq_dev, oracle, ref):
     g_ctx_v, g_ctx_a, g_cs_v, g_cs_a = dv(ctx_v), dv(ctx_a), dv(cs_v), dv(cs_a)
     want_v, want_a, ex_v, ex_a = xv0, xa0, xv0, xa0
     gsd = _gpu_sdpa(sdq_dev)
+    sets = []
+    for k in range(NSETS):
+        lv = _weights(oracle, dim, ffn, 1000 + 100 * k, True)
+        la = _weights(oracle, dim, ffn, 5000 + 100 * k, True)
+        sets.append((lv, la, sdq.DitBlock(lv, True), sdq.DitBlock(la, True)))
+        print(f"  weight set {k} uploaded", flush=True)
     report = []
     for i in range(L):
         ev = (oracle.randn(6 * dim, 100 + i) * np.float32(0.3)).reshape(6, dim)
         ea = (oracle.randn(6 * dim, 200 + i) * np.float32(0.3)).reshape(6, dim)
-        lv = _weights(oracle, dim, ffn, 1000 + 100 * i, True)
-        la = _weights(oracle, dim, ffn, 5000 + 100 * i, True)
+        lv, la, bv, ba = sets[i % NSETS]
         nv, na = _norms(oracle, dim, 300 + i), _norms(oracle, dim, 400 + i)
-        bv, ba = sdq.DitBlock(lv, True), sdq.DitBlock(la, True)
         bv.set_norms(nv)
         ba.set_norms(na)
         # the GPU: fusion layer order (ovi_dit.cpp:726-734)
@@ -106,10 +126,8 @@ def test_twin_backbone_drift_real_width(sdq_dev, oracle, ref):
         bv.step(gxv, g_ctx_v, dv(ev), heads, cs=g_cs_v, target=og_a, cs_tgt=g_cs_a,
                 phases=sdq.CROSS_FFN)
         torch.cuda.synchronize()
-        bv.free()
-        ba.free()
-        # the two CPU chains, same order
-        for kind in ("want", "exact"):
+        # the CPU chains, same order
+        for kind in (("want", "exact") if i < EXACT else ("want",)):
             xv, xa = (want_v, want_a) if kind == "want" else (ex_v, ex_a)
             kw_a = kw_v = {}
             if kind == "exact":
@@ -124,16 +142,25 @@ def test_twin_backbone_drift_real_width(sdq_dev, oracle, ref):
             else:
                 ex_v, ex_a = xv2, xa2
         got_v, got_a = gxv.cpu().numpy(), gxa.cpu().numpy()
-        assert_bitexact(got_v, ex_v, f"layer {i} video vs the chain with the GPU's sdpa and GELU")
-        assert_bitexact(got_a, ex_a, f"layer {i} audio vs the chain with the GPU's sdpa and GELU")
+        if i < EXACT:
+            assert_bitexact(got_v, ex_v, f"layer {i} video vs the chain with the GPU's sdpa and GELU")
+            assert_bitexact(got_a, ex_a, f"layer {i} audio vs the chain with the GPU's sdpa and GELU")
         row = {"layer": i}
         for name, g, w in (("video", got_v, want_v), ("audio", got_a, want_a)):
             err = np.abs(g.astype(np.float64) - w) / (np.abs(w).max() + 1e-30)
-            row[name] = (round(_cos(g, w), 8), float(f"{err.max():.3e}"))
+            row[name] = (round(_cos(g, w), 8), float(f"{err.max():.3e}"),
+                         float(f"{np.abs(w).max():.4e}"))
         report.append(row)
-        print(f"  layer {i}: cosine / max rel err vs the reference chain: "
+        print(f"  layer {i}: cosine / max rel err / max |x| vs the reference chain: "
               f"video {row['video']}, audio {row['audio']}", flush=True)
         for name in ("video", "audio"):
-            cos, err = row[name]
+            cos, err, _ = row[name]
             assert cos > 0.99, (i, name, cos)  # the reference's own int8 DiT gate
-            assert err < 0.1, (i, name, err)
+            assert cos > COS_BOUND and err < ERR_BOUND, (i, name, cos, err)
+    for _, _, bv, ba in sets:
+        bv.free()
+        ba.free()
+    out = os.environ.get("SDQ_DRIFT_REPORT")
+    if out:
+        with open(out, "w") as f:
+            json.dump(report, f, indent=1)
