@@ -52,6 +52,13 @@ def parse():
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="read rocprofv3 --pmc output directories (FETCH_SIZE, WRITE_SIZE, "
                          "MFMA busy, L2 hit passes of --profile-pass) and write --counters-json")
+    ap.add_argument("--kernel-counters", nargs="+", metavar="DIR",
+                    help="read rocprofv3 --pmc output directories of any bench.py run and print "
+                         "per-kernel means (dispatches, FETCH_SIZE / WRITE_SIZE in bytes with the "
+                         "--calibrate copy's scale, MFMA busy fraction, duration) as JSON")
+    ap.add_argument("--calibrate", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="--kernel-counters: FETCH_SIZE and WRITE_SIZE runs of --profile-pass, "
+                         "whose 1 GiB copy gives the bytes-per-KiB scale of each counter")
     ap.add_argument("--config", default="ns",
                     choices=["ns", "block", "blockfull", "ffn", "cross", "twin", "load"],
                     help="ns: the north-star qGEMM (the driver's bench line); block: one DiT "
@@ -643,6 +650,9 @@ def cpu_baseline(args, K, N):
 
 def main():
     args = parse()
+    if args.kernel_counters:
+        kernel_counters(args)
+        return
     if args.summarize_counters:
         summarize_counters(args)
         return
@@ -812,6 +822,61 @@ def _short_kernel(name):
     if "copyBuffer" in name:  # the runtime's device-to-device copy (the 1 GiB calibration)
         return "copy"
     return None
+
+
+def _counter_rows(dirs):
+    """(kernel name without arguments, counter) -> per-dispatch values, and
+    kernel name -> per-dispatch durations in us, from rocprofv3 --pmc CSVs."""
+    import csv
+    import glob
+
+    vals, dur = {}, {}
+    for d in dirs:
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(fn, newline="") as f:
+                for row in csv.DictReader(f):
+                    name = row["Kernel_Name"].replace("(anonymous namespace)::", "")
+                    name = name.replace("void ", "").split("(")[0]
+                    vals.setdefault((name, row["Counter_Name"]), []).append(
+                        float(row["Counter_Value"]))
+                    if row.get("Start_Timestamp") and row.get("End_Timestamp"):
+                        key = (name, row["Dispatch_Id"])
+                        dur[key] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+    per = {}
+    for (name, _), us in dur.items():
+        per.setdefault(name, []).append(us)
+    return vals, per
+
+
+def kernel_counters(args):
+    """Per-kernel means of rocprofv3 --pmc runs of any bench.py config:
+    FETCH_SIZE and WRITE_SIZE scaled to bytes by the --profile-pass copy
+    (see summarize_counters), the MFMA busy fraction over the kernel's active
+    cycles, and the mean duration under the profiler (kernels serialized)."""
+    vals, dur = _counter_rows(args.kernel_counters)
+    scale = {}
+    if args.calibrate:
+        for d, c in zip(args.calibrate, ("FETCH_SIZE", "WRITE_SIZE")):
+            cv, _ = _counter_rows([d])
+            copy = [v for (k, cc), v in cv.items() if "copyBuffer" in k and cc == c]
+            if copy:
+                scale[c] = (1 << 30) / (max(copy[0]) * 1024)
+    mean = lambda v: sum(v) / len(v)  # noqa: E731
+    names = sorted({k for k, _ in vals})
+    out = {"calibration": scale, "kernels": {}}
+    for k in names:
+        kc = {"dispatches": max(len(v) for (kk, _), v in vals.items() if kk == k)}
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            if (k, c) in vals and c in scale:
+                kc[c.lower().replace("_size", "_bytes")] = round(mean(vals[(k, c)]) * 1024 * scale[c])
+        busy, act = vals.get((k, "SQ_VALU_MFMA_BUSY_CYCLES")), vals.get((k, "GRBM_GUI_ACTIVE"))
+        if busy and act:
+            # GRBM_GUI_ACTIVE is summed over the 8 XCDs; 256 CUs x 4 SIMDs
+            kc["mfma_busy_frac"] = round(mean(busy) / ((mean(act) / 8) * 256 * 4), 4)
+        if k in dur:
+            kc["us_mean"] = round(mean(dur[k]), 2)
+        out["kernels"][k] = kc
+    print(json.dumps(out, indent=1))
 
 
 def summarize_counters(args):
