@@ -177,6 +177,35 @@ typedef struct sdq_group_item {
 #define SDQ_MAX_GROUP 16
 int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream);
 
+/* One DiT block's linear stack when every Linear's input is already there
+ * (the attention output, the cross-attention output and the normalized
+ * tokens given, as in ovi_dit.cpp:176-222 with the tensors between the
+ * Linears as inputs): items[0..ngroup) are independent (as for
+ * sdq_qlinear_group), items[ngroup..n) run after them in the given order
+ * (e.g. the cross output projection into the x the self-attention output
+ * projection just updated), then the FFN when `ffn` is not NULL (as
+ * sdq_ffn). Same results as those calls made one after the other, bit for
+ * bit; the difference is that every input (the items' A and the FFN's h) is
+ * quantized by one launch before any GEMM runs. So no output (an item's Y,
+ * the FFN's hid or x) may overlap any of those inputs, and no output of the
+ * first ngroup items may overlap another of their outputs or residuals
+ * (SDQ_ERR_INVALID). Replaces: the separate mlin calls of block_self_fwd,
+ * fusion_cross_ffn and ffn_fwd (ovi_dit.cpp:176-222). */
+typedef struct sdq_ffn_item {
+  const sdq_weight* fc1; /* [F, D] */
+  const float* b1;       /* [F] or NULL */
+  const sdq_weight* fc2; /* [D, F] */
+  const float* b2;       /* [D] or NULL */
+  const float* h;        /* [M, D] */
+  int64_t M;
+  const float* gate;     /* [D] */
+  int gate_fma;
+  float* hid;            /* [M, F] (written) */
+  float* x;              /* [M, D] updated in place */
+} sdq_ffn_item;
+int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_ffn_item* ffn,
+                      void* stream);
+
 /* sdq_qlinear for callers that cannot allocate device memory (tight serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
  * Capturing it into a HIP graph is untested and unsupported. The same results as sdq_qlinear, bit for

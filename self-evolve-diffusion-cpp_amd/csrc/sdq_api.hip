@@ -821,6 +821,29 @@ bool groupable(const sdq_group_item& it, int cu_count) {
   return w->KFp * 1024 * 8 <= 0x7FFFFFFF && N * 4 * 256 <= 0x7FFFFFF0;
 }
 
+// Whether a Linear of sdq_qlinear_stack can run from an input quantized by
+// the stack's shared launch: one persistent launch of the tile config
+// qlinear_device would choose, without split-K, whose quantizer would be the
+// single-kernel form (the shared launch runs that form's per-unit code),
+// with the vector epilogue. *cfg: that tile config.
+bool stackable(const sdq_weight* w, int64_t M, int kind, const void* Y, const float* bias,
+               const float* gate, const float* resid, int cu_count, int* cfg) {
+  if (kind != SDQ_EPI_NONE && kind != SDQ_EPI_GELU && kind != SDQ_EPI_GATED &&
+      kind != SDQ_EPI_RESID)
+    return false;
+  const int64_t N = w->N;
+  if (w->K == 0 || M <= 0 || M > (int64_t(1) << 30) || N % 4 != 0) return false;
+  const int c = choose_gemm_cfg(M, N, w->KFp, kind, cu_count);
+  if (c != kCfg128x128 && c != kCfg256x256) return false;
+  if (choose_splitk(c, M, N, w->KFp, cu_count) != 1) return false;
+  if (act_quant_pmax_floats(round_up(M, gemm_cfg_bm(c)), w->KFp, cu_count) != 0) return false;
+  if (!aligned16(Y) || (bias && !aligned16(bias)) || (gate && !aligned16(gate)) ||
+      (resid && !aligned16(resid)))
+    return false;
+  *cfg = c;
+  return w->KFp * 1024 * 8 <= 0x7FFFFFFF && N * 4 * 256 <= 0x7FFFFFF0;
+}
+
 // Items that may share one GEMM launch: the same k-fragments (the launch
 // reads each problem's epilogue form from its table).
 bool same_group(const sdq_group_item& a, const sdq_group_item& b) {
@@ -1168,6 +1191,292 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
     const sdq_group_item& it = items[i];
     if ((rc = qlinear_device(it.w, it.A, it.M, it.w->K, &it.epi, it.Y, s))) return rc;
   }
+  return SDQ_OK;
+}
+
+int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_ffn_item* ffn,
+                      void* stream) {
+  if (n < 0 || n > SDQ_MAX_GROUP) return set_error(SDQ_ERR_INVALID, "stack: n must be 0..16");
+  if (ngroup < 0 || ngroup > n) return set_error(SDQ_ERR_INVALID, "stack: need 0 <= ngroup <= n");
+  if (n > 0 && !items) return set_error(SDQ_ERR_INVALID, "stack: null items");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  for (int i = 0; i < n; i++) {
+    const sdq_group_item& it = items[i];
+    const std::string tag = "stack item " + std::to_string(i);
+    if (!it.w) return set_error(SDQ_ERR_INVALID, tag + ": null weight");
+    if ((rc = check_weight(it.w, it.w->K))) return rc;
+    if ((rc = validate_epi(&it.epi))) return rc;
+    if (it.M < 0) return set_error(SDQ_ERR_INVALID, tag + ": negative M");
+    if (it.M > 0 && it.w->N > 0 && ((!it.A && it.w->K > 0) || !it.Y))
+      return set_error(SDQ_ERR_INVALID, tag + ": null A or Y");
+  }
+  const bool has_ffn = ffn && ffn->M != 0;
+  if (ffn) {
+    if (!ffn->fc1 || !ffn->fc2) return set_error(SDQ_ERR_INVALID, "stack: null FFN weight");
+    if ((rc = check_weight(ffn->fc1, ffn->fc1->K)) || (rc = check_weight(ffn->fc2, ffn->fc2->K)))
+      return rc;
+    if (ffn->fc2->K != ffn->fc1->N || ffn->fc2->N != ffn->fc1->K)
+      return set_error(SDQ_ERR_INVALID, "stack: need fc1 [F,D] and fc2 [D,F]");
+    if (ffn->M < 0) return set_error(SDQ_ERR_INVALID, "stack: negative FFN M");
+    if (has_ffn && ((!ffn->h && ffn->fc1->K > 0) || !ffn->gate || !ffn->hid || !ffn->x))
+      return set_error(SDQ_ERR_INVALID, "stack: null FFN h, gate, hid or x");
+  }
+  // Every input is quantized before any GEMM runs: no output may overlap
+  // one. The first ngroup items run in any order among themselves.
+  {
+    struct Span {
+      uintptr_t lo, hi;
+      int who;
+    };
+    auto span = [](const void* p, int64_t bytes, int who) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+      return Span{a, a + (uintptr_t)(bytes > 0 ? bytes : 0), who};
+    };
+    auto meet = [](Span a, Span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; };
+    std::vector<Span> ins, outs;
+    for (int i = 0; i < n; i++) {
+      const sdq_group_item& it = items[i];
+      if (it.M == 0 || it.w->N == 0) continue;
+      ins.push_back(span(it.A, it.M * it.w->K * 4, i));
+      outs.push_back(span(it.Y, it.M * it.w->N * 4, i));
+    }
+    if (has_ffn) {
+      const int64_t D = ffn->fc1->K, F = ffn->fc1->N;
+      ins.push_back(span(ffn->h, ffn->M * D * 4, n));
+      outs.push_back(span(ffn->hid, ffn->M * F * 4, n));
+      outs.push_back(span(ffn->x, ffn->M * D * 4, n));
+    }
+    auto who = [&](int i) { return i == n ? std::string("the FFN") : "item " + std::to_string(i); };
+    for (const Span& o : outs)
+      for (const Span& a : ins)
+        if (meet(o, a))
+          return set_error(SDQ_ERR_INVALID, "stack: an output of " + who(o.who) +
+                                                " overlaps the input of " + who(a.who) +
+                                                " (every input is quantized first)");
+    for (int i = 0; i < ngroup; i++) {
+      const sdq_group_item& a = items[i];
+      if (a.M == 0 || a.w->N == 0) continue;
+      const Span ya = span(a.Y, a.M * a.w->N * 4, i);
+      for (int j = 0; j < ngroup; j++) {
+        const sdq_group_item& b = items[j];
+        if (j == i || b.M == 0 || b.w->N == 0) continue;
+        if (meet(ya, span(b.Y, b.M * b.w->N * 4, j)) ||
+            (b.epi.resid && meet(ya, span(b.epi.resid, b.M * b.w->N * 4, j))))
+          return set_error(SDQ_ERR_INVALID, "stack: grouped item " + std::to_string(i) +
+                                                " writes the output or residual of item " +
+                                                std::to_string(j));
+      }
+    }
+  }
+  if ((rc = ensure_device(dev))) return rc;
+  const int cu_count = g_dev[dev].cu_count;
+  // The shared-launch plan: every input through the segmented quantizer,
+  // each GEMM as the launch its own call would make, minus its quantizer.
+  std::vector<int> cfgs(n, -1);
+  int nseg = 0, cfg1 = -1;
+  bool fast = true;
+  for (int i = 0; i < n && fast; i++) {
+    const sdq_group_item& it = items[i];
+    if (it.M == 0 || it.w->N == 0) continue;
+    nseg++;
+    if (i < ngroup) {
+      fast = groupable(it, cu_count);
+      cfgs[i] = kCfg128x128;
+    } else {
+      fast = stackable(it.w, it.M, it.epi.kind, it.Y, it.epi.bias, it.epi.gate, it.epi.resid,
+                       cu_count, &cfgs[i]);
+    }
+  }
+  if (has_ffn && fast) {
+    nseg++;
+    fast = stackable(ffn->fc1, ffn->M, SDQ_EPI_GELU, ffn->hid, ffn->b1, nullptr, nullptr, cu_count,
+                     &cfg1);
+  }
+  if (!fast || nseg < 2 || nseg > kMaxQuantSegs) {
+    // the same calls, one after another
+    if (ngroup > 0 && (rc = sdq_qlinear_group(items, ngroup, stream))) return rc;
+    for (int i = ngroup; i < n; i++) {
+      const sdq_group_item& it = items[i];
+      if ((rc = qlinear_device(it.w, it.A, it.M, it.w->K, &it.epi, it.Y, s))) return rc;
+    }
+    if (has_ffn)
+      return ffn_device(ffn->fc1, ffn->b1, ffn->fc2, ffn->b2, ffn->h, ffn->M, ffn->gate,
+                        ffn->gate_fma, ffn->hid, ffn->x, s, nullptr);
+    return SDQ_OK;
+  }
+  // scratch: per input its quantized rows (padded to its GEMM's tile), row
+  // scales and padded column copies
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (size_t)round_up((int64_t)bytes, 256);
+    return o;
+  };
+  const size_t sink_off = take(4096);
+  struct Carve {
+    size_t at, as, cols;
+    int seg;
+  };
+  std::vector<Carve> cv(n + 1, Carve{0, 0, 0, -1});
+  struct Input {
+    const sdq_weight* w;
+    const float* A;
+    int64_t M;
+    int cfg;
+    const float* bias;
+    const float* gate;
+  };
+  std::vector<Input> in;
+  std::vector<int> owner;  // item index (n: the FFN's fc1) of each segment
+  for (int i = 0; i < n; i++) {
+    const sdq_group_item& it = items[i];
+    if (it.M == 0 || it.w->N == 0) continue;
+    in.push_back(Input{it.w, it.A, it.M, cfgs[i], it.epi.bias, it.epi.gate});
+    owner.push_back(i);
+  }
+  if (has_ffn) {
+    in.push_back(Input{ffn->fc1, ffn->h, ffn->M, cfg1, ffn->b1, nullptr});
+    owner.push_back(n);
+  }
+  for (size_t j = 0; j < in.size(); j++) {
+    const int64_t Mp = round_up(in[j].M, gemm_cfg_bm(in[j].cfg));
+    Carve& c = cv[owner[j]];
+    c.at = take((size_t)(Mp / kFragRows) * (size_t)in[j].w->KFp * kFragBytes);
+    c.as = take((size_t)Mp * sizeof(float));
+    c.cols = take((size_t)(in[j].w->Np + kColPad) * 2 * sizeof(float));
+    c.seg = (int)j;
+  }
+  char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace& ws = g_ws[{dev, s}];
+    if ((rc = grow(s, reinterpret_cast<void**>(&ws.grp), &ws.grp_bytes, off))) return rc;
+    base = ws.grp;
+  }
+  float* sink = reinterpret_cast<float*>(base + sink_off);
+  QuantSegs qs{};
+  qs.count = (int)in.size();
+  int64_t units = 0;
+  for (size_t j = 0; j < in.size(); j++) {
+    const Input& x = in[j];
+    const Carve& c = cv[owner[j]];
+    const int64_t Mp = round_up(x.M, gemm_cfg_bm(x.cfg));
+    const int64_t cap = x.w->Np + kColPad;
+    QuantSeg& q = qs.s[j];
+    q.A = x.A;
+    q.M = x.M;
+    q.K = x.w->K;
+    q.KFp = x.w->KFp;
+    q.vec = (aligned16(x.A) && x.w->K % 4 == 0) ? 1 : 0;
+    q.at = reinterpret_cast<int8_t*>(base + c.at);
+    q.as = reinterpret_cast<float*>(base + c.as);
+    float* cols = reinterpret_cast<float*>(base + c.cols);
+    q.cc.bias = x.bias;
+    q.cc.gate = x.gate;
+    q.cc.bias_pad = x.bias ? cols : nullptr;
+    q.cc.gate_pad = x.gate ? cols + cap : nullptr;
+    q.cc.N = x.w->N;
+    q.cc.CP = cap;
+    q.unit0 = units;
+    units += Mp / 8;  // the quantizer's 8-row units
+  }
+  qs.total = units;
+  std::vector<hipEvent_t> marks;
+  auto mark = [&]() {
+    if (t_prof) marks.push_back(prof_mark(s));
+  };
+  mark();
+  hipError_t e = launch_act_quant_segs(qs, s);
+  if (e != hipSuccess) return hip_error(e, "stack act_quant launch");
+  mark();
+  // the independent items: one grouped launch per set with the same K
+  std::vector<bool> done(n, false);
+  for (int j = 0; j < ngroup; j++) {
+    if (done[j] || cv[j].seg < 0) continue;
+    GemmGroup g{};
+    const sdq_group_item& first = items[j];
+    for (int k = j; k < ngroup; k++) {
+      const sdq_group_item& it = items[k];
+      if (done[k] || cv[k].seg < 0 || !same_group(first, it)) continue;
+      done[k] = true;
+      const QuantSeg& q = qs.s[cv[k].seg];
+      GemmProblem& p = g.p[g.count++];
+      p.wt = it.w->frags;
+      p.scale = it.w->scale;
+      p.bias = q.cc.bias_pad;
+      p.gate = q.cc.gate_pad;
+      p.at = q.at;
+      p.as = q.as;
+      p.resid = it.epi.resid;
+      p.Y = it.Y;
+      p.M = (int)it.M;
+      p.N = (int)it.w->N;
+      p.kind = it.epi.kind;
+      p.gate_fma = it.epi.gate_fma;
+    }
+    EpiArgs ea = make_epi(&first.epi, first.w->K);
+    ea.bias = ea.gate = ea.resid = nullptr;  // per problem, from the table
+    e = launch_qgemm_group(g, first.w->KFp, ea, sink, cu_count, s);
+    if (e != hipSuccess) return hip_error(e, "stack grouped qgemm launch");
+  }
+  mark();
+  // then the others, in order
+  int tail = 0;
+  for (int i = ngroup; i < n; i++) {
+    const sdq_group_item& it = items[i];
+    if (cv[i].seg < 0) continue;
+    const QuantSeg& q = qs.s[cv[i].seg];
+    const EpiArgs ea = make_epi(&it.epi, it.w->K);
+    const GemmAux aux{q.cc.bias_pad, q.cc.gate_pad, sink, cu_count, 1, nullptr, nullptr, &tail,
+                      nullptr};
+    e = launch_qgemm(cfgs[i], it.w->frags, it.w->scale, q.at, q.as, it.M, it.w->N, it.w->KFp, ea,
+                     it.Y, 1, aux, s);
+    if (e != hipSuccess) return hip_error(e, "stack qgemm launch");
+  }
+  mark();
+  if (has_ffn) {
+    // fc1 + GELU, writing the hidden state's row maxima, then fc2's quantizer
+    // from them and fc2 with the gated residual (as ffn_device)
+    const sdq_weight* fc1 = ffn->fc1;
+    RowMax rm;
+    rm.stride = (int)round_up(std::max(gemm_rmax_chunks(kCfg128x128, fc1->N),
+                                       gemm_rmax_chunks(kCfg256x256, fc1->N)),
+                              4);
+    if ((rc = rmax_buffer(dev, s, (size_t)ffn->M * rm.stride * sizeof(float), &rm.p))) return rc;
+    const sdq_epilogue e1{SDQ_EPI_GELU, 1, ffn->b1, nullptr, nullptr};
+    EpiArgs ea = make_epi(&e1, fc1->K);
+    ea.rmax = rm.p;
+    ea.rmax_stride = rm.stride;
+    const QuantSeg& q = qs.s[cv[n].seg];
+    const GemmAux aux{q.cc.bias_pad, nullptr, sink, cu_count, 1, nullptr, &rm.chunks, &tail,
+                      nullptr};
+    e = launch_qgemm(cfg1, fc1->frags, fc1->scale, q.at, q.as, ffn->M, fc1->N, fc1->KFp, ea,
+                     ffn->hid, 1, aux, s);
+    if (e != hipSuccess) return hip_error(e, "stack fc1 launch");
+    mark();
+    if (marks.size() == 5 && std::all_of(marks.begin(), marks.end(), [](hipEvent_t v) { return v; })) {
+      t_recs.push_back({"act_quant_stack", marks[0], marks[1]});
+      t_recs.push_back({"qgemm_group", marks[1], marks[2]});
+      t_recs.push_back({"qgemm_stack_seq", marks[2], marks[3]});
+      t_recs.push_back({"qgemm_fc1_stack", marks[3], marks[4]});
+      marks.clear();
+    }
+    for (hipEvent_t v : marks)
+      if (v) (void)hipEventDestroy(v);
+    const sdq_epilogue e2{SDQ_EPI_GATED, ffn->gate_fma, ffn->b2, ffn->gate, ffn->x};
+    return qlinear_device(ffn->fc2, ffn->hid, ffn->M, ffn->fc2->K, &e2, ffn->x, s, &rm, nullptr);
+  }
+  if (marks.size() == 4 && std::all_of(marks.begin(), marks.end(), [](hipEvent_t v) { return v; })) {
+    t_recs.push_back({"act_quant_stack", marks[0], marks[1]});
+    t_recs.push_back({"qgemm_group", marks[1], marks[2]});
+    t_recs.push_back({"qgemm_stack_seq", marks[2], marks[3]});
+    marks.clear();
+  }
+  for (hipEvent_t v : marks)
+    if (v) (void)hipEventDestroy(v);
   return SDQ_OK;
 }
 

@@ -128,7 +128,74 @@ void run_linears(const std::vector<LinCall>& calls, void* s) {
   check(sdq_qlinear_group(items.data(), (int)items.size(), s), "DitBlock linears");
 }
 
+sdq_group_item group_item(const LinCall& c) {
+  const bool res = c.kind == SDQ_EPI_GATED || c.kind == SDQ_EPI_RESID;
+  return sdq_group_item{c.l->handle(), c.A, c.M,
+                        sdq_epilogue{c.kind, 1, c.l->bias_device(), c.gate, res ? c.Y : nullptr},
+                        c.Y};
+}
+
+// `group` (independent), then `seq` in order, then the FFN when `ffn` is
+// given, as one sdq_qlinear_stack: every input quantized by one launch. That
+// needs every input in place before the first GEMM (no output overlaps an
+// input) and `group` independent; otherwise the same calls run one by one.
+void run_stack(const std::vector<LinCall>& group, const std::vector<LinCall>& seq,
+               const sdq_ffn_item* ffn, int64_t D, int64_t F, void* s) {
+  struct Buf {
+    const void* p;
+    size_t n;
+  };
+  std::vector<Buf> ins, outs;
+  auto add = [&](const LinCall& c) {
+    ins.push_back({c.A, (size_t)(c.M * c.l->in_features()) * sizeof(float)});
+    outs.push_back({c.Y, (size_t)(c.M * c.l->out_features()) * sizeof(float)});
+  };
+  for (const LinCall& c : group) add(c);
+  for (const LinCall& c : seq) add(c);
+  if (ffn) {
+    const size_t d = (size_t)D * sizeof(float), f = (size_t)F * sizeof(float);
+    ins.push_back({ffn->h, (size_t)ffn->M * d});
+    outs.push_back({ffn->hid, (size_t)ffn->M * f});
+    outs.push_back({ffn->x, (size_t)ffn->M * d});
+  }
+  bool ok = group.size() + seq.size() <= SDQ_MAX_GROUP;
+  for (const Buf& o : outs)
+    for (const Buf& a : ins) ok = ok && !overlap(o.p, o.n, a.p, a.n);
+  for (size_t i = 0; ok && i < group.size(); i++)
+    for (size_t j = 0; j < group.size(); j++) {
+      if (i == j) continue;
+      const LinCall& c = group[i];
+      const LinCall& d = group[j];
+      ok = ok && !overlap(c.Y, (size_t)(c.M * c.l->out_features()) * sizeof(float), d.Y,
+                          (size_t)(d.M * d.l->out_features()) * sizeof(float));
+    }
+  if (!ok) {
+    run_linears(group, s);
+    for (const LinCall& c : seq) run_linears({c}, s);
+    if (ffn)
+      check(sdq_ffn(ffn->fc1, ffn->b1, ffn->fc2, ffn->b2, ffn->h, ffn->M, ffn->gate,
+                    ffn->gate_fma, ffn->hid, ffn->x, s),
+            "DitBlock ffn");
+    return;
+  }
+  std::vector<sdq_group_item> items;
+  for (const LinCall& c : group) items.push_back(group_item(c));
+  for (const LinCall& c : seq) items.push_back(group_item(c));
+  check(sdq_qlinear_stack(items.data(), (int)items.size(), (int)group.size(), ffn, s),
+        "DitBlock linear stack");
+}
+
 }  // namespace
+
+// The FFN of the block as a stack entry, when it takes its normalized input
+// from the caller (no norm + modulation folded into fc1's quantizer).
+bool DitBlock::ffn_item(const sd_dit_block_io& io, sdq_ffn_item* f) const {
+  if (io.shift_ffn && io.scale_ffn) return false;
+  *f = sdq_ffn_item{fc1_.handle(), fc1_.bias_device(), fc2_.handle(), fc2_.bias_device(),
+                    io.h_ffn,      io.M,               io.gate_ffn,   1,
+                    io.hid,        io.x};
+  return true;
+}
 
 // The Linears of the self and cross attention that read inputs the caller
 // already has (ovi_dit.cpp:176-188, 229-254): q|k|v (unless the block
@@ -174,13 +241,17 @@ void DitBlock::forward_linears(const sd_dit_block_io& io, void* s) const {
   // cross attention: q on tokens, k|v on the context, k_fusion|v_fusion on
   // the other branch (229-254). Independent given the inputs: one grouped
   // run when no output overlaps another Linear's input.
+  // The whole stack from given inputs: every input quantized by one launch
+  // (sdq_qlinear_stack), then the attention Linears grouped, x += o(xt) (251)
+  // and the FFN in order.
   if (io.shift_sa && io.scale_sa) qkv_lnmod(io, s);
   std::vector<LinCall> calls;
   attn_linears(io, calls);
-  run_linears(calls, s);
-  // then x += o(xt)                                   (251)
-  co_.forward_device(io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x, io.x, s);
-  ffn_linears(io, s);
+  sdq_ffn_item f;
+  const bool fi = ffn_item(io, &f);
+  run_stack(calls, {{&co_, io.xt, io.M, SDQ_EPI_RESID, nullptr, io.x}}, fi ? &f : nullptr, dim_,
+            ffn_, s);
+  if (!fi) ffn_linears(io, s);
 }
 
 namespace {
@@ -249,12 +320,14 @@ void forward_linears_pair(const DitBlock& a, const sd_dit_block_io& ia, const Di
       }
       b.attn_linears(ib, cb);
       for (const LinCall& c : ctx) cb.push_back(c);
-      run_linears(ca, s);
-      run_linears(cb, s2);
-      run_linears({{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x}}, s);
-      run_linears({{&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}}, s2);
-      a.ffn_linears(ia, s);
-      b.ffn_linears(ib, s2);
+      sdq_ffn_item fa, fb;
+      const bool ha = a.ffn_item(ia, &fa), hb = b.ffn_item(ib, &fb);
+      run_stack(ca, {{&a.co_, ia.xt, ia.M, SDQ_EPI_RESID, nullptr, ia.x}}, ha ? &fa : nullptr,
+                a.dim(), a.ffn_dim(), s);
+      run_stack(cb, {{&b.co_, ib.xt, ib.M, SDQ_EPI_RESID, nullptr, ib.x}}, hb ? &fb : nullptr,
+                b.dim(), b.ffn_dim(), s2);
+      if (!ha) a.ffn_linears(ia, s);
+      if (!hb) b.ffn_linears(ib, s2);
       check(sdq_stream_wait(s, s2), "pair join");
       return;
     }

@@ -232,6 +232,7 @@ class DitBlock {
   void qkv_lnmod(const sd_dit_block_io& io, void* s) const;
   void attn_linears(const sd_dit_block_io& io, std::vector<LinCall>& out) const;
   void ffn_linears(const sd_dit_block_io& io, void* s) const;
+  bool ffn_item(const sd_dit_block_io& io, sdq_ffn_item* f) const;
   void cross_ffn_phase(const sd_dit_block_step& st, int batch, float* ws, void* s) const;
   friend std::vector<DitBlock> dit_blocks_from_pack_file(const std::string&, const std::string&,
                                                          const std::vector<int>&, int64_t,

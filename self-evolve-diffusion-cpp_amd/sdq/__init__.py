@@ -41,6 +41,13 @@ class GroupItem(ctypes.Structure):
                 ("epi", Epilogue), ("Y", ctypes.c_void_p)]
 
 
+class FfnItem(ctypes.Structure):
+    _fields_ = [("fc1", ctypes.c_void_p), ("b1", ctypes.c_void_p), ("fc2", ctypes.c_void_p),
+                ("b2", ctypes.c_void_p), ("h", ctypes.c_void_p), ("M", ctypes.c_int64),
+                ("gate", ctypes.c_void_p), ("gate_fma", ctypes.c_int), ("hid", ctypes.c_void_p),
+                ("x", ctypes.c_void_p)]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int), ("cu_count", ctypes.c_int),
                 ("max_clock_khz", ctypes.c_int), ("mem_clock_khz", ctypes.c_int),
@@ -80,6 +87,8 @@ SIGNATURES = {
     "sdq_qlinear_noalloc": (ctypes.c_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(Epilogue), _vp,
                                            _vp]),
     "sdq_qlinear_group": (ctypes.c_int, [ctypes.POINTER(GroupItem), ctypes.c_int, _vp]),
+    "sdq_qlinear_stack": (ctypes.c_int, [ctypes.POINTER(GroupItem), ctypes.c_int, ctypes.c_int,
+                                         ctypes.POINTER(FfnItem), _vp]),
     "sdq_rmsnorm_rope_batch": (ctypes.c_int, [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_float,
                                               _vp]),
     "sdq_layernorm": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp]),
@@ -410,6 +419,50 @@ def qlinear_group(items, stream=None):
                      (M, w.N))
     c.done()
     _check(_lib.sdq_qlinear_group(arr, len(items), _stream(stream)))
+
+
+def _group_items(c, items):
+    arr = (GroupItem * max(1, len(items)))()
+    for i, it in enumerate(items):
+        w = it["w"]
+        arr[i].w = _weight(w, f"items[{i}].w")
+        arr[i].A = c(it["A"], f"items[{i}].A", "f32", (None, w.K))
+        M = it["A"].shape[0]
+        arr[i].M = M
+        arr[i].epi = _epilogue_args(c, it.get("kind", "none"), M, w.N, it["out"], it.get("bias"),
+                                    it.get("gate"), it.get("resid"), it.get("gate_fma", True))
+        arr[i].Y = c(it["out"], f"items[{i}].out", "i32" if arr[i].epi.kind == EPI_ACC else "f32",
+                     (M, w.N))
+    return arr
+
+
+def qlinear_stack(items, ngroup, ffn=None, stream=None):
+    """A block's linear stack from given inputs (sdq_qlinear_stack): the same
+    results as qlinear_group(items[:ngroup]), then qlinear on each later item
+    in order, then ffn(**ffn); every input quantized by one launch first.
+    items: as for qlinear_group; ffn: dict with fc1, b1, fc2, b2, h, gate,
+    hid, x and optionally gate_fma (as ffn's arguments), or None."""
+    if len(items) > MAX_GROUP:
+        raise _bad(f"at most {MAX_GROUP} items")
+    c = _Args()
+    arr = _group_items(c, items)
+    f = None
+    if ffn is not None:
+        fc1, fc2 = ffn["fc1"], ffn["fc2"]
+        M = ffn["h"].shape[0]
+        f = FfnItem()
+        f.fc1, f.fc2 = _weight(fc1, "fc1"), _weight(fc2, "fc2")
+        f.b1 = c(ffn.get("b1"), "b1", "f32", (fc1.N,), optional=True)
+        f.b2 = c(ffn.get("b2"), "b2", "f32", (fc2.N,), optional=True)
+        f.h = c(ffn["h"], "h", "f32", (M, fc1.K))
+        f.M = M
+        f.gate = c(ffn["gate"], "gate", "f32", (fc2.N,))
+        f.gate_fma = 1 if ffn.get("gate_fma", True) else 0
+        f.hid = c(ffn["hid"], "hid", "f32", (M, fc1.N))
+        f.x = c(ffn["x"], "x", "f32", (M, fc2.N))
+    c.done()
+    _check(_lib.sdq_qlinear_stack(arr, len(items), ngroup,
+                                  ctypes.byref(f) if f is not None else None, _stream(stream)))
 
 
 NOALLOC_SCRATCH_BYTES = 64 << 20  # SDQ_NOALLOC_SCRATCH_BYTES

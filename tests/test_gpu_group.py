@@ -168,3 +168,122 @@ def test_group_rejects_overlapping_items(sdq_dev, oracle):
     torch.cuda.synchronize()
     for it in items:
         it["w"].free()
+
+
+def _stack_case(sdq, torch, oracle, dev, specs, seq_specs, ffn_shape, seed, chain=None):
+    """items: grouped `specs` then `seq_specs` (M, K, N, kind, bias); with
+    `chain` = i, the later items of a residual kind and the FFN update grouped
+    item i's output in place after it (as a block's cross o and FFN follow its
+    o, all on x); plus an FFN (M, D, F) or None. Returns (stack results,
+    separate-call results)."""
+    items, _ = _items(sdq, torch, oracle, dev, specs + seq_specs, seed)
+    ng = len(specs)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)  # noqa
+    ffn = None
+    if ffn_shape is not None:
+        M, D, F = ffn_shape
+        w1, _, _ = _weight(sdq, oracle, F, D, seed + 900)
+        w2, _, _ = _weight(sdq, oracle, D, F, seed + 910)
+        ffn = dict(fc1=w1, fc2=w2, b1=t(oracle.randn(F, seed + 920) * np.float32(0.01)),
+                   b2=t(oracle.randn(D, seed + 921) * np.float32(0.01)),
+                   h=t(oracle.randn(M * D, seed + 922).reshape(M, D)),
+                   gate=t(oracle.randn(D, seed + 923)), hid=torch.empty((M, F), device=dev),
+                   x=t(oracle.randn(M * D, seed + 924).reshape(M, D)))
+
+    def link(its, f):
+        if chain is None:
+            return
+        x = its[chain]["out"]
+        for it in its[ng:]:
+            if it["kind"] in ("gated", "resid"):
+                it["out"] = it["resid"] = x
+        if f is not None:
+            f["x"] = x
+
+    # the separate calls, on copies of every output
+    ref = [dict(it, out=it["out"].clone()) for it in items]
+    for it in ref:
+        if it["kind"] in ("gated", "resid"):
+            it["resid"] = it["out"]
+    rffn = None if ffn is None else dict(ffn, hid=ffn["hid"].clone(), x=ffn["x"].clone())
+    link(items, ffn)
+    link(ref, rffn)
+    sdq.qlinear_group(ref[:ng])
+    for it in ref[ng:]:
+        sdq.qlinear(it["w"], it["A"], it["out"], kind=it["kind"], bias=it["bias"],
+                    gate=it.get("gate"), resid=it.get("resid"), gate_fma=it["gate_fma"])
+    if rffn is not None:
+        sdq.ffn(rffn["fc1"], rffn["b1"], rffn["fc2"], rffn["b2"], rffn["h"], rffn["gate"],
+                rffn["hid"], rffn["x"])
+    sdq.qlinear_stack(items, ng, ffn)
+    torch.cuda.synchronize()
+    got = [it["out"].cpu().numpy() for it in items]
+    want = [it["out"].cpu().numpy() for it in ref]
+    if ffn is not None:
+        got += [ffn["hid"].cpu().numpy(), ffn["x"].cpu().numpy()]
+        want += [rffn["hid"].cpu().numpy(), rffn["x"].cpu().numpy()]
+    for it in items:
+        it["w"].free()
+    if ffn is not None:
+        ffn["fc1"].free()
+        ffn["fc2"].free()
+    return got, want
+
+
+@pytest.mark.parametrize("case", ["block768", "block157", "no_ffn", "fallback_skinny", "big_rows"])
+def test_stack_equals_separate_calls(sdq_dev, oracle, case):
+    """sdq_qlinear_stack against qlinear_group + qlinear per later item +
+    ffn, bit for bit: a block's shapes at small widths (every input through
+    the shared quantizer launch), a stack without FFN, one whose item takes
+    another path (few rows: the whole stack runs as the separate calls), and
+    256x256 tiles for the sequential item and fc1."""
+    import torch
+
+    import sdq
+
+    D = 512
+    if case == "block768":
+        specs = [(768, D, 3 * D, "none", True), (768, D, D, "gated", True),
+                 (768, D, D, "none", True), (96, D, 2 * D, "none", True), (157, D, 2 * D, "none", True)]
+        seq, ffn = [(768, D, D, "resid", True)], (768, D, 4 * D)
+    elif case == "block157":
+        specs = [(157, D, 3 * D, "none", True), (157, D, D, "gated", True),
+                 (157, D, D, "none", True), (96, D, 2 * D, "none", True), (768, D, 2 * D, "none", True)]
+        seq, ffn = [(157, D, D, "resid", True)], (157, D, 4 * D)
+    elif case == "no_ffn":
+        specs = [(300, D, 256, "none", True), (300, D, 384, "gelu", False)]
+        seq, ffn = [(300, D, 256, "resid", False), (200, D, 512, "none", True)], None
+    elif case == "fallback_skinny":
+        specs = [(300, D, 256, "none", True), (40, D, 128, "none", True)]
+        seq, ffn = [(300, D, 256, "gated", True)], (130, D, 2 * D)
+    else:  # 256x256 tiles for the later item and fc1 (>= 2 rounds of them)
+        specs = [(256, D, 512, "none", True), (256, D, 256, "gated", True)]
+        seq, ffn = [(8192, D, 4096, "none", True)], (8192, D, 4096)
+    print(f"[stack] {case}", flush=True)
+    chain = 1 if case.startswith("block") else None
+    got, want = _stack_case(sdq, torch, oracle, sdq_dev, specs, seq, ffn, 700, chain)
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert_bitexact(g, w, f"{case}: output {i} vs the separate calls")
+
+
+def test_stack_rejects_overlaps(sdq_dev, oracle):
+    """An output over an input that the stack quantizes up front (here a later
+    item writing the first item's input), or two grouped items writing the
+    same buffer, is refused before anything runs."""
+    import torch
+
+    import sdq
+
+    specs = [(96, 512, 512, "none", True), (96, 512, 512, "none", True)]
+    items, _ = _items(sdq, torch, oracle, sdq_dev, specs, 950)
+    items[1]["out"] = items[0]["A"]
+    with pytest.raises(sdq.SdqError) as ei:
+        sdq.qlinear_stack(items, 1)
+    assert "overlaps the input" in str(ei.value)
+    items[1]["out"] = items[0]["out"]
+    with pytest.raises(sdq.SdqError) as ei:
+        sdq.qlinear_stack(items, 2)
+    assert "writes the output" in str(ei.value)
+    torch.cuda.synchronize()
+    for it in items:
+        it["w"].free()
