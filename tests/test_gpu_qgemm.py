@@ -365,6 +365,29 @@ def test_host_pointer_entry_point(sdq_dev, oracle):
                     "host gated")
 
 
+def test_host_entry_multi_chunk(sdq_dev, oracle):
+    """Host arrays larger than one 16 MiB pinned bounce buffer: A (2 chunks),
+    the residual and Y (3 chunks each) cross chunk edges in the middle of a
+    row (K*4 and N*4 do not divide 16 MiB). Two calls in a row, the second
+    smaller, reuse the same staging. Each result equals the device entry's
+    bit for bit; the device entry is pinned against the oracle elsewhere."""
+    import sdq
+
+    rng = np.random.default_rng(5)
+    K, N = 1540, 2620
+    q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    s = (rng.random(N, dtype=np.float32) * 0.01 + 1e-3).astype(np.float32)
+    w = sdq.Weight.from_host(q, s)
+    bias = rng.standard_normal(N).astype(np.float32)
+    gate = rng.standard_normal(N).astype(np.float32)
+    for M in (4100, 1703):
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        x = rng.standard_normal((M, N)).astype(np.float32)
+        got = sdq.qlinear_host(w, A, kind="gated", bias=bias, gate=gate, resid=x)
+        want = _run(sdq_dev, w, A, kind="gated", bias=bias, gate=gate, resid=x)
+        assert_bitexact(got, want, f"host multi-chunk M={M}")
+
+
 def test_unaligned_and_strided_buffers(sdq_dev, oracle):
     """A and Y at 4-byte (not 16-byte) aligned device addresses take the
     scalar load/store paths and still match bit for bit."""
