@@ -456,12 +456,19 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
   __shared__ __attribute__((aligned(16))) float colb[2][3][BN];
   __shared__ __attribute__((aligned(16))) float rowb[2][BM];
-  // Epilogue transpose scratch: 4 KB per wave of its own when LDS has room,
-  // else the wave's DMA slots in the tile's last stage buffer (whose refill
-  // is then deferred until after the epilogue).
+  // Epilogue transpose scratch of each wave, beside the operand ring: 4 KB
+  // (a whole 32x32 block) when LDS has room, else 2 KB (the block in two
+  // halves of 16 rows). Both persistent configurations take 2 KB: 256x256
+  // 128 + 8 + 16 KB, 128x128 twice 64 + 4 + 8 KB. Owning it keeps the ring
+  // refilling through the tile's last stage (borrowing a stage buffer would
+  // hold that refill until after the epilogue: 1% slower at 27280 rows).
   constexpr int kLdsPipe = STAGES * STAGE + (2 * 3 * BN + 2 * BM) * 4;
-  constexpr bool kOwnScratch = OCC * (kLdsPipe + NW * 4096) <= 160 * 1024;
-  __shared__ __attribute__((aligned(1024))) char escr[kOwnScratch ? NW * 4096 : 16];
+  constexpr bool kFullScr = OCC * (kLdsPipe + NW * 4096) <= 160 * 1024;
+  static_assert(kFullScr || OCC * (kLdsPipe + NW * 2048) <= 160 * 1024,
+                "LDS: operand ring plus transpose scratch");
+  constexpr int kScrBytes = kFullScr ? 4096 : 2048;
+  constexpr int kHalves = kFullScr ? 1 : 2;
+  __shared__ __attribute__((aligned(1024))) char escr[NW * kScrBytes];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -635,8 +642,7 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   //           with the LDS-DMA of the stage STAGES ahead into buffer gs and
   //           the reads of the next stage's weight operands 0..FN-1 and
   //           activation operands.
-  auto step16 = [&](auto dma_tag, int gs, auto first_tag) {
-    constexpr bool Dma = decltype(dma_tag)::value;
+  auto step16 = [&](int gs, auto first_tag) {
     constexpr bool First = decltype(first_tag)::value;
     const char* cb = lds + ((unsigned)gs % STAGES) * STAGE;
 #pragma unroll
@@ -652,15 +658,15 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
 #pragma unroll
     for (int i = 0; i < FN * YM; i++) {
       mma16(FN + i % FN, i / FN, First);
-      if (Dma && i < LPW) dma_stage(i);
+      if (i < LPW) dma_stage(i);
       if (i < FN) read16(nb, i);
       if (i % FN == FN - 1) read16(nb, XN + i / FN);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (Dma) advance();
+    advance();
   };
-  const std::true_type with_dma, first_stage;
-  const std::false_type defer_dma, next_stage;
+  const std::true_type first_stage;
+  const std::false_type next_stage;
 
   // prologue: STAGES stages in flight, stage 0 landed
 #pragma unroll
@@ -695,26 +701,14 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
   int gs = 0;
   for (int j = 0; j < ntile; j++) {
     const int nst = nks;  // >= STAGES
-    // Transpose scratch of this wave: four 1 KB slots (stride kSlot), slot
-    // t holding block rows 8t..8t+7 (128 bytes each, 16-byte chunks
+    step16(gs++, first_stage);
+    for (int q = 1; q < nst; q++) step16(gs++, next_stage);
+    // Transpose scratch of this wave: 1 KB slots, slot t holding block rows
+    // 8t..8t+7 (8t+7 mod 16 with 2 KB; 128 bytes each, 16-byte chunks
     // XOR-swizzled by the row so both access patterns are bank-conflict
-    // free). Without room of its own, the slots are this wave's four DMA
-    // slots in the buffer of the tile's last stage: every wave read that
-    // buffer before the last barrier, its refill is deferred, and only this
-    // wave writes these slots, now and in the deferred refill.
-    char* scr;
-    if constexpr (kOwnScratch) {
-      step16(with_dma, gs++, first_stage);
-      for (int q = 1; q < nst; q++) step16(with_dma, gs++, next_stage);
-      scr = escr + w * 4096;
-    } else {
-      step16(with_dma, gs++, first_stage);
-      for (int q = 2; q < nst; q++) step16(with_dma, gs++, next_stage);
-      step16(defer_dma, gs, next_stage);
-      scr = lds + ((unsigned)gs % STAGES) * STAGE + w * 1024;
-      gs++;
-    }
-    constexpr int kSlot = kOwnScratch ? 1024 : NW * 1024;
+    // free).
+    char* const scr = escr + w * kScrBytes;
+    constexpr int kSlot = 1024;
     // ---- epilogue of tile j
     int tm, tn, ksp, pb;
     coords(j, tm, tn, ksp, pb);
@@ -783,17 +777,28 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
         // transpose the block: MFMA layout -> scratch -> row layout. Its
         // four 16x16 quarters: lane holds block row 16hb + (l & 15), 4-column
         // chunk 4ha + (l >> 4).
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int ha = q >> 1, hb = q & 1;
-          const int row = 16 * hb + (lane & 15), chunk = 4 * ha + (lane >> 4);
-          *reinterpret_cast<v4i*>(scr + (row >> 3) * kSlot + (row & 7) * 128 +
-                                  ((chunk ^ (row & 7)) * 16)) = acc16[2 * a + ha][2 * b + hb];
-        }
+        // With 2 KB of scratch the block goes through in two halves of 16
+        // rows (slots 0 and 1 each time); a wave's LDS accesses run in
+        // order, so the second half's writes follow the first half's reads.
         v4i t4[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          t4[i] = *reinterpret_cast<const v4i*>(scr + i * kSlot + rr * 128 + ((rc ^ rr) * 16));
+        for (int h = 0; h < kHalves; h++) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int ha = q >> 1, hb = q & 1;
+            if (kHalves == 2 && hb != h) continue;
+            const int row = 16 * hb + (lane & 15), chunk = 4 * ha + (lane >> 4);
+            const int slot = kHalves == 2 ? ((row >> 3) & 1) : (row >> 3);
+            *reinterpret_cast<v4i*>(scr + slot * kSlot + (row & 7) * 128 +
+                                    ((chunk ^ (row & 7)) * 16)) = acc16[2 * a + ha][2 * b + hb];
+          }
+#pragma unroll
+          for (int i = 0; i < 4 / kHalves; i++) {
+            const int slot = kHalves == 2 ? i : i + h * 4;
+            t4[h * (4 / kHalves) + i] =
+                *reinterpret_cast<const v4i*>(scr + slot * kSlot + rr * 128 + ((rc ^ rr) * 16));
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int rl = b * 32 + 8 * i;  // block row offset of this store
@@ -895,13 +900,6 @@ qgemm_persist(const int8_t* __restrict__ wt, ColOps cols, const int8_t* __restri
               epi.rmax[(int64_t)row * epi.rmax_stride + tn * WN + wn] = m;
           }
       }
-    }
-    if constexpr (!kOwnScratch) {
-      // this wave's scratch reads are done: the deferred refill may land
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(63) & ~(15 << 8));
-#pragma unroll
-      for (int t = 0; t < LPW; t++) dma_stage(t);
-      advance();
     }
   }
   // the cursor's zero-range loads past the end still land in LDS
