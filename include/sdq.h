@@ -342,7 +342,12 @@ int sdq_qgemm(const sdq_weight* w, const float* A, int64_t M, int64_t K, float* 
 
 /* Host-pointer synchronous variant of sdq_qlinear: copies A (and bias /
  * gate / resid) in, runs, copies Y out. Replaces sd::qgemm's host-tensor
- * contract (tensor.h:52) for callers that hold CPU tensors. */
+ * contract (tensor.h:52) for callers that hold CPU tensors. Each calling
+ * thread keeps, per device, a stream of its own, two 16 MiB pinned bounce
+ * buffers and a device buffer that grows to the largest call's inputs and
+ * output; they are reused by its later calls (no allocation once grown) and
+ * are not released when the thread exits, so call it from long-lived
+ * threads. */
 int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                      const sdq_epilogue* epi, void* Y);
 

@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <new>
@@ -103,6 +104,12 @@ hipEvent_t prof_mark(hipStream_t s) {
     return nullptr;
   }
   return e;
+}
+
+// Profiling marks not handed to the records (an error return).
+void drop_events(std::initializer_list<hipEvent_t> evs) {
+  for (hipEvent_t e : evs)
+    if (e) (void)hipEventDestroy(e);
 }
 
 int current_device(int* dev) {
@@ -327,7 +334,10 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
     if (rmax_out) rmax_out->chunks = 0;
     hipEvent_t p0 = prof ? prof_mark(s) : nullptr;
     hipError_t e = launch_qgemm_qin(w->frags, w->scale, A, M, K, N, w->KFp, ea, Y, vec, s);
-    if (e != hipSuccess) return hip_error(e, "qgemm launch");
+    if (e != hipSuccess) {
+      drop_events({p0});
+      return hip_error(e, "qgemm launch");
+    }
     if (prof) {
       hipEvent_t p1 = prof_mark(s);
       if (p0 && p1) {
@@ -406,7 +416,10 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
                                                pre->chunks, pre->stride, cu_count, s)
                : launch_act_quant_frags(A, M, K, Mp, w->KFp, ws->at, ws->as, cc,
                                         pmax_bytes ? ws->pmax : nullptr, cu_count, s);
-  if (e != hipSuccess) return hip_error(e, "act_quant launch");
+  if (e != hipSuccess) {
+    drop_events({p0});
+    return hip_error(e, "act_quant launch");
+  }
   hipEvent_t p1 = prof ? prof_mark(s) : nullptr;
   int vec = (N % 4 == 0) && aligned16(Y);
   if (ea.bias) vec = vec && aligned16(ea.bias);
@@ -420,7 +433,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
               pmid};
   e = launch_qgemm(cfg, w->frags, w->scale, ws->at, ws->as, M, N, w->KFp, ea, Y, vec, aux, s);
   if (e != hipSuccess) {
-    if (pmid) (void)hipEventDestroy(pmid);
+    drop_events({p0, p1, pmid});
     return hip_error(e, "qgemm launch");
   }
   if (prof) {
@@ -1143,7 +1156,10 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
     qs.total = units;
     hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
     hipError_t e = launch_act_quant_segs(qs, s);
-    if (e != hipSuccess) return hip_error(e, "group act_quant launch");
+    if (e != hipSuccess) {
+      drop_events({p0});
+      return hip_error(e, "group act_quant launch");
+    }
     hipEvent_t p1 = t_prof ? prof_mark(s) : nullptr;
     // one GEMM launch per set of items with the same K (each problem carries
     // its own epilogue form)
@@ -1174,7 +1190,10 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
       ea.bias = ea.gate = ea.resid = nullptr;  // per problem, from the table
       e = launch_qgemm_group(g, first.w->KFp, ea, reinterpret_cast<float*>(base + sink_off),
                              cu_count, s);
-      if (e != hipSuccess) return hip_error(e, "group qgemm launch");
+      if (e != hipSuccess) {
+        drop_events({p0, p1});
+        return hip_error(e, "group qgemm launch");
+      }
     }
     if (t_prof) {
       hipEvent_t p2 = prof_mark(s);
@@ -1384,9 +1403,20 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
     units += Mp / 8;  // the quantizer's 8-row units
   }
   qs.total = units;
-  std::vector<hipEvent_t> marks;
+  // profiling marks; whatever is not handed to the records (an early
+  // return, a failed mark) is destroyed on the way out
+  struct Marks {
+    std::vector<hipEvent_t> v;
+    ~Marks() {
+      for (hipEvent_t e : v)
+        if (e) (void)hipEventDestroy(e);
+    }
+    bool all(size_t n) const {
+      return v.size() == n && std::all_of(v.begin(), v.end(), [](hipEvent_t e) { return e; });
+    }
+  } marks;
   auto mark = [&]() {
-    if (t_prof) marks.push_back(prof_mark(s));
+    if (t_prof) marks.v.push_back(prof_mark(s));
   };
   mark();
   hipError_t e = launch_act_quant_segs(qs, s);
@@ -1457,26 +1487,22 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
                      ffn->hid, 1, aux, s);
     if (e != hipSuccess) return hip_error(e, "stack fc1 launch");
     mark();
-    if (marks.size() == 5 && std::all_of(marks.begin(), marks.end(), [](hipEvent_t v) { return v; })) {
-      t_recs.push_back({"act_quant_stack", marks[0], marks[1]});
-      t_recs.push_back({"qgemm_group", marks[1], marks[2]});
-      t_recs.push_back({"qgemm_stack_seq", marks[2], marks[3]});
-      t_recs.push_back({"qgemm_fc1_stack", marks[3], marks[4]});
-      marks.clear();
+    if (marks.all(5)) {
+      t_recs.push_back({"act_quant_stack", marks.v[0], marks.v[1]});
+      t_recs.push_back({"qgemm_group", marks.v[1], marks.v[2]});
+      t_recs.push_back({"qgemm_stack_seq", marks.v[2], marks.v[3]});
+      t_recs.push_back({"qgemm_fc1_stack", marks.v[3], marks.v[4]});
+      marks.v.clear();
     }
-    for (hipEvent_t v : marks)
-      if (v) (void)hipEventDestroy(v);
     const sdq_epilogue e2{SDQ_EPI_GATED, ffn->gate_fma, ffn->b2, ffn->gate, ffn->x};
     return qlinear_device(ffn->fc2, ffn->hid, ffn->M, ffn->fc2->K, &e2, ffn->x, s, &rm, nullptr);
   }
-  if (marks.size() == 4 && std::all_of(marks.begin(), marks.end(), [](hipEvent_t v) { return v; })) {
-    t_recs.push_back({"act_quant_stack", marks[0], marks[1]});
-    t_recs.push_back({"qgemm_group", marks[1], marks[2]});
-    t_recs.push_back({"qgemm_stack_seq", marks[2], marks[3]});
-    marks.clear();
+  if (marks.all(4)) {
+    t_recs.push_back({"act_quant_stack", marks.v[0], marks.v[1]});
+    t_recs.push_back({"qgemm_group", marks.v[1], marks.v[2]});
+    t_recs.push_back({"qgemm_stack_seq", marks.v[2], marks.v[3]});
+    marks.v.clear();
   }
-  for (hipEvent_t v : marks)
-    if (v) (void)hipEventDestroy(v);
   return SDQ_OK;
 }
 
@@ -1544,7 +1570,10 @@ int sdq_rmsnorm_rope_batch(const sdq_rms_seg* segs, int nseg, int64_t C, int hea
     }
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   hipError_t e = launch_rmsnorm_rope_segs(g, n, C, heads, eps, s);
-  if (e != hipSuccess) return hip_error(e, "rmsnorm_rope launch");
+  if (e != hipSuccess) {
+    drop_events({p0});
+    return hip_error(e, "rmsnorm_rope launch");
+  }
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);
     if (p0 && p1) {
@@ -1584,7 +1613,10 @@ int sdq_layernorm(const float* x, int64_t M, int64_t K, const float* w, const fl
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   hipError_t e = launch_ln_stats(x, M, K, eps, st, s);
   if (e == hipSuccess) e = launch_ln_apply(x, M, K, st, w, b, y, s);
-  if (e != hipSuccess) return hip_error(e, "layernorm launch");
+  if (e != hipSuccess) {
+    drop_events({p0});
+    return hip_error(e, "layernorm launch");
+  }
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);
     if (p0 && p1) {
@@ -1617,7 +1649,10 @@ int sdq_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   const hipError_t e = launch_linear_f32(x, M, K, w, N, bias, y, g_dev[dev].cu_count, s);
-  if (e != hipSuccess) return hip_error(e, "linear_f32 launch");
+  if (e != hipSuccess) {
+    drop_events({p0});
+    return hip_error(e, "linear_f32 launch");
+  }
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);
     if (p0 && p1) {
@@ -1666,7 +1701,10 @@ int sdq_sdpa_batched(const float* q, int64_t ldq, const float* k, int64_t ldk, c
   hipEvent_t p0 = t_prof ? prof_mark(s) : nullptr;
   hipError_t e = launch_sdpa(q, ldq, k, ldk, v, ldv, out, ldo, Lq, Lk, heads, s, batch, part,
                              cu_count);
-  if (e != hipSuccess) return hip_error(e, "sdpa launch");
+  if (e != hipSuccess) {
+    drop_events({p0});
+    return hip_error(e, "sdpa launch");
+  }
   if (t_prof) {
     hipEvent_t p1 = prof_mark(s);
     if (p0 && p1) {
