@@ -303,17 +303,18 @@ def make_epilogue(kind="none", bias=None, gate=None, resid=None, gate_fma=True):
     return e
 
 
-def _epilogue_args(c, kind, M, N, out, bias, gate, resid, gate_fma):
+def _epilogue_args(c, kind, M, N, out, bias, gate, resid, gate_fma, prefix=""):
     """make_epilogue for device tensors, every operand checked against
-    [M, N] (out: int32 for the raw-accumulator kind, else float32)."""
+    [M, N] (out: int32 for the raw-accumulator kind, else float32); prefix
+    names the operands in errors (e.g. "items[2].")."""
     k = EPI_NAMES[kind] if isinstance(kind, str) else int(kind)
-    c(out, "out", "i32" if k == EPI_ACC else "f32", (M, N))
+    c(out, prefix + "out", "i32" if k == EPI_ACC else "f32", (M, N))
     e = Epilogue()
     e.kind = k
     e.gate_fma = 1 if gate_fma else 0
-    e.bias = c(bias, "bias", "f32", (N,), optional=True)
-    e.gate = c(gate, "gate", "f32", (N,), optional=True)
-    e.resid = c(resid, "resid", "f32", (M, N), optional=True)
+    e.bias = c(bias, prefix + "bias", "f32", (N,), optional=True)
+    e.gate = c(gate, prefix + "gate", "f32", (N,), optional=True)
+    e.resid = c(resid, prefix + "resid", "f32", (M, N), optional=True)
     return e
 
 
@@ -406,22 +407,14 @@ def qlinear_group(items, stream=None):
     if len(items) > MAX_GROUP:
         raise _bad(f"at most {MAX_GROUP} items")
     c = _Args()
-    arr = (GroupItem * max(1, len(items)))()
-    for i, it in enumerate(items):
-        w = it["w"]
-        arr[i].w = _weight(w, f"items[{i}].w")
-        arr[i].A = c(it["A"], f"items[{i}].A", "f32", (None, w.K))
-        M = it["A"].shape[0]
-        arr[i].M = M
-        arr[i].epi = _epilogue_args(c, it.get("kind", "none"), M, w.N, it["out"], it.get("bias"),
-                                    it.get("gate"), it.get("resid"), it.get("gate_fma", True))
-        arr[i].Y = c(it["out"], f"items[{i}].out", "i32" if arr[i].epi.kind == EPI_ACC else "f32",
-                     (M, w.N))
+    arr = _group_items(c, items)
     c.done()
     _check(_lib.sdq_qlinear_group(arr, len(items), _stream(stream)))
 
 
 def _group_items(c, items):
+    """The GroupItem array of qlinear_group / qlinear_stack, every tensor
+    checked by c."""
     arr = (GroupItem * max(1, len(items)))()
     for i, it in enumerate(items):
         w = it["w"]
@@ -430,7 +423,8 @@ def _group_items(c, items):
         M = it["A"].shape[0]
         arr[i].M = M
         arr[i].epi = _epilogue_args(c, it.get("kind", "none"), M, w.N, it["out"], it.get("bias"),
-                                    it.get("gate"), it.get("resid"), it.get("gate_fma", True))
+                                    it.get("gate"), it.get("resid"), it.get("gate_fma", True),
+                                    prefix=f"items[{i}].")
         arr[i].Y = c(it["out"], f"items[{i}].out", "i32" if arr[i].epi.kind == EPI_ACC else "f32",
                      (M, w.N))
     return arr

@@ -169,3 +169,32 @@ def test_linear_f32_checks():
     _raises(r"bias: shape \(19,\)", sdq.linear_f32, x, w, y, bias=torch.zeros(19))
     _raises("x: dtype", sdq.linear_f32, x.double(), w, y)
     _raises("w: must be contiguous", sdq.linear_f32, x, torch.zeros((20, 32)).t(), y)
+
+
+def test_group_and_stack_item_checks():
+    wa, wb = _fake_weight(16, 32), _fake_weight(24, 32)
+    good = [dict(w=wa, A=torch.zeros((4, 32)), out=torch.zeros((4, 16))),
+            dict(w=wb, A=torch.zeros((6, 32)), out=torch.zeros((6, 24)), kind="gated",
+                 bias=torch.zeros(24), gate=torch.zeros(24), resid=torch.zeros((6, 24)))]
+    for fn, extra in ((sdq.qlinear_group, ()), (sdq.qlinear_stack, (1,))):
+        _raises(r"items\[0\]\.A: must be on the GPU", fn, good, *extra)
+        bad = [dict(good[0], A=torch.zeros((4, 31))), good[1]]
+        _raises(r"items\[0\]\.A: shape \(4, 31\)", fn, bad, *extra)
+        bad = [good[0], dict(good[1], out=torch.zeros((6, 23)))]
+        _raises(r"items\[1\]\.out: shape \(6, 23\)", fn, bad, *extra)
+        bad = [good[0], dict(good[1], resid=torch.zeros((5, 24)))]
+        _raises(r"items\[1\]\.resid: shape \(5, 24\)", fn, bad, *extra)
+        _raises("at most 16 items", fn, good * 9, *extra)
+
+
+def test_stack_ffn_checks():
+    fc1, fc2 = _fake_weight(64, 32), _fake_weight(32, 64)
+    M = 6
+    ffn = dict(fc1=fc1, fc2=fc2, b1=torch.zeros(64), b2=torch.zeros(32), h=torch.zeros((M, 32)),
+               gate=torch.zeros(32), hid=torch.zeros((M, 64)), x=torch.zeros((M, 32)))
+    _raises("b1: must be on the GPU", sdq.qlinear_stack, [], 0, ffn)
+    _raises(r"h: shape \(6, 31\)", sdq.qlinear_stack, [], 0, dict(ffn, h=torch.zeros((M, 31))))
+    _raises(r"hid: shape \(6, 63\)", sdq.qlinear_stack, [], 0, dict(ffn, hid=torch.zeros((M, 63))))
+    _raises(r"x: shape \(5, 32\)", sdq.qlinear_stack, [], 0, dict(ffn, x=torch.zeros((5, 32))))
+    _raises(r"gate: shape \(31,\)", sdq.qlinear_stack, [], 0, dict(ffn, gate=torch.zeros(31)))
+    _raises(r"b2: shape \(33,\)", sdq.qlinear_stack, [], 0, dict(ffn, b2=torch.zeros(33)))
