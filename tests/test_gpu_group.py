@@ -287,3 +287,43 @@ def test_stack_rejects_overlaps(sdq_dev, oracle):
     torch.cuda.synchronize()
     for it in items:
         it["w"].free()
+
+
+def _random_stack(i):
+    """Draws 0-6: shapes that the stack's shared quantizer launch takes (more
+    than 64 rows, N a multiple of 4); draws 7-9 also few rows or a ragged N,
+    so that the stack falls back to the separate calls."""
+    r = np.random.default_rng(6600 + i)
+    Ks = [256, 512, 1024, 1536]
+    kinds = ["none", "gelu", "gated", "gated_nofma", "resid"]
+    odd = 0.25 if i >= 7 else 0.0
+
+    def spec(k_choices):
+        M = int(r.integers(1, 65)) if r.random() < odd else int(r.integers(65, 900))
+        N = int(r.integers(1, 1400)) if r.random() < odd else 4 * int(r.integers(16, 350))
+        return (M, int(r.choice(k_choices)), N, str(r.choice(kinds)), bool(r.random() < 0.7))
+
+    group = [spec(Ks) for _ in range(int(r.integers(1, 7)))]
+    seq = [spec(Ks) for _ in range(int(r.integers(0, 4)))]
+    ffn = None
+    if r.random() < 0.6:
+        D = int(r.choice(Ks))
+        ffn = (int(r.integers(65, 900)), D, D * int(r.choice([2, 4])))
+    return group, seq, ffn
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_stack_random_sets(sdq_dev, oracle, i):
+    """Seeded random stacks (1-6 grouped items, 0-3 later items, an FFN or
+    not; mixed rows, K, N, epilogue forms and bias) against qlinear_group, then
+    qlinear per later item, then ffn: bit for bit, on the shared quantizer
+    launch and on the fallback path."""
+    import torch
+
+    import sdq
+
+    group, seq, ffn = _random_stack(i)
+    print(f"[stack-random] {i} group={group} seq={seq} ffn={ffn}", flush=True)
+    got, want = _stack_case(sdq, torch, oracle, sdq_dev, group, seq, ffn, 1300 + 50 * i)
+    for j, (g, w) in enumerate(zip(got, want)):
+        assert_bitexact(g, w, f"random stack {i}: output {j}")
