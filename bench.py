@@ -873,6 +873,17 @@ def kernel_counters(args):
         if busy and act:
             # GRBM_GUI_ACTIVE is summed over the 8 XCDs; 256 CUs x 4 SIMDs
             kc["mfma_busy_frac"] = round(mean(busy) / ((mean(act) / 8) * 256 * 4), 4)
+        # where the waves' time goes: the share of wave cycles spent waiting on
+        # an instruction dependency (s_waitcnt, barrier), the mean L2 read
+        # latency seen by the L1, LDS bank-conflict cycles per LDS instruction
+        for key, num, den in (("wait_frac", "SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES"),
+                              ("l2_read_latency_cycles", "TCP_TCC_READ_REQ_LATENCY_sum",
+                               "TCP_TCC_READ_REQ_sum"),
+                              ("lds_conflict_cycles_per_inst", "SQ_LDS_BANK_CONFLICT",
+                               "SQ_INSTS_LDS")):
+            a, b = vals.get((k, num)), vals.get((k, den))
+            if a and b and mean(b) > 0:
+                kc[key] = round(mean(a) / mean(b), 4)
         if k in dur:
             kc["us_mean"] = round(mean(dur[k]), 2)
         out["kernels"][k] = kc
