@@ -100,3 +100,48 @@ def test_host_library_exports_its_c_shim():
     lib = sdq.load_host_library()
     missing = sorted(n for n in names if not hasattr(lib, n))
     assert not missing, missing
+
+
+def _prototypes():
+    """name -> (return type, [parameter types]) of every function in sdq.h."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    text = re.sub(r"#.*", "", text)
+    protos = {}
+    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(sdq_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        ret, name, params = " ".join(m.group(1).split()), m.group(2), m.group(3).strip()
+        if params in ("", "void"):
+            protos[name] = (ret, [])
+            continue
+        types = []
+        for p in params.split(","):
+            p = " ".join(p.split())
+            # drop the parameter name (the last identifier), keep the type and its stars
+            types.append(re.sub(r"\s*\b\w+$", "", p) if re.search(r"[\w\*]\s+\w+$", p) else p)
+        protos[name] = (ret, types)
+    return protos
+
+
+def test_binding_signatures_match_the_header():
+    """Every prototype's parameter count, scalar types and pointer-ness as
+    the Python binding declares them: a drift would pass wrong arguments
+    through ctypes without any error until a GPU run."""
+    import sdq
+
+    scalar = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
+              "float": ctypes.c_float, "double": ctypes.c_double}
+    protos = _prototypes()
+    assert set(protos) == set(sdq.SIGNATURES)
+    for name, (ret, params) in protos.items():
+        res, args = sdq.SIGNATURES[name]
+        assert len(args) == len(params), (name, params, args)
+        for p, a in zip(params, args):
+            if "*" in p:
+                assert a in (ctypes.c_void_p, ctypes.c_char_p) or issubclass(a, ctypes._Pointer), \
+                    (name, p, a)
+            else:
+                base = p.replace("const ", "").strip()
+                assert scalar.get(base) is a, (name, p, a)
+        if "*" in ret:
+            assert res is ctypes.c_char_p, (name, ret)
+        else:
+            assert scalar[ret.replace("const ", "").strip()] is res, (name, ret, res)
