@@ -102,12 +102,15 @@ def test_host_library_exports_its_c_shim():
     assert not missing, missing
 
 
-def _prototypes():
-    """name -> (return type, [parameter types]) of every function in sdq.h."""
-    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+def _prototypes(header=HEADER, prefix="sdq_"):
+    """name -> (return type, [parameter types]) of every function named
+    prefix* declared in `header`."""
+    text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
     text = re.sub(r"#.*", "", text)
     protos = {}
-    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(sdq_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+    pat = r"([A-Za-z_][\w\s\*]*?)\b(" + prefix + r"[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;"
+    for m in re.finditer(pat, text):
         ret, name, params = " ".join(m.group(1).split()), m.group(2), m.group(3).strip()
         if params in ("", "void"):
             protos[name] = (ret, [])
@@ -145,3 +148,33 @@ def test_binding_signatures_match_the_header():
             assert res is ctypes.c_char_p, (name, ret)
         else:
             assert scalar[ret.replace("const ", "").strip()] is res, (name, ret, res)
+
+
+def test_host_shim_signatures_match_its_headers():
+    """The same for libsd_host.so's C shim (sd_dit_*, sd_rope_*), whose
+    argument types the binding sets on the loaded library."""
+    import sdq
+
+    scalar = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
+              "float": ctypes.c_float, "double": ctypes.c_double}
+    host = sdq.load_host_library()
+    protos = {}
+    for h in ("dit_block.h", "rope.h"):
+        protos.update(_prototypes(os.path.join(PKG, "host", "sd", h), "sd_"))
+    assert "sd_dit_block_forward" in protos and "sd_rope_table_3d" in protos
+    unbound = []
+    for name, (ret, params) in sorted(protos.items()):
+        fn = getattr(host, name)
+        if fn.argtypes is None:
+            unbound.append(name)
+            continue
+        assert len(fn.argtypes) == len(params), (name, params, fn.argtypes)
+        for p, a in zip(params, fn.argtypes):
+            if "*" in p:
+                assert a in (ctypes.c_void_p, ctypes.c_char_p) or issubclass(a, ctypes._Pointer), \
+                    (name, p, a)
+            else:
+                assert scalar.get(p.replace("const ", "").strip()) is a, (name, p, a)
+        want = ctypes.c_char_p if "*" in ret else scalar[ret.replace("const ", "").strip()]
+        assert fn.restype is want, (name, ret, fn.restype)
+    assert not unbound, f"declared but not bound by the binding: {unbound}"
