@@ -5,7 +5,8 @@
 // reference's sources where they lie, twice:
 //   _ref/ref_forward_cpu: with the reference's src/core/qgemm.cpp;
 //   _ref/ref_forward_gpu: without it, linked to libsd_qgemm.so (sd::qgemm on
-//     the MI355X, -DREF_FORWARD_GPU), the drop-in link of INTEGRATION.md.
+//     the MI355X, -DREF_FORWARD_GPU): the reference's link line with
+//     -lsd_qgemm -lsdq in place of qgemm.cpp.
 // Every other step (patch embeds, norms, attention, GELU, the bias pass of
 // mlin) is the same compiled reference code in both.
 //

@@ -3,11 +3,11 @@
 oracle/Makefile builds tests/cpp/ref_forward.cpp (OviDit::forward from the
 reference's model/ovi_dit.cpp, blocks.cpp, gemm.cpp, tensor.cpp and
 sdcpp.cpp, compiled where they lie) twice: with the reference's qgemm.cpp
-(ref_forward_cpu) and with libsd_qgemm.so in its place (ref_forward_gpu),
-the link INTEGRATION.md gives a maintainer. Every int8 Linear of the forward
-(ovi_dit.cpp:66-84, mlin: text embedding te0/te2 662-673, the M=1 time MLP
-tm2 and AdaLN projection tp1 678-700, every block Linear, the video head
-298-314) then goes through the GPU. Both builds run OviDitCfg::test()
+(ref_forward_cpu) and with libsd_qgemm.so in its place (ref_forward_gpu: the
+reference's own link line with -lsd_qgemm -lsdq for qgemm.cpp). Every int8
+Linear of the forward (ovi_dit.cpp:66-84, mlin: text embedding te0/te2
+662-673, the M=1 time MLP tm2 and AdaLN projection tp1 678-700, every block
+Linear, the video head 298-314) then goes through the GPU. Both builds run OviDitCfg::test()
 (ovi_dit.cpp:336-342) on one int8 pack and the same inputs; their outputs
 must be bit-identical. As in tests/test_ovit8.cpp:83-125, the int8 forward
 is also gated against the fp32 forward of the same weights (the pack written
