@@ -7,6 +7,7 @@
 // place of qgemm.cpp with one definition of every Tensor member.
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -27,7 +28,9 @@ void check_rc(int rc, const char* what) {
 // address can be reused for other contents (a pack unmapped and another
 // mapped in its place, weights rewritten in place), so each entry also keeps
 // a fingerprint of the contents: all of bs and the first and last rows of
-// Bq. A changed fingerprint replaces the device copy.
+// Bq. A changed fingerprint replaces the device copy. Entries are shared: a
+// call holds its weight until it returns, so a copy replaced or cleared by
+// another thread meanwhile is freed only after its last user is done.
 struct WeightKey {
   const void* q;
   const void* s;
@@ -36,8 +39,9 @@ struct WeightKey {
     return std::tie(q, s, N, K) < std::tie(o.q, o.s, o.N, o.K);
   }
 };
+using WeightRef = std::shared_ptr<sdq_weight>;
 struct CachedWeight {
-  sdq_weight* w;
+  WeightRef w;
   uint64_t print;
 };
 
@@ -56,24 +60,25 @@ uint64_t fingerprint(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t K) {
 }
 
 std::mutex g_cache_mu;
+// Never destroyed: no device memory is freed while the process exits.
 std::map<WeightKey, CachedWeight>& cache() {
-  static std::map<WeightKey, CachedWeight> m;
-  return m;
+  static auto* m = new std::map<WeightKey, CachedWeight>();
+  return *m;
 }
 
-sdq_weight* cached_weight(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t K) {
+WeightRef cached_weight(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t K) {
   const uint64_t print = fingerprint(Bq, bs, N, K);
   std::lock_guard<std::mutex> lk(g_cache_mu);
   WeightKey key{Bq.data, bs.data, N, K};
   auto it = cache().find(key);
   if (it != cache().end()) {
     if (it->second.print == print) return it->second.w;
-    sdq_weight_free(it->second.w);
-    cache().erase(it);
+    cache().erase(it);  // freed once no call holds it
   }
-  sdq_weight* w = nullptr;
-  check_rc(sdq_weight_upload(Bq.ptr<int8_t>(), bs.ptr<float>(), N, K, nullptr, &w),
+  sdq_weight* raw = nullptr;
+  check_rc(sdq_weight_upload(Bq.ptr<int8_t>(), bs.ptr<float>(), N, K, nullptr, &raw),
            "qgemm: weight upload");
+  WeightRef w(raw, [](sdq_weight* p) { sdq_weight_free(p); });
   cache().emplace(key, CachedWeight{w, print});
   return w;
 }
@@ -82,8 +87,7 @@ sdq_weight* cached_weight(const Tensor& Bq, const Tensor& bs, int64_t N, int64_t
 
 void qgemm_cache_clear() {
   std::lock_guard<std::mutex> lk(g_cache_mu);
-  for (auto& kv : cache()) sdq_weight_free(kv.second.w);
-  cache().clear();
+  cache().clear();  // each copy is freed once no call holds it
 }
 
 size_t qgemm_cache_size() {
@@ -102,8 +106,8 @@ void qgemm(const Tensor& A, const Tensor& Bq, const Tensor& bs, Tensor& out) {
   if (bs.numel() != N) throw std::runtime_error("qgemm: bs must have N entries");
   out = Tensor({M, N}, DType::F32);
   if (M == 0 || N == 0 || K == 0) return;  // zero-filled, src/core/qgemm.cpp:74-76
-  sdq_weight* w = cached_weight(Bq, bs, N, K);
-  check_rc(sdq_qlinear_host(w, A.ptr<float>(), M, K, nullptr, out.data), "qgemm");
+  const WeightRef w = cached_weight(Bq, bs, N, K);  // held until the call has returned
+  check_rc(sdq_qlinear_host(w.get(), A.ptr<float>(), M, K, nullptr, out.data), "qgemm");
 }
 
 }  // namespace sd

@@ -50,7 +50,9 @@ struct Tensor {
 // checked on every call: new contents at a cached address are uploaded
 // again. A change confined to Bq's middle rows is not seen, so a caller that
 // rewrites weights in place or releases a pack calls qgemm_cache_clear(),
-// which also frees the device copies.
+// which also frees the device copies. Safe to call from several threads: a
+// device copy that one thread replaces or clears while another thread's call
+// uses it is freed when that call returns.
 // Unlike the reference, shape mismatches throw std::runtime_error("qgemm: …")
 // instead of reading out of bounds; GPU failures throw too.
 void qgemm(const Tensor& A, const Tensor& Bq, const Tensor& bs, Tensor& out);

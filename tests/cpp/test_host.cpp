@@ -5,9 +5,11 @@
 //   sdcpp <pack>                    list entries: name code ndim dims... off soff
 //   sdcpp_err <pack>                exit 0 iff load_sdcpp throws (prints what())
 //   qgemm M K N A.bin Bq.bin bs.bin out.bin
+//   qgemm_threads M K N A.bin Bq.bin bs.bin out.bin threads reps
 //   linear <pack> <base> in out M mode x.bin gate.bin res.bin out.bin
 //          mode: mlin | gelu | gated | add   (gate/res ignored when unused)
 //   linear_err <pack> <base> in out  exit 0 iff qlinear_from_pack throws
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -15,6 +17,7 @@
 #include <iterator>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "sd/qlinear.h"
@@ -82,6 +85,53 @@ static int cmd_sdcpp_err(const std::string& path) {
   return 1;
 }
 
+// `threads` threads each call sd::qgemm `reps` times on the same weights while
+// another thread keeps clearing the weight cache, so device copies are
+// dropped from the cache while calls still use them. Every result must equal
+// the first; that one is written for the oracle comparison.
+static int cmd_qgemm_threads(char** argv) {
+  gpu::check(sdq_init(0), "sdq_init");
+  const int64_t M = std::atoll(argv[2]), K = std::atoll(argv[3]), N = std::atoll(argv[4]);
+  const int threads = std::atoi(argv[9]), reps = std::atoi(argv[10]);
+  const Tensor A = load_tensor(argv[5], {M, K}, DType::F32);
+  const Tensor Bq = load_tensor(argv[6], {N, K}, DType::I8);
+  const Tensor bs = load_tensor(argv[7], {N}, DType::F32);
+  Tensor first;
+  qgemm(A, Bq, bs, first);
+  std::atomic<int> bad{0}, calls{0}, clears{0};
+  std::atomic<bool> done{false};
+  std::vector<std::thread> pool;
+  for (int t = 0; t < threads; t++)
+    pool.emplace_back([&] {
+      try {
+        for (int r = 0; r < reps; r++) {
+          Tensor out;
+          qgemm(A, Bq, bs, out);
+          calls++;
+          if (std::memcmp(out.data, first.data, first.nbytes) != 0) bad++;
+        }
+      } catch (const std::exception& e) {
+        std::fprintf(stderr, "worker: %s\n", e.what());
+        bad++;
+      }
+    });
+  std::thread clearer([&] {
+    while (!done.load()) {
+      qgemm_cache_clear();
+      clears++;
+      std::this_thread::yield();
+    }
+  });
+  for (auto& th : pool) th.join();
+  done = true;
+  clearer.join();
+  qgemm_cache_clear();
+  std::printf("calls %d mismatches %d clears %d cache entries %zu\n", calls.load(), bad.load(),
+              clears.load(), qgemm_cache_size());
+  write_file(argv[8], first.data, first.nbytes);
+  return bad.load() == 0 ? 0 : 1;
+}
+
 int main(int argc, char** argv) {
   if (argc < 2) {
     std::fprintf(stderr, "usage: test_host <cmd> ...\n");
@@ -122,6 +172,7 @@ int main(int argc, char** argv) {
       write_file(std::string(argv[8]) + ".rewritten", out3.data, out3.nbytes);
       return 0;
     }
+    if (cmd == "qgemm_threads" && argc == 11) return cmd_qgemm_threads(argv);
     if (cmd == "linear" && argc == 12) {
       gpu::check(sdq_init(0), "sdq_init");
       std::shared_ptr<void> owner;

@@ -255,6 +255,26 @@ def test_sd_qgemm_host_tensor_api(tmp_path, sdq_dev, oracle):
 
 
 @pytest.mark.gpu
+def test_sd_qgemm_cache_under_threads(tmp_path, sdq_dev, oracle):
+    """Four threads call sd::qgemm on the same weights while a fifth keeps
+    clearing the weight cache: a device copy dropped from the cache while a
+    call uses it must stay valid until that call returns, and every result
+    stays bit-exact."""
+    M, K, N = 96, 768, 512
+    A = oracle.randn(M * K, 5).reshape(M, K)
+    W = oracle.randn(N * K, 6).reshape(N, K) * np.float32(0.02)
+    q, s = oracle.quant_rows(W)
+    for nm, arr in (("A", A), ("q", q), ("s", s)):
+        arr.tofile(tmp_path / f"{nm}.bin")
+    r = run("qgemm_threads", M, K, N, tmp_path / "A.bin", tmp_path / "q.bin",
+            tmp_path / "s.bin", tmp_path / "o.bin", 4, 25)
+    assert "calls 100 mismatches 0" in r.stdout, r.stdout
+    assert r.stdout.rstrip().endswith("cache entries 0"), r.stdout
+    got = np.fromfile(tmp_path / "o.bin", np.float32).reshape(M, N)
+    assert_bitexact(got, oracle.qgemm(A, q, s), "sd::qgemm under threads")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode", ["mlin", "gelu", "gated", "add"])
 def test_qlinear_from_pack(tmp_path, sdq_dev, oracle, mode):
     p = str(tmp_path / "f.sdcpp")
