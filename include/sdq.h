@@ -30,6 +30,11 @@
  * message. Device pointers are plain HIP device addresses; `stream` is a
  * hipStream_t passed as void* (NULL = the null stream). Functions named
  * *_host take host pointers and are synchronous.
+ *
+ * Size limits (the kernels' in-tile offsets and tile counters are 32-bit):
+ * a weight has at most 2^20 outputs (N) and 2^22 inputs (K); a GEMM call has
+ * at most 2^30 rows (M) and M*N under 2^40. Larger shapes are refused with
+ * SDQ_ERR_INVALID before anything is allocated or launched.
  */
 #ifndef SDQ_H_
 #define SDQ_H_

@@ -216,8 +216,26 @@ int check_weight(const sdq_weight* w, int64_t K) {
   return SDQ_OK;
 }
 
+// Size limits of the GEMM kernels, whose in-tile offsets, panel sizes and
+// tile counters are 32-bit: a weight of at most 2^20 outputs and 2^22 inputs,
+// at most 2^30 rows per call, and fewer than 2^40 output values.
+constexpr int64_t kMaxWeightN = int64_t(1) << 20;
+constexpr int64_t kMaxWeightK = int64_t(1) << 22;
+constexpr int64_t kMaxRows = int64_t(1) << 30;
+constexpr int64_t kMaxOutputs = int64_t(1) << 40;
+
+int check_rows(int64_t M, int64_t N, const std::string& tag) {
+  if (M > kMaxRows) return set_error(SDQ_ERR_INVALID, tag + "M too large (at most 2^30 rows)");
+  if (M * N >= kMaxOutputs)
+    return set_error(SDQ_ERR_INVALID, tag + "output too large (M*N must stay under 2^40)");
+  return SDQ_OK;
+}
+
 int alloc_weight(int dev, int64_t N, int64_t K, sdq_weight** out) {
   if (N < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative weight dims");
+  if (N > kMaxWeightN || K > kMaxWeightK)
+    return set_error(SDQ_ERR_INVALID, "weight too large: N at most 2^20, K at most 2^22 (N=" +
+                                          std::to_string(N) + ", K=" + std::to_string(K) + ")");
   const int64_t Np = round_up(N < 1 ? 1 : N, kRowAlign);
   const int64_t KFp = kfrags_padded(K);
   const int64_t bytes = (Np / kFragRows) * KFp * kFragBytes;
@@ -317,7 +335,7 @@ int qlinear_device(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if (!Y) return set_error(SDQ_ERR_INVALID, "null Y");
   if ((rc = ensure_device(w->device))) return rc;
   const int64_t N = w->N;
-  if (M > (int64_t(1) << 30)) return set_error(SDQ_ERR_INVALID, "M too large");
+  if ((rc = check_rows(M, N, ""))) return rc;
 
   const int cfg = choose_gemm_cfg(M, N, w->KFp, epi ? epi->kind : SDQ_EPI_NONE,
                                   g_dev[w->device].cu_count);
@@ -1056,6 +1074,7 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream) {
     if ((rc = check_weight(it.w, it.w->K))) return rc;
     if ((rc = validate_epi(&it.epi))) return rc;
     if (it.M < 0) return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": negative M");
+    if ((rc = check_rows(it.M, it.w->N, "group item " + std::to_string(i) + ": "))) return rc;
     if (it.M > 0 && it.w->N > 0 && ((!it.A && it.w->K > 0) || !it.Y))
       return set_error(SDQ_ERR_INVALID, "group item " + std::to_string(i) + ": null A or Y");
   }
@@ -1229,6 +1248,7 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
     if ((rc = check_weight(it.w, it.w->K))) return rc;
     if ((rc = validate_epi(&it.epi))) return rc;
     if (it.M < 0) return set_error(SDQ_ERR_INVALID, tag + ": negative M");
+    if ((rc = check_rows(it.M, it.w->N, tag + ": "))) return rc;
     if (it.M > 0 && it.w->N > 0 && ((!it.A && it.w->K > 0) || !it.Y))
       return set_error(SDQ_ERR_INVALID, tag + ": null A or Y");
   }
@@ -1240,6 +1260,7 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
     if (ffn->fc2->K != ffn->fc1->N || ffn->fc2->N != ffn->fc1->K)
       return set_error(SDQ_ERR_INVALID, "stack: need fc1 [F,D] and fc2 [D,F]");
     if (ffn->M < 0) return set_error(SDQ_ERR_INVALID, "stack: negative FFN M");
+    if ((rc = check_rows(ffn->M, ffn->fc1->N, "stack FFN: "))) return rc;
     if (has_ffn && ((!ffn->h && ffn->fc1->K > 0) || !ffn->gate || !ffn->hid || !ffn->x))
       return set_error(SDQ_ERR_INVALID, "stack: null FFN h, gate, hid or x");
   }
@@ -1728,6 +1749,7 @@ int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
   if ((rc = validate_epi(epi))) return rc;
   if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
   const int64_t N = w->N;
+  if ((rc = check_rows(M, N, ""))) return rc;
   if (M == 0 || N == 0) return SDQ_OK;
   int dev = -1;
   if ((rc = current_device(&dev))) return rc;
@@ -1780,6 +1802,8 @@ int sdq_qlinear_host(const sdq_weight* w, const float* A, int64_t M, int64_t K,
 
 int sdq_act_quant(const float* A, int64_t M, int64_t K, int8_t* aq, float* as, void* stream) {
   if (M < 0 || K < 0) return set_error(SDQ_ERR_INVALID, "negative dims");
+  if (M > kMaxRows || K > kMaxWeightK)
+    return set_error(SDQ_ERR_INVALID, "act_quant: at most 2^30 rows of at most 2^22 values");
   if (M == 0) return SDQ_OK;
   if (!as || (K > 0 && (!A || !aq))) return set_error(SDQ_ERR_INVALID, "null pointer");
   int dev = -1;
@@ -1869,8 +1893,9 @@ int sdq_qlinear_noalloc(const sdq_weight* w, const float* A, int64_t M, int64_t 
 int sdq_qlinear_plan(const sdq_weight* w, int64_t M, int epi_kind, sdq_gemm_plan* out) {
   if (!w || !out) return set_error(SDQ_ERR_INVALID, "null weight or out");
   if (M < 0) return set_error(SDQ_ERR_INVALID, "negative M");
-  int rc = ensure_device(w->device);
+  int rc = check_rows(M, w->N, "");
   if (rc) return rc;
+  if ((rc = ensure_device(w->device))) return rc;
   std::memset(out, 0, sizeof(*out));
   out->splitk = 1;
   if (M == 0 || w->N == 0) return SDQ_OK;

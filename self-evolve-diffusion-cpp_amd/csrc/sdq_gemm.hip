@@ -1127,6 +1127,7 @@ hipError_t run_tiled(const int8_t* wt, const float* bs, const int8_t* at, const 
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m;
   if (T <= 0) return hipSuccess;
+  if (T > 0x3FFFFFFF) return hipErrorInvalidValue;  // the kernel counts tiles in 32 bits
   if (KFp % KS != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL((qgemm_tiled<BN, BM, WN, WM, KS, STAGES>), dim3((unsigned)T),
                      dim3(WN * WM * 64), 0, s, wt, bs, at, as, M, N, KFp, tiles_n, tiles_m, epi, Y,
@@ -1141,6 +1142,7 @@ hipError_t run_persist(const int8_t* wt, const ColOps& cols, const int8_t* at, c
   const int tiles_n = (int)ceil_div(N, BN), tiles_m = (int)ceil_div(M, BM);
   const int64_t T = (int64_t)tiles_n * tiles_m * splits;
   if (T <= 0) return hipSuccess;
+  if (T > 0x3FFFFFFF) return hipErrorInvalidValue;  // the kernel counts work items in 32 bits
   // K > 0 and at least STAGES stages per work item: the epilogue has no
   // K == 0 case
   if (splits < 1 || KFp % (KS * splits) != 0 || KFp / splits / KS < STAGES || epi.kzero)

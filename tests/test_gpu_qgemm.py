@@ -350,6 +350,37 @@ def test_errors_are_reported(sdq_dev):
         sdq.qlinear(w, torch.zeros((4, 16), device=sdq_dev), Y, kind="gated")
 
 
+def test_size_limits_are_refused(sdq_dev):
+    """Shapes past the GEMM kernels' 32-bit offsets and tile counters are
+    refused through the C ABI before anything is read, allocated or launched
+    (the small buffers passed here are never touched)."""
+    import torch
+
+    import sdq
+
+    lib = sdq._lib
+    q, s = np.ones(64, np.int8), np.ones(16, np.float32)
+    for N, K in ((2**20 + 1, 16), (4, 2**22 + 1)):
+        out = ctypes.c_void_p()
+        rc = lib.sdq_weight_upload(q.ctypes.data, s.ctypes.data, N, K, None, ctypes.byref(out))
+        assert rc == sdq.ERR_INVALID and b"weight too large" in lib.sdq_last_error(), (N, K)
+        assert not out.value
+    w = sdq.Weight.from_host(np.ones((8, 16), np.int8), np.ones(8, np.float32))
+    A = torch.zeros((4, 16), device=sdq_dev)
+    Y = torch.zeros((4, 8), device=sdq_dev)
+    e = sdq.make_epilogue()
+    pa, py = ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(Y.data_ptr())
+    rc = lib.sdq_qlinear(w.h, pa, 2**30 + 1, 16, ctypes.byref(e), py, None)
+    assert rc == sdq.ERR_INVALID and b"M too large" in lib.sdq_last_error()
+    item = sdq.GroupItem(w.h, pa, 2**30 + 1, e, py)
+    rc = lib.sdq_qlinear_group(ctypes.byref(item), 1, None)
+    assert rc == sdq.ERR_INVALID and b"group item 0: M too large" in lib.sdq_last_error()
+    rc = lib.sdq_act_quant(pa, 4, 2**22 + 1, py, py, None)
+    assert rc == sdq.ERR_INVALID and b"2^22" in lib.sdq_last_error()
+    torch.cuda.synchronize()
+    assert float(Y.abs().sum()) == 0.0  # nothing ran
+
+
 def test_host_pointer_entry_point(sdq_dev, oracle):
     import sdq
 
