@@ -20,8 +20,8 @@
 #include <thread>
 #include <vector>
 
+#include "sd/pack.h"
 #include "sd/qlinear.h"
-#include "sd/sdcpp.h"
 #include "sd/tensor.h"
 
 using namespace sd;

@@ -71,7 +71,7 @@ def test_host_mirror_headers_compile_standalone(tmp_path):
     """The C++17 mirror of the reference interface builds with plain g++."""
     src = tmp_path / "use.cpp"
     src.write_text(
-        '#include "sd/tensor.h"\n#include "sd/sdcpp.h"\n#include "sd/qlinear.h"\n'
+        '#include "sd/tensor.h"\n#include "sd/pack.h"\n#include "sd/qlinear.h"\n'
         "int main(){ sd::Tensor t({2,3}, sd::DType::F32); return (int)t.numel() - 6; }\n")
     exe = tmp_path / "use"
     r = subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), "-I",
