@@ -155,6 +155,13 @@ int sdq_weight_export_host(const sdq_weight* w, int8_t* q, float* scale);
  * contiguous). K must equal the weight's K. M == 0 is a no-op; K == 0 gives
  * y = 0 (then bias/epilogue), matching the zero-filled Tensor the reference
  * returns (src/core/qgemm.cpp:74-76). Stream-ordered; no host sync.
+ * Scratch (quantized activations, row scales, split-K partials) comes from a
+ * workspace per (device, stream) that grows, never shrinks, when a call needs
+ * more than any call before it on that stream; growing synchronizes the
+ * stream and allocates. Under HIP-graph capture such a call is refused with
+ * SDQ_ERR_INVALID before anything is queued (the capture stays usable); one
+ * call of the same shape on the stream before the capture makes the captured
+ * call allocation-free, and its graph replays bit-identical results.
  * Replaces: sd::qgemm (src/core/tensor.h:52) + mlin's bias pass
  * (src/model/ovi_dit.cpp:66-84) + the consumer named by epi->kind. */
 int sdq_qlinear(const sdq_weight* w, const float* A, int64_t M, int64_t K, const sdq_epilogue* epi,
@@ -213,7 +220,7 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
 
 /* sdq_qlinear for callers that cannot allocate device memory (tight serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
- * Capturing it into a HIP graph is untested and unsupported. The same results as sdq_qlinear, bit for
+ * It can be captured into a HIP graph with no warm-up call. The same results as sdq_qlinear, bit for
  * bit, with no hipMalloc / hipFree or other allocation on any call: the
  * quantized activations and the GEMM's other scratch live in a static device
  * array of SDQ_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).
@@ -373,7 +380,9 @@ int sdq_stream_sync(void* stream);
 /* Work enqueued on `waiter` after this call starts only after the work
  * enqueued on `signaler` before it has finished (an event recorded on
  * signaler, waited on by waiter; the host does not block). The same stream
- * twice: nothing to do. No counterpart in the reference (one CPU thread pool,
+ * twice: nothing to do. The event is one per host thread and device, kept
+ * for the life of the process, so the call can be captured into a graph (it
+ * then joins the two streams in the capture). No counterpart in the reference (one CPU thread pool,
  * no streams): the twin-layer pair forward forks the two branches' FFNs onto
  * two streams and joins them with it. */
 int sdq_stream_wait(void* waiter, void* signaler);

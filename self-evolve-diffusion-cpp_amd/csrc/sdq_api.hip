@@ -145,10 +145,20 @@ int ensure_device(int dev) {
 
 // Grows (never shrinks) the workspace of (dev, stream). A buffer that is
 // replaced may still be read by work queued on `stream`, so the stream is
-// drained before the old buffer is freed.
+// drained before the old buffer is freed. A stream that is capturing a graph
+// can be neither drained nor given new memory: the call is refused with an
+// error that leaves the capture intact (a call of the same size or larger on
+// the stream before the capture grows it in advance).
 int grow(hipStream_t s, void** p, size_t* have, size_t need) {
   if (*have >= need) return SDQ_OK;
-  hipError_t e = hipStreamSynchronize(s);
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &st);
+  if (e != hipSuccess) return hip_error(e, "hipStreamIsCapturing");
+  if (st != hipStreamCaptureStatusNone)
+    return set_error(SDQ_ERR_INVALID,
+                     "the stream's workspace would have to grow while the stream captures a "
+                     "graph: make the same call once on this stream before the capture");
+  e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
   if (*p) (void)hipFree(*p);
   *p = nullptr;
@@ -1856,15 +1866,26 @@ int sdq_stream_sync(void* stream) {
 
 int sdq_stream_wait(void* waiter, void* signaler) {
   if (waiter == signaler) return SDQ_OK;
-  hipEvent_t ev = nullptr;
-  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-  if (e != hipSuccess) return hip_error(e, "hipEventCreateWithFlags");
+  // One event per thread and device, made once and kept: a wait takes the
+  // event's latest record at the time of the call, so recording it again
+  // later leaves earlier waits alone, and an event a graph capture recorded
+  // is never destroyed under it.
+  thread_local hipEvent_t t_ev[kMaxDev] = {};
+  int dev = -1;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  hipEvent_t& ev = t_ev[dev];
+  hipError_t e = hipSuccess;
+  if (!ev) {
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      ev = nullptr;
+      return hip_error(e, "hipEventCreateWithFlags");
+    }
+  }
   e = hipEventRecord(ev, static_cast<hipStream_t>(signaler));
   if (e == hipSuccess) e = hipStreamWaitEvent(static_cast<hipStream_t>(waiter), ev, 0);
-  // destroying a pending event is allowed: its resources go when it completes
-  const hipError_t d = hipEventDestroy(ev);
   if (e != hipSuccess) return hip_error(e, "stream wait");
-  if (d != hipSuccess) return hip_error(d, "hipEventDestroy");
   return SDQ_OK;
 }
 
