@@ -198,7 +198,11 @@ int sdq_qlinear_group(const sdq_group_item* items, int n, void* stream);
  * projection just updated), then the FFN when `ffn` is not NULL (as
  * sdq_ffn). Same results as those calls made one after the other, bit for
  * bit; the difference is that every input (the items' A and the FFN's h) is
- * quantized by one launch before any GEMM runs. So no output (an item's Y,
+ * quantized by one launch before any GEMM runs, and that the first later
+ * item, when it adds into the output a grouped item adds into (both GATED or
+ * RESID in place, same shape), joins the grouped launch: the two plain
+ * outputs go to scratch and one elementwise pass applies both residual steps
+ * in order. So no output (an item's Y,
  * the FFN's hid or x) may overlap any of those inputs, and no output of the
  * first ngroup items may overlap another of their outputs or residuals
  * (SDQ_ERR_INVALID). Replaces: the separate mlin calls of block_self_fwd,

@@ -1357,6 +1357,28 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
                         ffn->gate_fma, ffn->hid, ffn->x, s, nullptr);
     return SDQ_OK;
   }
+  // The first Linear after the group, when it adds into what a grouped
+  // Linear adds into (the cross output projection after the self-attention
+  // output, both into x: ovi_dit.cpp:187, 251), joins the grouped launch:
+  // both write their plain outputs (bias included) to scratch, and one
+  // elementwise pass applies the two residual epilogues to the target in
+  // their order, the same bits as the two GEMM epilogues one after the other.
+  // (SDQ_NO_STACK_FOLD: the separate launch, for comparisons.)
+  int fold_g = -1;
+  const int fold_s = ngroup;
+  if (fast && ngroup < n && !std::getenv("SDQ_NO_STACK_FOLD")) {
+    const sdq_group_item& S = items[fold_s];
+    auto adds = [](const sdq_group_item& it) {
+      return it.M > 0 && it.w->N > 0 && it.epi.resid == it.Y &&
+             (it.epi.kind == SDQ_EPI_GATED || it.epi.kind == SDQ_EPI_RESID);
+    };
+    if (adds(S) && groupable(S, cu_count))
+      for (int j = 0; j < ngroup; j++) {
+        const sdq_group_item& G = items[j];
+        if (G.Y == S.Y && adds(G) && G.M == S.M && G.w->N == S.w->N && same_group(G, S))
+          fold_g = j;
+      }
+  }
   // scratch: per input its quantized rows (padded to its GEMM's tile), row
   // scales and padded column copies
   size_t off = 0;
@@ -1366,6 +1388,12 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
     return o;
   };
   const size_t sink_off = take(4096);
+  size_t yg_off = 0, ys_off = 0;  // the folded pair's plain outputs
+  if (fold_g >= 0) {
+    const size_t b = (size_t)(items[fold_s].M * items[fold_s].w->N) * sizeof(float);
+    yg_off = take(b);
+    ys_off = take(b);
+  }
   struct Carve {
     size_t at, as, cols;
     int seg;
@@ -1453,13 +1481,19 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
   hipError_t e = launch_act_quant_segs(qs, s);
   if (e != hipSuccess) return hip_error(e, "stack act_quant launch");
   mark();
-  // the independent items: one grouped launch per set with the same K
+  // the independent items (and a folded one): one grouped launch per set
+  // with the same K
+  std::vector<int> members;
+  for (int j = 0; j < ngroup; j++) members.push_back(j);
+  if (fold_g >= 0) members.push_back(fold_s);
   std::vector<bool> done(n, false);
-  for (int j = 0; j < ngroup; j++) {
+  for (size_t a = 0; a < members.size(); a++) {
+    const int j = members[a];
     if (done[j] || cv[j].seg < 0) continue;
     GemmGroup g{};
     const sdq_group_item& first = items[j];
-    for (int k = j; k < ngroup; k++) {
+    for (size_t b = a; b < members.size(); b++) {
+      const int k = members[b];
       const sdq_group_item& it = items[k];
       if (done[k] || cv[k].seg < 0 || !same_group(first, it)) continue;
       done[k] = true;
@@ -1477,18 +1511,34 @@ int sdq_qlinear_stack(const sdq_group_item* items, int n, int ngroup, const sdq_
       p.N = (int)it.w->N;
       p.kind = it.epi.kind;
       p.gate_fma = it.epi.gate_fma;
+      if (fold_g >= 0 && (k == fold_g || k == fold_s)) {  // plain output into scratch
+        p.kind = SDQ_EPI_NONE;
+        p.gate = nullptr;
+        p.resid = nullptr;
+        p.Y = base + (k == fold_g ? yg_off : ys_off);
+      }
     }
     EpiArgs ea = make_epi(&first.epi, first.w->K);
     ea.bias = ea.gate = ea.resid = nullptr;  // per problem, from the table
     e = launch_qgemm_group(g, first.w->KFp, ea, sink, cu_count, s);
     if (e != hipSuccess) return hip_error(e, "stack grouped qgemm launch");
   }
+  if (fold_g >= 0) {
+    const sdq_group_item& G = items[fold_g];
+    const sdq_group_item& S = items[fold_s];
+    const ResidStep ra{reinterpret_cast<const float*>(base + yg_off), G.epi.gate, G.epi.kind,
+                       G.epi.gate_fma};
+    const ResidStep rb{reinterpret_cast<const float*>(base + ys_off), S.epi.gate, S.epi.kind,
+                       S.epi.gate_fma};
+    e = launch_resid2(static_cast<float*>(S.Y), S.M, S.w->N, ra, rb, s);
+    if (e != hipSuccess) return hip_error(e, "stack residual launch");
+  }
   mark();
   // then the others, in order
   int tail = 0;
   for (int i = ngroup; i < n; i++) {
     const sdq_group_item& it = items[i];
-    if (cv[i].seg < 0) continue;
+    if (cv[i].seg < 0 || (fold_g >= 0 && i == fold_s)) continue;
     const QuantSeg& q = qs.s[cv[i].seg];
     const EpiArgs ea = make_epi(&it.epi, it.w->K);
     const GemmAux aux{q.cc.bias_pad, q.cc.gate_pad, sink, cu_count, 1, nullptr, nullptr, &tail,

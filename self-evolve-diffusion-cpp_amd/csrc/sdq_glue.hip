@@ -213,6 +213,34 @@ add_kernel(float* x, const float* y, int64_t n) {
   if (i < n) x[i] = x[i] + y[i];
 }
 
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+// The residual step as the GEMM epilogue applies it (contraction is off
+// outside the explicit fma).
+__device__ __forceinline__ float resid_apply(float x, float y, float g, int kind, int fma) {
+  if (kind == SDQ_EPI_RESID) return x + y;
+  return fma ? __builtin_fmaf(y, g, x) : x + y * g;
+}
+
+// Four consecutive columns per thread: i indexes float4 groups of x.
+__global__ void __launch_bounds__(256)
+resid2_kernel(float* __restrict__ x, int64_t n4, int64_t N4, ResidStep a, ResidStep b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  const int64_t c = i % N4;
+  v4f_t v = reinterpret_cast<const v4f_t*>(x)[i];
+  const v4f_t ya = reinterpret_cast<const v4f_t*>(a.y)[i];
+  const v4f_t yb = reinterpret_cast<const v4f_t*>(b.y)[i];
+  const v4f_t ga = a.gate ? reinterpret_cast<const v4f_t*>(a.gate)[c] : v4f_t{0.f, 0.f, 0.f, 0.f};
+  const v4f_t gb = b.gate ? reinterpret_cast<const v4f_t*>(b.gate)[c] : v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float t = resid_apply(v[e], ya[e], ga[e], a.kind, a.gate_fma);
+    v[e] = resid_apply(t, yb[e], gb[e], b.kind, b.gate_fma);
+  }
+  reinterpret_cast<v4f_t*>(x)[i] = v;
+}
+
 }  // namespace
 
 hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* st, const float* w,
@@ -227,6 +255,19 @@ hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* s
 hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(add_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_resid2(float* x, int64_t M, int64_t N, const ResidStep& a, const ResidStep& b,
+                         hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  auto ok = [](int k) { return k == SDQ_EPI_GATED || k == SDQ_EPI_RESID; };
+  if (N % 4 != 0 || !ok(a.kind) || !ok(b.kind) || !a.y || !b.y ||
+      (a.kind == SDQ_EPI_GATED && !a.gate) || (b.kind == SDQ_EPI_GATED && !b.gate))
+    return hipErrorInvalidValue;
+  const int64_t n4 = M * N / 4;
+  hipLaunchKernelGGL(resid2_kernel, dim3((unsigned)ceil_div(n4, 256)), dim3(256), 0, s, x, n4,
+                     N / 4, a, b);
   return hipGetLastError();
 }
 

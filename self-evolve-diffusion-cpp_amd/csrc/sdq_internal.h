@@ -143,6 +143,20 @@ hipError_t launch_ln_apply(const float* x, int64_t M, int64_t K, const float2* s
                            const float* b, float* y, hipStream_t s);
 // x[i] += y[i], i < n.
 hipError_t launch_add(float* x, const float* y, int64_t n, hipStream_t s);
+// One residual epilogue of a Linear applied to x from the Linear's plain
+// output y (the NONE epilogue, bias included): GATED x = fma(y, g, x) (or
+// x + fl(y*g)), RESID x = x + y.
+struct ResidStep {
+  const float* y;     // [M, N]
+  const float* gate;  // [N] (GATED)
+  int kind;           // SDQ_EPI_GATED or SDQ_EPI_RESID
+  int gate_fma;
+};
+// x[M, N] = b(a(x)): two Linears' residual epilogues in order, from outputs
+// computed apart; the same bits as the two GEMMs applying them one after the
+// other. N % 4 == 0 and every array 16-byte aligned.
+hipError_t launch_resid2(float* x, int64_t M, int64_t N, const ResidStep& a, const ResidStep& b,
+                         hipStream_t s);
 // y[M,N] = x[M,K] . w[K,N] (+ bias): one fmaf chain per output over k in
 // order from +0, then + bias (sd::matmul's per-output steps).
 hipError_t launch_linear_f32(const float* x, int64_t M, int64_t K, const float* w, int64_t N,
