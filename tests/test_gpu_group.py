@@ -327,3 +327,30 @@ def test_stack_random_sets(sdq_dev, oracle, i):
     got, want = _stack_case(sdq, torch, oracle, sdq_dev, group, seq, ffn, 1300 + 50 * i)
     for j, (g, w) in enumerate(zip(got, want)):
         assert_bitexact(g, w, f"random stack {i}: output {j}")
+
+
+@pytest.mark.parametrize("fold", [True, False], ids=["fold", "nofold"])
+@pytest.mark.parametrize("s_kind", ["gated", "gated_nofma", "resid"])
+@pytest.mark.parametrize("g_kind", ["gated", "gated_nofma", "resid"])
+def test_stack_folded_residual_pair(sdq_dev, oracle, monkeypatch, g_kind, s_kind, fold):
+    """The first later item adds into the output a grouped item adds into
+    (every pair of residual forms, with and without bias): the stack runs it
+    in the grouped launch, both plain outputs to scratch and one elementwise
+    pass applying the two residual steps in order. A second later item and
+    the FFN then add into the same output after it. Bit for bit against the
+    separate calls, with the fold and with it switched off
+    (SDQ_NO_STACK_FOLD)."""
+    import torch
+
+    import sdq
+
+    if not fold:
+        monkeypatch.setenv("SDQ_NO_STACK_FOLD", "1")
+    D = 512
+    specs = [(300, D, 3 * D, "none", True), (300, D, D, g_kind, s_kind != "resid"),
+             (200, D, 2 * D, "none", False)]
+    seq = [(300, D, D, s_kind, g_kind == "resid"), (300, D, D, "resid", True)]
+    print(f"[stack-fold] {g_kind} then {s_kind} fold={fold}", flush=True)
+    got, want = _stack_case(sdq, torch, oracle, sdq_dev, specs, seq, (300, D, 2 * D), 4100, chain=1)
+    for j, (g, w) in enumerate(zip(got, want)):
+        assert_bitexact(g, w, f"fold {g_kind}+{s_kind} ({fold}): output {j}")
