@@ -85,18 +85,28 @@ __device__ __forceinline__ uint4 pack16(const float v[16], float inv) {
 // by the eight lanes l = row + 8j that share the row (lane l takes every
 // eighth float4 from l / 8), then combined across them; `ok` (the row
 // exists) is the same on all eight. Every lane must call it. NaN never
-// enters the maxima, and max is exact and order-free.
+// enters the maxima, and max is exact and order-free. Each lane issues up
+// to eight float4 loads before it uses any (one memory latency for up to
+// 256 maxima per row, e.g. a 14336-column fc1's 224, instead of one per
+// load); the zeros past the end cannot win, as the maxima are >= 0.
 __device__ __forceinline__ float premax_row(const float* __restrict__ pm, int pc, bool ok,
                                             int l) {
   float mx = 0.f;
   if (ok) {
     const float4* p4 = reinterpret_cast<const float4*>(pm);
-    for (int j = l >> 3; j < pc / 4; j += 8) {
-      const float4 r = p4[j];
-      mx = (mx < r.x) ? r.x : mx;
-      mx = (mx < r.y) ? r.y : mx;
-      mx = (mx < r.z) ? r.z : mx;
-      mx = (mx < r.w) ? r.w : mx;
+    const int n4 = pc / 4;
+    for (int j0 = l >> 3; j0 < n4; j0 += 64) {
+      float4 r[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        r[u] = j0 + 8 * u < n4 ? p4[j0 + 8 * u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        mx = (mx < r[u].x) ? r[u].x : mx;
+        mx = (mx < r[u].y) ? r[u].y : mx;
+        mx = (mx < r[u].z) ? r[u].z : mx;
+        mx = (mx < r[u].w) ? r[u].w : mx;
+      }
     }
     for (int j = (pc & ~3) + (l >> 3); j < pc; j += 8) mx = (mx < pm[j]) ? pm[j] : mx;
   }
