@@ -338,14 +338,17 @@ def _read_ref_caller(path):
     raw = open(path, "rb").read()
     M, K, N = struct.unpack_from("<3q", raw, 0)
     o = 24
-    A = np.frombuffer(raw, np.float32, M * K, o).reshape(M, K)
-    o += 4 * M * K
-    Wq = np.frombuffer(raw, np.int8, N * K, o).reshape(N, K)
-    o += N * K
-    sc = np.frombuffer(raw, np.float32, N, o)
-    o += 4 * N
-    out = np.frombuffer(raw, np.float32, M * N, o).reshape(M, N)
-    assert o + 4 * M * N == len(raw)
+    def take(dtype, count, shape):
+        nonlocal o
+        a = (np.frombuffer(raw, dtype, count, o) if count else np.zeros(0, dtype)).reshape(shape)
+        o += a.nbytes
+        return a
+
+    A = take(np.float32, M * K, (M, K))
+    Wq = take(np.int8, N * K, (N, K))
+    sc = take(np.float32, N, (N,))
+    out = take(np.float32, M * N, (M, N))
+    assert o == len(raw)
     return A, Wq, sc, out
 
 
@@ -373,11 +376,13 @@ def test_ref_caller_links_without_a_second_tensor():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,K,N", [(17, 31, 13), (64, 1024, 512), (300, 3072, 1000),
-                                   (2100, 640, 384)])
+                                   (2100, 640, 384), (0, 64, 32), (5, 0, 7), (5, 64, 0)])
 def test_ref_caller_bitexact(tmp_path, oracle, M, K, N):
     """A program written against the reference's src/core/tensor.h, linked with
     the reference's tensor.cpp and libsd_qgemm.so, gets the reference's qgemm
-    output bit for bit (test_core.cpp's seeds: randu 7+M for A, 13+N for W)."""
+    output bit for bit (test_core.cpp's seeds: randu 7+M for A, 13+N for W),
+    including the empty shapes for which the reference returns its zero-filled
+    output (qgemm.cpp:74-76)."""
     if not os.path.exists(REF_CALLER):
         pytest.skip("oracle/_ref/ref_caller not built (reference sources absent)")
     out = tmp_path / "o.bin"
