@@ -354,3 +354,46 @@ def test_stack_folded_residual_pair(sdq_dev, oracle, monkeypatch, g_kind, s_kind
     got, want = _stack_case(sdq, torch, oracle, sdq_dev, specs, seq, (300, D, 2 * D), 4100, chain=1)
     for j, (g, w) in enumerate(zip(got, want)):
         assert_bitexact(g, w, f"fold {g_kind}+{s_kind} ({fold}): output {j}")
+
+
+def _random_chain(i):
+    """A group with one residual-form item (the target), later items of which
+    those with a residual form add into the target after it (the first of them
+    always, with the target's shape), and an FFN adding into it last or none."""
+    r = np.random.default_rng(7700 + i)
+    K = int(r.choice([256, 512, 1024]))
+    M = int(r.integers(65, 900))
+    N = 4 * int(r.integers(16, 300))
+    res = ["gated", "gated_nofma", "resid"]
+    others = ["none", "gelu"] + res
+    target = (M, K, N, str(r.choice(res)), bool(r.random() < 0.7))
+    group = [(int(r.integers(65, 900)), K, 4 * int(r.integers(16, 300)), "none",
+              bool(r.random() < 0.7)) for _ in range(int(r.integers(0, 4)))]
+    t = int(r.integers(0, len(group) + 1))
+    group.insert(t, target)
+    seq = [(M, int(r.choice([K, 2 * K])), N, str(r.choice(res)), bool(r.random() < 0.7))]
+    for _ in range(int(r.integers(0, 3))):
+        kind = str(r.choice(others))
+        seq.append((M, K, N, kind, bool(r.random() < 0.7)) if kind in res else
+                   (int(r.integers(65, 900)), K, 4 * int(r.integers(16, 300)), kind, True))
+    ffn = (M, N, N * int(r.choice([2, 4]))) if r.random() < 0.6 else None
+    return group, seq, ffn, t
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_stack_random_chained(sdq_dev, oracle, i):
+    """Seeded random stacks whose later residual items (and FFN) add into a
+    grouped item's output, as a block's cross output projection and FFN add
+    into x after its self-attention output: bit for bit against qlinear_group,
+    then qlinear per later item, then ffn. The first later item takes the
+    folded path when it shares the target's K (same k-fragments), the
+    separate one otherwise."""
+    import torch
+
+    import sdq
+
+    group, seq, ffn, t = _random_chain(i)
+    print(f"[stack-chain] {i} group={group} target={t} seq={seq} ffn={ffn}", flush=True)
+    got, want = _stack_case(sdq, torch, oracle, sdq_dev, group, seq, ffn, 5200 + 50 * i, chain=t)
+    for j, (g, w) in enumerate(zip(got, want)):
+        assert_bitexact(g, w, f"chained stack {i}: output {j}")
