@@ -123,3 +123,88 @@ def test_growth_under_capture_is_refused(sdq_dev, oracle):
     del graph
     _replays(sdq_dev, oracle, sdq.qlinear, M, K, N, "none", 300, warm=True)
     w.free()
+
+_BLOCK_NAMES = ("q", "k", "v", "o", "cq", "ck", "cv", "co", "kf", "vf", "fc1", "fc2")
+
+
+def _block_weights(oracle, dim, ffn, seed):
+    lin = {}
+    for i, n in enumerate(_BLOCK_NAMES):
+        out, inp = (ffn, dim) if n == "fc1" else ((dim, ffn) if n == "fc2" else (dim, dim))
+        W = oracle.randn(out * inp, seed + 10 * i).reshape(out, inp) * np.float32(0.02)
+        q, s = oracle.quant_rows(W)
+        lin[n] = (q, s, oracle.randn(out, seed + 10 * i + 1) * np.float32(0.01))
+    return lin
+
+
+def test_pair_pass_captures_and_replays(sdq_dev, oracle):
+    """HIP-graph capture of the twin pair pass (DitBlock.forward_pair over two
+    streams), two fusion layers at small widths: after one eager pass on the
+    capture stream and the second stream (their workspaces then large enough),
+    the pass is captured, joined back by the pair's own stream waits, and
+    replayed three times with new inputs written eagerly between the replays.
+    Every replay's outputs equal an eager pass on the same inputs, bit for bit
+    (the eager pair pass is pinned against the oracle in test_gpu_block.py)."""
+    import torch
+
+    import sdq
+
+    dim, ffn, Mv, Ma, Mc, layers = 512, 1408, 300, 90, 77, 2
+    print(f"[graph-pair] dim={dim} Mv={Mv} Ma={Ma} Mc={Mc} layers={layers}", flush=True)
+    blocks = [sdq.DitBlock(_block_weights(oracle, dim, ffn, 1000 + 100 * b), True)
+              for b in range(2 * layers)]
+    dev = sdq_dev
+
+    def io(M, Mt):
+        r = lambda rows: torch.empty((rows, dim), device=dev)  # noqa: E731
+        return dict(M=M, Mc=Mc, Mt=Mt, h_sa=r(M), att=r(M), xq=r(M), ctx=r(Mc), tn=r(Mt),
+                    xt=r(M), h_ffn=r(M), x=r(M), gate_sa=torch.empty(dim, device=dev),
+                    gate_ffn=torch.empty(dim, device=dev),
+                    qkv=torch.empty((M, 3 * dim), device=dev), cq=r(M),
+                    ckv=torch.empty((Mc, 2 * dim), device=dev),
+                    kvt=torch.empty((Mt, 2 * dim), device=dev),
+                    hid=torch.empty((M, ffn), device=dev))
+
+    iov, ioa = io(Mv, Ma), io(Ma, Mv)
+    tensors = [(k, v) for d in (iov, ioa) for k, v in d.items() if torch.is_tensor(v)]
+
+    def fill(seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        for _, t in tensors:
+            t.copy_(torch.randn(t.shape, generator=g, device=dev))
+
+    s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def passes():
+        for i in range(layers):
+            blocks[2 * i].forward_pair(blocks[2 * i + 1], iov, ioa, stream2=s2)
+
+    fill(1)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        passes()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        passes()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        fill(10 + rep)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = {f"{which}.{k}": v.cpu().numpy() for which, d in (("v", iov), ("a", ioa))
+               for k, v in d.items() if torch.is_tensor(v)}
+        fill(10 + rep)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            passes()
+        torch.cuda.synchronize()
+        for name, a in got.items():
+            which, k = name.split(".")
+            b = (iov if which == "v" else ioa)[k].cpu().numpy()
+            assert_bitexact(a, b, f"replay {rep}: {name}")
+    del graph
+    for b in blocks:
+        b.free()
